@@ -1,0 +1,250 @@
+"""Benchmark of the fused W8A8 linear on one MI355X.
+
+Workload (the configuration the metric is quoted
+on): per-channel W8A8 linear, M=4096, N=10240, K=2560.  One step is one pass
+of the hot path over that batch, i.e. exactly the two kernels
+cider_perchannel_linear launches (per-token quantize, then int8 GEMM with the
+fused per-channel epilogue); they are enqueued through the C ABI as
+cider_quantize_per_token + cider_perchannel_gemm so that HIP events can
+bracket the GEMM kernel alone for the roofline figure.  Inputs are resident in
+HBM before timing starts.
+
+Also reported, in the same run:
+  * decode: the M == 1 MV (N=10240, K=2560), cycling over enough weight copies
+    (>= 2x the 256 MB Infinity Cache) that every launch streams from HBM;
+  * cpu_baseline: the C restatement of the reference math (oracle/) on rows
+    0..127 of the same inputs (= configs[0], M=128), all host threads, and a
+    bit-exact comparison of those rows with the GPU output.
+
+Prints ONE JSON line.
+"""
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POPS
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+MALL_BYTES = 256 << 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--M", type=int, default=4096)
+    ap.add_argument("--N", type=int, default=10240)
+    ap.add_argument("--K", type=int, default=2560)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--no-decode", action="store_true", help="skip the M=1 decode leg")
+    ap.add_argument("--seed", type=int, default=20261201)
+    return ap.parse_args()
+
+
+def synth_inputs(torch, M, N, K, seed, dev):
+    """X fp16 ~ N(0,1) with K//100 outlier columns x20; W int8 U[-127,127];
+    scale_w fp32 U[1e-3,1e-2]; bias zeros (the reference default)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn(M, K, generator=g, dtype=torch.float32)
+    cols = torch.randperm(K, generator=g)[: K // 100]
+    x[:, cols] *= 20.0
+    x = x.to(torch.float16)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    sw = torch.rand(N, generator=g, dtype=torch.float32) * 9e-3 + 1e-3
+    bias = torch.zeros(N, dtype=torch.float16)
+    return [t.to(dev) for t in (x, w, sw, bias)]
+
+
+def vp(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards by output columns with no collective; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from cider_amd import _lib
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    lib = _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, N, K = args.M, args.N, args.K
+    x, w, sw, bias = synth_inputs(torch, M, N, K, args.seed, dev)
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    sa = torch.empty((M,), dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        _lib.check(lib.cider_quantize_per_token(vp(x), vp(q), vp(sa), M, K, sp))
+        if ev is not None:
+            ev[1].record(stream)
+        _lib.check(lib.cider_perchannel_gemm(vp(q), vp(sa), vp(w), vp(sw), vp(bias), vp(y),
+                                             M, N, K, sp))
+        if ev is not None:
+            ev[2].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    wall_ms = (t1 - t0) * 1e3 / args.steps
+    gemm_ms = [e[1].elapsed_time(e[2]) for e in events]
+    quant_ms = [e[0].elapsed_time(e[1]) for e in events]
+    gemm_avg = sum(gemm_ms) / len(gemm_ms)
+    quant_avg = sum(quant_ms) / len(quant_ms)
+    ops = 2.0 * M * N * K
+    value_tops = ops / (wall_ms * 1e-3) / 1e12
+    gemm_tops = ops / (gemm_avg * 1e-3) / 1e12
+
+    result = {
+        "metric": "W8A8 GEMM TOPS (% INT8 peak) at M=4096; GB/s (% HBM peak) at M=1",
+        "value": round(value_tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "configs[1]: W8A8 per-channel linear (quantize + int8 GEMM + "
+                               "fused dequant), X fp16 N(0,1) with 1% outlier columns x20",
+                   "M": M, "N": N, "K": K, "seed": args.seed, "parallelism": "none (1 GPU)"},
+        "kernels": {"quantize_ms": round(quant_avg, 4), "gemm_ms": round(gemm_avg, 4),
+                    "gemm_tops": round(gemm_tops, 2),
+                    "frac_of_int8_peak_whole_step": round(value_tops / INT8_PEAK_TOPS, 4)},
+        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,I8,PC>",
+                     "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TOPS", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
+                     "traffic": load_traffic()},
+    }
+
+    if not args.no_decode:
+        result["decode"] = bench_decode(torch, lib, _lib, N, K, args, dev, stream)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(x, w, sw, bias, y, N, K)
+    print(json.dumps(result), flush=True)
+
+
+def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
+    """M == 1 fp16-activation MV, weights rotated across >= 2x MALL."""
+    wbytes = N * K
+    copies = max(2, -(-2 * MALL_BYTES // wbytes) + 1)
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 1)
+    ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+          for _ in range(copies)]
+    sw = (torch.rand(N, generator=g) * 9e-3 + 1e-3).to(dev)
+    bias = torch.zeros(N, dtype=torch.float16, device=dev)
+    x = torch.randn(1, K, generator=g).to(torch.float16).to(dev)
+    y = torch.empty((1, N), dtype=torch.float16, device=dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    iters = max(args.steps, copies * 4)
+
+    def call(i):
+        _lib.check(lib.cider_perchannel_linear(vp(x), vp(ws[i % copies]), vp(sw), vp(bias), vp(y),
+                                               None, 0, 1, N, K, sp))
+
+    for i in range(max(args.warmup, copies)):
+        call(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for i in range(iters):
+        evs[i][0].record(stream)
+        call(i)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    times = [a.elapsed_time(b) for a, b in evs]
+    avg = sum(times) / len(times)
+    nbytes = N * K + 2 * K + 4 * N + 2 * N + 2 * N  # W, x, scale_w, bias, y
+    gbs = nbytes / (avg * 1e-3) / 1e9
+    return {"workload": "M=1 per-channel MV (configs[1] decode)", "N": N, "K": K,
+            "weight_copies": copies, "us_per_call_avg": round(avg * 1e3, 3),
+            "us_per_call_median": round(statistics.median(times) * 1e3, 3),
+            "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
+            "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "bound": "hbm", "kernel": "mv_kernel<per-channel>"}
+
+
+def cpu_baseline(x, w, sw, bias, y, N, K):
+    """The oracle's C restatement (reference math, reference order) on rows
+    0..127 of the workload, timed on this host; also checks those rows."""
+    import numpy as np
+
+    from oracle import c_oracle
+
+    rows = 128
+    xs = x[:rows].cpu().numpy()
+    wn = w.cpu().numpy()
+    swn = sw.cpu().numpy()
+    bn = bias.cpu().numpy()
+    threads = c_oracle.num_threads()
+    times = []
+    out = None
+    deadline = time.perf_counter() + 30.0
+    for _ in range(5):
+        t0 = time.perf_counter()
+        out = c_oracle.perchannel_linear_gemm(xs, wn, swn, bn)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > deadline:
+            break
+    med = statistics.median(times)
+    gpu_rows = y[:rows].cpu().numpy()
+    exact = bool(np.array_equal(gpu_rows.view(np.uint16), out.view(np.uint16)))
+    return {"value": round(2.0 * rows * N * K / med / 1e12, 4), "unit": "TOPS",
+            "cores": threads, "kind": "port",
+            "sample": f"rows 0..{rows - 1} of the M=4096 workload (configs[0] shape "
+                      f"M={rows},N={N},K={K}); C oracle, quantize+int32 GEMM+dequant; "
+                      f"median of {len(times)} runs",
+            "ms": round(med * 1e3, 2), "cpu": cpu_model(),
+            "gpu_rows_bit_exact": exact}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(ROOT, "profiles", "gemm_pc_m4096_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,285 @@
+// extern "C" entry points of libcider_hip.so (declared in include/cider_hip.h).
+//
+// This layer is the counterpart of the reference's op constructors and
+// primitive eval_gpu methods (csrc/src/w8a8_primitive.mm:137-342,
+// csrc/src/pergroup_primitive.mm:138-312, csrc/src/w4a8_primitive.mm:175-283):
+// it validates shapes and group sizes (std::invalid_argument there,
+// CIDER_E_INVALID here), carves the quantized-activation scratch out of the
+// caller's workspace, and applies the reference's dispatch policy:
+//   W8 per-channel / per-group: M == 1 -> fp16 MV, otherwise quantize -> GEMM
+//   W4A8: always quantize -> GEMM (M == 1 included)
+// The GEMM launcher picks the tile shape from M (skinny for M <= 64); the
+// choice never changes results on the integer path.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "cider_hip.h"
+#include "kernels.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return CIDER_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(CIDER_E_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+  return ok();
+}
+
+constexpr int64_t kMaxDim = (int64_t)1 << 30;
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t quant_ws_bytes(int64_t M, int64_t K) {
+  return align256((size_t)M * (size_t)K) + align256((size_t)M * sizeof(float));
+}
+
+int check_dims(const char* fn, int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(CIDER_E_INVALID, "%s: negative dimension (M=%lld N=%lld K=%lld)", fn,
+                (long long)M, (long long)N, (long long)K);
+  if (M > kMaxDim || N > kMaxDim || K > kMaxDim)
+    return fail(CIDER_E_INVALID, "%s: dimension above 2^30 (M=%lld N=%lld K=%lld)", fn,
+                (long long)M, (long long)N, (long long)K);
+  return CIDER_OK;
+}
+
+int need(const char* fn, const void* p, const char* name, bool required) {
+  if (required && p == nullptr)
+    return fail(CIDER_E_INVALID, "%s: %s is NULL", fn, name);
+  return CIDER_OK;
+}
+
+#define CIDER_TRY(expr)           \
+  do {                            \
+    const int _rc = (expr);       \
+    if (_rc != CIDER_OK) return _rc; \
+  } while (0)
+
+int check_ws(const char* fn, const void* ws, size_t ws_bytes, size_t needed) {
+  if (needed == 0) return CIDER_OK;
+  if (ws == nullptr)
+    return fail(CIDER_E_INVALID, "%s: workspace is NULL (%zu bytes needed)", fn, needed);
+  if (ws_bytes < needed)
+    return fail(CIDER_E_INVALID, "%s: workspace of %zu bytes, %zu needed", fn, ws_bytes, needed);
+  if (((uintptr_t)ws & 255) != 0)
+    return fail(CIDER_E_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  return CIDER_OK;
+}
+
+// Quantizes x into the workspace; returns q and sa pointers.
+int quantize_into_ws(const char* fn, const void* x, void* ws, int64_t M, int64_t K,
+                     hipStream_t s, int8_t** q, float** sa) {
+  *q = reinterpret_cast<int8_t*>(ws);
+  *sa = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + align256((size_t)M * (size_t)K));
+  return hip_status(cider::launch_quantize(reinterpret_cast<const uint16_t*>(x), *q, *sa,
+                                           (int)M, (int)K, s),
+                    fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int cider_version(void) { return 100; }  // 0.1.0
+
+const char* cider_last_error(void) { return g_last_error.c_str(); }
+
+size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K, int group_size) {
+  (void)N;
+  (void)group_size;
+  if (M <= 0 || K < 0) return 0;
+  switch (op) {
+    case CIDER_OP_PERCHANNEL:
+    case CIDER_OP_PERGROUP:
+      return M <= 1 ? 0 : quant_ws_bytes(M, K);
+    case CIDER_OP_W4A8:
+    case CIDER_OP_W4A8_PERGROUP:
+      return quant_ws_bytes(M, K);
+    default:
+      return 0;
+  }
+}
+
+int cider_quantize_per_token(const void* x_f16, int8_t* q, float* sa, int64_t M, int64_t K,
+                             void* stream) {
+  static const char* fn = "cider_quantize_per_token";
+  CIDER_TRY(check_dims(fn, M, 1, K));
+  if (M == 0) return ok();
+  const bool elems = K > 0;
+  CIDER_TRY(need(fn, x_f16, "x", elems));
+  CIDER_TRY(need(fn, q, "q", elems));
+  CIDER_TRY(need(fn, sa, "sa", true));
+  return hip_status(cider::launch_quantize(reinterpret_cast<const uint16_t*>(x_f16), q, sa,
+                                           (int)M, (int)K, (hipStream_t)stream),
+                    fn);
+}
+
+int cider_int8_matmul_int32(const int8_t* a, const int8_t* b_nk, int32_t* c, int64_t M,
+                            int64_t N, int64_t K, void* stream) {
+  static const char* fn = "cider_int8_matmul_int32";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, a, "a", K > 0));
+  CIDER_TRY(need(fn, b_nk, "b", K > 0));
+  CIDER_TRY(need(fn, c, "c", true));
+  cider::GemmArgs g{a, b_nk, nullptr, nullptr, nullptr, c, (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_I32, false, 0,
+                                       (hipStream_t)stream),
+                    fn);
+}
+
+int cider_perchannel_gemm(const int8_t* q, const float* sa, const int8_t* w_nk, const float* sw,
+                          const void* bias_f16, void* y_f16, int64_t M, int64_t N, int64_t K,
+                          void* stream) {
+  static const char* fn = "cider_perchannel_gemm";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, q, "q", K > 0));
+  CIDER_TRY(need(fn, sa, "sa", true));
+  CIDER_TRY(need(fn, w_nk, "w", K > 0));
+  CIDER_TRY(need(fn, sw, "scale_w", true));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  cider::GemmArgs g{q, w_nk, sa, sw, reinterpret_cast<const uint16_t*>(bias_f16), y_f16,
+                    (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PC, false, 0,
+                                       (hipStream_t)stream),
+                    fn);
+}
+
+int cider_perchannel_linear(const void* x_f16, const int8_t* w_nk, const float* sw,
+                            const void* bias_f16, void* y_f16, void* ws, size_t ws_bytes,
+                            int64_t M, int64_t N, int64_t K, void* stream) {
+  static const char* fn = "cider_perchannel_linear";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", K > 0));
+  CIDER_TRY(need(fn, w_nk, "w", K > 0));
+  CIDER_TRY(need(fn, sw, "scale_w", true));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  const hipStream_t s = (hipStream_t)stream;
+  const uint16_t* bias = reinterpret_cast<const uint16_t*>(bias_f16);
+  if (M == 1)
+    return hip_status(cider::launch_mv(reinterpret_cast<const uint16_t*>(x_f16), w_nk, sw, bias,
+                                       reinterpret_cast<uint16_t*>(y_f16), (int)N, (int)K, 0, s),
+                      fn);
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int8_t* q;
+  float* sa;
+  CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
+  cider::GemmArgs g{q, w_nk, sa, sw, bias, y_f16, (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PC, false, 0, s), fn);
+}
+
+int cider_pergroup_linear(const void* x_f16, const int8_t* w_nk, const float* sw_gn,
+                          const void* bias_f16, void* y_f16, void* ws, size_t ws_bytes,
+                          int64_t M, int64_t N, int64_t K, int group_size, void* stream) {
+  static const char* fn = "cider_pergroup_linear";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (group_size != 64 && group_size != 128 && group_size != 256)
+    return fail(CIDER_E_INVALID, "%s: group_size must be 64, 128, or 256 (got %d)", fn,
+                group_size);
+  if (K % group_size != 0)
+    return fail(CIDER_E_INVALID, "%s: K=%lld is not a multiple of group_size=%d", fn,
+                (long long)K, group_size);
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", K > 0));
+  CIDER_TRY(need(fn, w_nk, "w", K > 0));
+  CIDER_TRY(need(fn, sw_gn, "scale_w", K > 0));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  const hipStream_t s = (hipStream_t)stream;
+  const uint16_t* bias = reinterpret_cast<const uint16_t*>(bias_f16);
+  if (M == 1)
+    return hip_status(cider::launch_mv(reinterpret_cast<const uint16_t*>(x_f16), w_nk, sw_gn,
+                                       bias, reinterpret_cast<uint16_t*>(y_f16), (int)N, (int)K,
+                                       group_size, s),
+                      fn);
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int8_t* q;
+  float* sa;
+  CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
+  cider::GemmArgs g{q, w_nk, sa, sw_gn, bias, y_f16, (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PG, false, group_size, s), fn);
+}
+
+int cider_w4_repack_ref(const uint8_t* src_kn, uint8_t* dst_nk, int64_t N, int64_t K,
+                        void* stream) {
+  static const char* fn = "cider_w4_repack_ref";
+  CIDER_TRY(check_dims(fn, 1, N, K));
+  if (K % 2 != 0)
+    return fail(CIDER_E_INVALID, "%s: K=%lld must be even", fn, (long long)K);
+  if (N == 0 || K == 0) return ok();
+  CIDER_TRY(need(fn, src_kn, "src", true));
+  CIDER_TRY(need(fn, dst_nk, "dst", true));
+  return hip_status(cider::launch_w4_repack_ref(src_kn, dst_nk, (int)N, (int)K,
+                                                (hipStream_t)stream),
+                    fn);
+}
+
+int cider_w4a8_linear(const void* x_f16, const uint8_t* w4_nk, const float* sw, void* y_f16,
+                      void* ws, size_t ws_bytes, int64_t M, int64_t N, int64_t K,
+                      void* stream) {
+  static const char* fn = "cider_w4a8_linear";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (K % 2 != 0)
+    return fail(CIDER_E_INVALID, "%s: K=%lld must be even", fn, (long long)K);
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", K > 0));
+  CIDER_TRY(need(fn, w4_nk, "packed_w", K > 0));
+  CIDER_TRY(need(fn, sw, "scale_w", true));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  const hipStream_t s = (hipStream_t)stream;
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int8_t* q;
+  float* sa;
+  CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
+  cider::GemmArgs g{q, w4_nk, sa, sw, nullptr, y_f16, (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I4, cider::EPI_PC, false, 0, s), fn);
+}
+
+int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
+                               const void* scale_gn_f16, const void* bias_f16, void* y_f16,
+                               void* ws, size_t ws_bytes, int64_t M, int64_t N, int64_t K,
+                               int group_size, void* stream) {
+  static const char* fn = "cider_w4a8_pergroup_linear";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (group_size != 64 && group_size != 128)
+    return fail(CIDER_E_INVALID, "%s: group_size must be 64 or 128 (got %d)", fn, group_size);
+  if (K % group_size != 0)
+    return fail(CIDER_E_INVALID, "%s: K=%lld is not a multiple of group_size=%d", fn,
+                (long long)K, group_size);
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", K > 0));
+  CIDER_TRY(need(fn, w4_nk, "packed_w", K > 0));
+  CIDER_TRY(need(fn, scale_gn_f16, "scales", K > 0));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  const hipStream_t s = (hipStream_t)stream;
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int8_t* q;
+  float* sa;
+  CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
+  cider::GemmArgs g{q, w4_nk, sa, scale_gn_f16, reinterpret_cast<const uint16_t*>(bias_f16),
+                    y_f16, (int)M, (int)N, (int)K};
+  return hip_status(cider::launch_gemm(g, cider::W_I4, cider::EPI_PG, true, group_size, s), fn);
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+// Device helpers shared by the gfx950 kernels of libcider_hip.so.
+//
+// Numerics contract of every kernel in this library:
+//   * binary32 arithmetic rounds each operation (built with -ffp-contract=off,
+//     no fast-math), so  a*b*c+d  is evaluated as ((a*b)*c)+d, four roundings;
+//   * float division is IEEE correctly rounded (HIP's default);
+//   * fp32 -> fp16 is round-to-nearest-even (v_cvt_f16_f32 in RNE mode);
+//   * integer dot products are exact int32 (i8 MFMA / integer adds).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cider {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// 16x16x64 int8 MFMA: C[i][j] += sum_k A[i][k] * B[k][j].
+// Operand layout (64 lanes, 16 bytes each): lane l holds row i = l % 16 of A
+// (column j = l % 16 of B) and one 16-byte slice of K selected by l / 16; the
+// slice-to-K mapping is the same for A and B, so any consistent assignment of
+// K elements to (l / 16, byte) pairs yields the exact dot product.
+// Result layout: lane l, element r holds C[4 * (l / 16) + r][l % 16].
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Sign-extends the four two's-complement nibbles held in the low half of each
+// byte of t (t & 0xF0F0F0F0 == 0) to four int8 bytes, without carries between
+// bytes:  (n ^ 0x88) - 8  lies in [120, 135] for every nibble n, and xor 0x80
+// maps it to n - 16*(n >= 8) modulo 256.
+__device__ __forceinline__ uint32_t sext_nibbles(uint32_t t) {
+  return ((t ^ 0x88888888u) - 0x08080808u) ^ 0x80808080u;
+}
+
+// Unpacks one 32-bit word of packed int4 (byte j holds element 2j in its low
+// nibble and 2j+1 in its high nibble) into 8 int8 values in element order:
+// e0123 = elements 0..3, e4567 = elements 4..7.
+__device__ __forceinline__ void unpack_w4_word(uint32_t w, uint32_t& e0123,
+                                               uint32_t& e4567) {
+  const uint32_t ev = sext_nibbles(w & 0x0F0F0F0Fu);         // elems 0,2,4,6
+  const uint32_t od = sext_nibbles((w >> 4) & 0x0F0F0F0Fu);  // elems 1,3,5,7
+  // v_perm_b32(S0=od, S1=ev): selector bytes 0-3 pick ev, 4-7 pick od.
+  e0123 = __builtin_amdgcn_perm(od, ev, 0x05010400u);
+  e4567 = __builtin_amdgcn_perm(od, ev, 0x07030602u);
+}
+
+// Loads `n` (< 16) bytes with byte loads, zero-filling the rest.
+__device__ __forceinline__ i32x4 load_bytes_partial(const int8_t* p, int n) {
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+  for (int i = 0; i < n; ++i)
+    w[i >> 2] |= (uint32_t)(uint8_t)p[i] << (8 * (i & 3));
+  return i32x4{(int32_t)w[0], (int32_t)w[1], (int32_t)w[2], (int32_t)w[3]};
+}
+
+__device__ __forceinline__ i32x4 ld16(const void* p) {
+  return *reinterpret_cast<const i32x4*>(p);
+}
+
+__device__ __forceinline__ i32x2 ld8(const void* p) {
+  return *reinterpret_cast<const i32x2*>(p);
+}
+
+// Maps a linear workgroup id to a tile index so that the workgroups one XCD
+// runs (the hardware deals workgroups to the 8 XCDs round-robin) receive a
+// contiguous range of tiles; neighbouring tiles share operand panels, which
+// then hit in that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int wg, int nwg) {
+  constexpr int kXcd = 8;
+  const int per = nwg / kXcd;          // full rounds
+  const int full = per * kXcd;
+  if (wg >= full) return wg;           // ragged tail keeps its id
+  return (wg % kXcd) * per + wg / kXcd;
+}
+
+}  // namespace cider

@@ -1,0 +1,228 @@
+// M == 1 decode MV: fp16 activation x int8 weight, no activation quantization.
+//
+// Reference semantics (cider/kernels/w8a8_int8_mv.metal:26-70 per-channel,
+// cider/kernels/pergroup_int8_mv.metal:35-105 per-group): for each output row
+// n, 32 lanes each own elements 256b + 8l + i (i < 8) of every 256-wide block
+// b; lane l forms  d = sum_i f32(w) * f32(x)  left to right (the products are
+// exact), accumulates  r_l += d  (per-channel) or  r_l += f32(sw[g,n] * d)
+// with g = (256b + 8l) / gs  (per-group) over the blocks in order, the 32
+// lanes are summed by an xor butterfly (16, 8, 4, 2, 1), and
+//   per-channel: y = h(f32(sw[n] * R) + f32(bias[n]))
+//   per-group:   y = h(f32(R + f32(bias[n])))
+// This kernel reproduces exactly that order, for every shape.
+//
+// MI355X design
+//   * 16 lanes per row, four rows per 64-lane wave.  Lane j carries the two
+//     reference lanes 2j and 2j+1, so each block costs it one 16-byte weight
+//     load (the 16 consecutive bytes 256b + 16j ..) instead of two 8-byte
+//     ones.  The butterfly over reference lanes 16, 8, 4, 2 is a shuffle over
+//     physical lanes 8, 4, 2, 1; offset 1 is the in-register sum of the pair.
+//   * x is staged once per workgroup in LDS (zero-padded to whole blocks);
+//     the weight stream is the only HBM traffic, with U blocks (U * 16 bytes
+//     per lane) in flight.  Per-group scales of the workgroup's rows are
+//     staged in LDS as well.
+//   * Rows per workgroup (4, 8 or 16) are chosen so the grid has enough
+//     waves to cover HBM latency on short-N shapes.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cider {
+
+namespace {
+
+constexpr int kLanesPerRow = 16;
+
+// d = sum_{i<8} f32(w_i) * f32(x_i), left to right, from 8 weight bytes
+// (two dwords) and 8 fp16 values (four dwords).
+__device__ __forceinline__ float dot8(uint32_t w0, uint32_t w1, uint32_t x0, uint32_t x1,
+                                      uint32_t x2, uint32_t x3) {
+  const uint32_t wv[2] = {w0, w1};
+  const uint32_t xv[4] = {x0, x1, x2, x3};
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int8_t wi = (int8_t)(wv[i >> 2] >> (8 * (i & 3)));
+    const float xf = h2f((uint16_t)((i & 1) ? (xv[i >> 1] >> 16) : (xv[i >> 1] & 0xffffu)));
+    const float prod = (float)wi * xf;  // exact: 8-bit x 11-bit significands
+    d = (i == 0) ? prod : d + prod;
+  }
+  return d;
+}
+
+}  // namespace
+
+// PG: per-group scales; VEC: K % 256 == 0 and 16-byte aligned w (full blocks,
+// vector loads); otherwise the weight tail is loaded bytewise with bounds.
+// XLDS: x staged in LDS (K <= kMaxLdsK); otherwise read from global.
+template <bool PG, bool VEC, bool XLDS, int U>
+__global__ __launch_bounds__(256) void mv_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const float* __restrict__ sw, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int N, int K, int gs, int rows_per_wg) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  const int nb = (K + 255) / 256;
+  const int kp = nb * 256;  // padded K
+  uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
+  const int G = PG ? K / gs : 0;
+  float* sws = reinterpret_cast<float*>(dyn + (XLDS ? (size_t)kp * 2 : 0));
+
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = lane >> 4, j = lane & 15;
+  const int row_in_wg = wave * 4 + rg;
+  const int n0 = blockIdx.x * rows_per_wg;
+  const int n = n0 + row_in_wg;
+  const bool live = n < N;
+  const int8_t* wr = w + (int64_t)(live ? n : 0) * K;
+
+  // ---- stage x (and the per-group scales of this workgroup's rows)
+  if constexpr (XLDS) {
+    for (int e = tid; e < kp / 8; e += nthr) {
+      const int k = 8 * e;
+      i32x4 v;
+      if (VEC || k + 8 <= K) {
+        if (VEC || (((uintptr_t)(x + k) & 15) == 0)) {
+          v = ld16(x + k);
+        } else {
+          uint32_t t[4] = {0u, 0u, 0u, 0u};
+          for (int i = 0; i < 8; ++i) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
+          v = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+        }
+      } else {
+        uint32_t t[4] = {0u, 0u, 0u, 0u};
+        for (int i = 0; i < 8; ++i)
+          if (k + i < K) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
+        v = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+      }
+      *reinterpret_cast<i32x4*>(xs + k) = v;
+    }
+  }
+  if constexpr (PG) {
+    for (int e = tid; e < G * rows_per_wg; e += nthr) {
+      const int g = e / rows_per_wg, r = e % rows_per_wg;
+      sws[e] = (n0 + r < N) ? sw[(int64_t)g * N + n0 + r] : 0.0f;
+    }
+  }
+  if (XLDS || PG) __syncthreads();
+
+  float r0 = 0.0f, r1 = 0.0f;  // chains of reference lanes 2j and 2j+1
+  for (int b = 0; b < nb; b += U) {
+    i32x4 wv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (b + u) * 256 + 16 * j;
+      if (live && b + u < nb) {
+        if (VEC) {
+          wv[u] = ld16(wr + k);
+        } else {
+          uint32_t t[4] = {0u, 0u, 0u, 0u};
+          for (int i = 0; i < 16; ++i)
+            if (k + i < K) t[i >> 2] |= (uint32_t)(uint8_t)wr[k + i] << (8 * (i & 3));
+          wv[u] = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+        }
+      } else {
+        wv[u] = i32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (b + u >= nb) break;
+      const int k = (b + u) * 256 + 16 * j;
+      i32x4 xa, xb;
+      if constexpr (XLDS) {
+        xa = *reinterpret_cast<const i32x4*>(xs + k);
+        xb = *reinterpret_cast<const i32x4*>(xs + k + 8);
+      } else {
+        uint32_t t[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        for (int i = 0; i < 16; ++i)
+          if (k + i < K) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
+        xa = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+        xb = i32x4{(int)t[4], (int)t[5], (int)t[6], (int)t[7]};
+      }
+      const float d0 = dot8((uint32_t)wv[u][0], (uint32_t)wv[u][1], (uint32_t)xa[0],
+                            (uint32_t)xa[1], (uint32_t)xa[2], (uint32_t)xa[3]);
+      const float d1 = dot8((uint32_t)wv[u][2], (uint32_t)wv[u][3], (uint32_t)xb[0],
+                            (uint32_t)xb[1], (uint32_t)xb[2], (uint32_t)xb[3]);
+      if constexpr (PG) {
+        // reference lanes past K (d == 0) use the last group's scale, as the
+        // padded blocks of the reference would; never an index past G
+        const int g0 = min(k / gs, G - 1), g1 = min((k + 8) / gs, G - 1);
+        const float t0 = sws[g0 * rows_per_wg + row_in_wg] * d0;
+        const float t1 = sws[g1 * rows_per_wg + row_in_wg] * d1;
+        r0 = r0 + t0;
+        r1 = r1 + t1;
+      } else {
+        r0 = r0 + d0;
+        r1 = r1 + d1;
+      }
+    }
+  }
+  // butterfly over reference lanes: offsets 16, 8, 4, 2 are physical 8, 4, 2, 1
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) {
+    r0 = r0 + __shfl_xor(r0, off, kLanesPerRow);
+    r1 = r1 + __shfl_xor(r1, off, kLanesPerRow);
+  }
+  const float R = r0 + r1;  // offset 1
+  if (j == 0 && live) {
+    float v;
+    if constexpr (PG) {
+      v = bias ? R + h2f(bias[n]) : R;
+    } else {
+      v = sw[n] * R;
+      if (bias) v = v + h2f(bias[n]);
+    }
+    y[n] = f2h(v);
+  }
+}
+
+namespace {
+
+constexpr int kMaxLdsK = 32768;  // x staged in LDS up to 64 KB
+
+template <bool PG, bool XLDS, int U>
+hipError_t run_mv(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
+                  uint16_t* y, int N, int K, int gs, bool vec, int rows, size_t lds,
+                  hipStream_t s) {
+  const dim3 grid((N + rows - 1) / rows), block(rows * kLanesPerRow);
+  if (vec)
+    mv_kernel<PG, true, XLDS, U><<<grid, block, lds, s>>>(x, w, sw, bias, y, N, K, gs, rows);
+  else
+    mv_kernel<PG, false, XLDS, U><<<grid, block, lds, s>>>(x, w, sw, bias, y, N, K, gs, rows);
+  return hipGetLastError();
+}
+
+template <bool PG, bool XLDS>
+hipError_t pick_u(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
+                  uint16_t* y, int N, int K, int gs, bool vec, int rows, size_t lds,
+                  hipStream_t s) {
+  const int nb = (K + 255) / 256;
+  if (nb <= 8) return run_mv<PG, XLDS, 8>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  return run_mv<PG, XLDS, 16>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+}
+
+}  // namespace
+
+hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
+                     const uint16_t* bias, uint16_t* y, int N, int K, int gs,
+                     hipStream_t s) {
+  // Rows per workgroup: 16 (4 waves) when N is large, down to 4 (one wave)
+  // so that short-N shapes still launch >= 512 workgroups.
+  int rows = 16;
+  while (rows > 4 && (N + rows - 1) / rows < 512) rows >>= 1;
+  const int nb = (K + 255) / 256;
+  const bool xlds = K <= kMaxLdsK;
+  const int G = gs > 0 ? K / gs : 0;
+  const size_t lds = (xlds ? (size_t)nb * 256 * 2 : 0) + (size_t)G * rows * sizeof(float);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const bool vec = (K % 256 == 0) && (((uintptr_t)w & 15) == 0) && (((uintptr_t)x & 15) == 0);
+  if (gs > 0) {
+    if (xlds) return pick_u<true, true>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+    return pick_u<true, false>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  }
+  if (xlds) return pick_u<false, true>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  return pick_u<false, false>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+}
+
+}  // namespace cider

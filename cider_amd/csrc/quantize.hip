@@ -1,0 +1,148 @@
+// Per-token activation quantization (fp16 [M,K] -> int8 [M,K] + fp32 [M]).
+//
+// Semantics of cider/kernels/w8a8_quantize.metal:33-86:
+//   amax = max_k |x[m,k]|        (fmax: NaN never wins)
+//   s    = amax / 127, s == 0 -> 1
+//   inv  = 1 / s
+//   q    = clamp(round_half_away(x * inv), -128, 127)   (NaN -> -128)
+//
+// MI355X design: one 64-lane wavefront owns one row, so the absmax is a pure
+// cross-lane reduction (no LDS, no barrier); a workgroup of 4 waves handles 4
+// rows.  Rows of up to 64*8*32 = 16384 elements stay in registers between the
+// absmax and the quantize pass (each element is read from HBM once); longer
+// rows are re-read, which hits in L2.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cider {
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ float row_scale(float amax) {
+  float s = amax / 127.0f;
+  return s == 0.0f ? 1.0f : s;
+}
+
+__device__ __forceinline__ int8_t quant1(float xv, float inv) {
+  float r = __builtin_roundf(xv * inv);  // half away from zero
+  r = fminf(fmaxf(r, -128.0f), 127.0f);  // fmax(NaN, -128) = -128
+  return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ float absmax8(i32x4 v, float m) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = (uint32_t)v[j];
+    m = fmaxf(m, fabsf(h2f((uint16_t)(w & 0xffffu))));
+    m = fmaxf(m, fabsf(h2f((uint16_t)(w >> 16))));
+  }
+  return m;
+}
+
+__device__ __forceinline__ i32x2 quant8(i32x4 v, float inv) {
+  uint32_t out[2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = (uint32_t)v[j];
+    const uint32_t a = (uint8_t)quant1(h2f((uint16_t)(w & 0xffffu)), inv);
+    const uint32_t b = (uint8_t)quant1(h2f((uint16_t)(w >> 16)), inv);
+    const uint32_t pair = a | (b << 8);
+    if (j & 1)
+      out[j >> 1] |= pair << 16;
+    else
+      out[j >> 1] = pair;
+  }
+  return i32x2{(int32_t)out[0], (int32_t)out[1]};
+}
+
+// Vectorized rows: K % 8 == 0, x 16-byte and q 8-byte aligned.  NV > 0 keeps
+// NV 16-byte vectors per lane in registers; NV == 0 streams the row twice.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_vec_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+    float* __restrict__ sa, int M, int K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // uniform per wave
+  const uint16_t* xr = x + row * K;
+  int8_t* qr = q + row * K;
+  const int nvec = K >> 3;
+  float amax = 0.0f;
+  if constexpr (NV > 0) {
+    i32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + i * kWave;
+      v[i] = e < nvec ? ld16(xr + 8 * e) : i32x4{0, 0, 0, 0};
+      amax = absmax8(v[i], amax);
+    }
+    amax = wave_max(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) sa[row] = s;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + i * kWave;
+      if (e < nvec) *reinterpret_cast<i32x2*>(qr + 8 * e) = quant8(v[i], inv);
+    }
+  } else {
+    for (int e = lane; e < nvec; e += kWave) amax = absmax8(ld16(xr + 8 * e), amax);
+    amax = wave_max(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) sa[row] = s;
+    for (int e = lane; e < nvec; e += kWave)
+      *reinterpret_cast<i32x2*>(qr + 8 * e) = quant8(ld16(xr + 8 * e), inv);
+  }
+}
+
+// Any K and alignment: element-wise, two passes.
+__global__ __launch_bounds__(256) void quantize_scalar_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+    float* __restrict__ sa, int M, int K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const uint16_t* xr = x + row * K;
+  int8_t* qr = q + row * K;
+  float amax = 0.0f;
+  for (int k = lane; k < K; k += kWave) amax = fmaxf(amax, fabsf(h2f(xr[k])));
+  amax = wave_max(amax);
+  const float s = row_scale(amax);
+  const float inv = 1.0f / s;
+  if (lane == 0) sa[row] = s;
+  for (int k = lane; k < K; k += kWave) qr[k] = quant1(h2f(xr[k]), inv);
+}
+
+hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
+                           int K, hipStream_t s) {
+  const dim3 grid((M + 3) / 4), block(256);
+  const bool vec = (K % 8 == 0) && (((uintptr_t)x & 15) == 0) &&
+                   (((uintptr_t)q & 7) == 0);
+  if (!vec) {
+    quantize_scalar_kernel<<<grid, block, 0, s>>>(x, q, sa, M, K);
+    return hipGetLastError();
+  }
+  const int per_lane = ((K >> 3) + kWave - 1) / kWave;
+  if (per_lane <= 1)
+    quantize_vec_kernel<1><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 2)
+    quantize_vec_kernel<2><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 4)
+    quantize_vec_kernel<4><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 8)
+    quantize_vec_kernel<8><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 16)
+    quantize_vec_kernel<16><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 32)
+    quantize_vec_kernel<32><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else
+    quantize_vec_kernel<0><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  return hipGetLastError();
+}
+
+}  // namespace cider

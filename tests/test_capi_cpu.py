@@ -1,0 +1,154 @@
+"""CPU tier: the C-ABI library loads, exports every symbol that
+include/cider_hip.h declares, and validates arguments without touching a GPU;
+the host-side weight quantizers match the oracle; CPU tensors are rejected.
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import cider_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cider_hip.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(cider_[a-z0-9_]+)\(",
+                                 text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from cider_amd import _lib
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    syms = header_symbols()
+    assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
+    assert len(syms) == 11, syms
+
+
+def test_library_exports_every_header_symbol(lib):
+    from cider_amd import _lib
+    syms = header_symbols()
+    assert sorted(_lib.SIGNATURES) == syms
+    for s in syms:
+        assert hasattr(lib, s), s
+    assert lib.cider_version() >= 100
+
+
+def test_workspace_bytes(lib):
+    from cider_amd import _lib
+    ws = _lib.workspace_bytes
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 1, 10240, 2560) == 0
+    assert ws(_lib.CIDER_OP_PERGROUP, 1, 10240, 2560, 128) == 0
+    # quantized activations + per-token scales, each 256-byte aligned
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 4096, 10240, 2560) == 4096 * 2560 + 4096 * 4
+    assert ws(_lib.CIDER_OP_W4A8, 1, 64, 64) == 256 + 256
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 3, 8, 10) == 256 + 256
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 0, 8, 10) == 0
+
+
+def _err(lib):
+    return lib.cider_last_error().decode()
+
+
+def test_validation_errors_without_gpu(lib):
+    from cider_amd import _lib
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    n = None
+    # bad group size (csrc/src/pergroup_primitive.mm:291-295)
+    rc = lib.cider_pergroup_linear(p, p, p, n, p, p, 1 << 20, 4, 8, 256, 100, n)
+    assert rc == _lib.CIDER_E_INVALID and "group_size" in _err(lib)
+    rc = lib.cider_pergroup_linear(p, p, p, n, p, p, 1 << 20, 4, 8, 320, 128, n)
+    assert rc == _lib.CIDER_E_INVALID and "multiple" in _err(lib)
+    rc = lib.cider_w4a8_pergroup_linear(p, p, p, n, p, p, 1 << 20, 4, 8, 256, 256, n)
+    assert rc == _lib.CIDER_E_INVALID
+    # negative dims
+    rc = lib.cider_int8_matmul_int32(p, p, p, -1, 4, 4, n)
+    assert rc == _lib.CIDER_E_INVALID and "negative" in _err(lib)
+    # NULL operands
+    rc = lib.cider_perchannel_linear(n, p, p, n, p, p, 1 << 20, 4, 8, 16, n)
+    assert rc == _lib.CIDER_E_INVALID and "x is NULL" in _err(lib)
+    # workspace missing / too small / misaligned
+    rc = lib.cider_perchannel_linear(p, p, p, n, p, n, 0, 4, 8, 16, n)
+    assert rc == _lib.CIDER_E_INVALID and "workspace" in _err(lib)
+    rc = lib.cider_perchannel_linear(p, p, p, n, p, p, 16, 4, 8, 16, n)
+    assert rc == _lib.CIDER_E_INVALID and "workspace" in _err(lib)
+    rc = lib.cider_perchannel_linear(p, p, p, n, p, ctypes.c_void_p(0x1010), 1 << 20, 4, 8, 16, n)
+    assert rc == _lib.CIDER_E_INVALID and "aligned" in _err(lib)
+    # odd K for int4
+    rc = lib.cider_w4a8_linear(p, p, p, p, p, 1 << 20, 4, 8, 15, n)
+    assert rc == _lib.CIDER_E_INVALID and "even" in _err(lib)
+    rc = lib.cider_w4_repack_ref(p, p, 8, 15, n)
+    assert rc == _lib.CIDER_E_INVALID
+    # empty problems are no-ops that succeed
+    assert lib.cider_perchannel_linear(n, n, n, n, n, n, 0, 0, 8, 16, n) == _lib.CIDER_OK
+    assert lib.cider_int8_matmul_int32(n, n, n, 5, 0, 16, n) == _lib.CIDER_OK
+    assert _err(lib) == ""
+
+
+def test_check_maps_codes_to_exceptions(lib):
+    from cider_amd import _lib
+    lib.cider_int8_matmul_int32(None, None, None, -1, 1, 1, None)
+    with pytest.raises(ValueError, match="negative"):
+        _lib.check(_lib.CIDER_E_INVALID)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.CIDER_E_HIP)
+
+
+def test_host_quantizers_match_oracle():
+    import cider_amd as C
+    rng = np.random.default_rng(0)
+    w = rng.standard_normal((37, 256)).astype(np.float32)
+    w[3] = 0
+    q, s = C.quantize_weight_int8(w)
+    qe, se = O.quantize_weight_int8(w)
+    np.testing.assert_array_equal(q, qe)
+    np.testing.assert_array_equal(s, se)
+    assert s[3] == 1.0 and (q[3] == 0).all()
+    qg, sg = C.quantize_weight_pergroup(w, 64)
+    qge, sge = O.quantize_weight_pergroup(w, 64)
+    np.testing.assert_array_equal(qg, qge)
+    np.testing.assert_array_equal(sg, sge)
+    wk = rng.standard_normal((64, 24)).astype(np.float32)
+    p, s4 = C.pack_weight_int4(wk)
+    pe, s4e = O.pack_weight_int4(wk)
+    np.testing.assert_array_equal(p, pe)
+    np.testing.assert_array_equal(s4, s4e)
+
+
+def test_pergroup_int4_packer_roundtrip():
+    import cider_amd as C
+    rng = np.random.default_rng(1)
+    w = rng.standard_normal((20, 256)).astype(np.float32)
+    packed, sc = C.pack_weight_int4_pergroup(w, 64)
+    assert packed.shape == (20, 128) and sc.shape == (4, 20) and sc.dtype == np.float16
+    q = O.unpack_w4_lo_first(packed)
+    assert q.min() >= -8 and q.max() <= 7
+    # each group's largest |w| maps to +-7 (half-to-even of exactly 7.0 or near it)
+    deq = q.reshape(20, 4, 64) * sc.T.astype(np.float32)[:, :, None]
+    err = np.abs(deq.reshape(20, 256) - w)
+    assert (err <= np.repeat(sc.T.astype(np.float32), 64, axis=1) * 0.5 + 1e-3).all()
+
+
+def test_cpu_tensors_rejected():
+    torch = pytest.importorskip("torch")
+    import cider_amd as C
+    x = torch.zeros(2, 8, dtype=torch.float16)
+    w = torch.zeros(4, 8, dtype=torch.int8)
+    s = torch.ones(4)
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        C.perchannel_linear(x, w, s)
+    with pytest.raises(RuntimeError):
+        C.int8_matmul_int32(w, w)
+    if not torch.cuda.is_available():
+        assert C.is_available() is False
+        with pytest.raises(RuntimeError):
+            C.convert_model(torch.nn.Linear(4, 4), verbose=False)

@@ -1,0 +1,353 @@
+"""Parity of the HIP path (through cider_amd -> C ABI) with the CPU oracle.
+
+Bars (stated per test): bit-exact for quantized activations, scales, int32
+accumulators, the fp16-activation MV (M == 1) and every GEMM output whose fp32
+operation order equals the reference's (per-channel, W4A8, per-group at
+M > 64); within 1 fp16 ulp / 1e-3 relative for per-group at 2 <= M <= 64,
+where the skinny kernel adds four sequential fp32 chains instead of one.
+"""
+
+import hashlib
+
+import numpy as np
+import pytest
+
+from oracle import cider_oracle as O
+from tests.golden.make_golden import bitexact_inputs
+from tests.util import assert_bits_equal, assert_f16_close
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    import cider_amd as C
+
+DEV = "cuda"
+
+
+def T(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def H(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def synth_pc(M, N, K, seed, bias=True):
+    x = O.synth_activations(M, K, seed)
+    w = O.synth_weights_i8(N, K, seed + 1)
+    sw = O.synth_scales(N, seed + 2)
+    b = ((np.random.default_rng(seed + 3).standard_normal(N) * 0.1).astype(np.float16)
+         if bias else None)
+    return x, w, sw, b
+
+
+# --------------------------------------------------------------------------
+# a1 quantize_per_token: bit-exact
+# --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("M,K", [(1, 8), (4, 2560), (7, 513), (33, 4097), (5, 10240),
+                                 (3, 16392), (2, 20000), (9, 64), (6, 6)])
+def test_quantize_bitexact(M, K):
+    x = O.synth_activations(M, K, 11 + M + K)
+    q, sa = C.quantize_per_token(T(x))
+    qe, sae = O.quantize_per_token(x)
+    assert_bits_equal(H(q), qe, "q")
+    assert_bits_equal(H(sa), sae, "scale_a")
+
+
+def test_quantize_special_rows():
+    K = 256
+    x = np.zeros((6, K), np.float16)
+    # row 0 all zeros -> s = 1, q = 0
+    # row 1 amax 127 -> s = 1: ties at .5 round away from zero (half-even would differ)
+    x[1, :6] = [127.0, 2.5, -3.5, 0.5, -0.5, 1.5]
+    # row 2 NaN is ignored by the absmax and quantizes to -128
+    x[2, :3] = [np.nan, 3.0, -6.0]
+    # row 3 inf: s = inf, inv = 0 -> 0 * inf = NaN -> -128, finite -> 0
+    x[3, :3] = [np.inf, 1.0, -2.0]
+    # row 4 subnormal fp16 only
+    x[4, :4] = np.array([6e-8, -1.2e-7, 3e-8, 0], np.float16)
+    # row 5 fp16 max
+    x[5, :3] = [65504.0, -65504.0, 1.0]
+    q, sa = C.quantize_per_token(T(x))
+    qe, sae = O.quantize_per_token(x)
+    assert_bits_equal(H(q), qe, "q")
+    assert_bits_equal(H(sa), sae, "scale_a")
+    qh = H(q)
+    assert list(qh[1, :6]) == [127, 3, -4, 1, -1, 2]
+
+
+# --------------------------------------------------------------------------
+# a3 int8_matmul_int32: the reference's own 14 shapes, bit-exact
+# --------------------------------------------------------------------------
+
+
+def test_int8_matmul_reference_shapes(bitexact_shapes):
+    for rec in bitexact_shapes:
+        a, b = bitexact_inputs(rec["M"], rec["K"], rec["N"])
+        c = H(C.int8_matmul_int32(T(a), T(b)))
+        assert c.dtype == np.int32 and c.shape == (rec["M"], rec["N"])
+        assert sha(c) == rec["sha_c"], (rec["M"], rec["K"], rec["N"])
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 64, 64), (256, 256, 128), (300, 520, 384),
+                                   (1000, 130, 1000), (2, 3, 1), (70, 90, 17)])
+def test_int8_matmul_more_shapes(M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    b = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    assert_bits_equal(H(C.int8_matmul_int32(T(a), T(b))), O.int8_matmul_int32(a, b))
+
+
+def test_int8_matmul_extremes():
+    K = 65536  # |acc| = 2^30, exact in int32
+    for M in (3, 130):
+        a = np.full((M, K), -128, np.int8)
+        b = np.full((5, K), -128, np.int8)
+        b[1] = 127
+        c = H(C.int8_matmul_int32(T(a), T(b)))
+        assert (c[:, 0] == 16384 * K).all() and (c[:, 1] == -128 * 127 * K).all()
+
+
+# --------------------------------------------------------------------------
+# a2 per-channel linear
+# --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 16, 64), (7, 33, 130), (16, 1000, 2560), (33, 257, 513),
+                                   (64, 128, 256), (65, 200, 320), (128, 10240, 2560),
+                                   (300, 1000, 1024), (257, 512, 4096), (100, 70, 100)])
+def test_perchannel_linear_bitexact(M, N, K):
+    for bias in (True, False):
+        x, w, sw, b = synth_pc(M, N, K, 1000 + M + N + K, bias)
+        y = C.perchannel_linear(T(x), T(w), T(sw), None if b is None else T(b))
+        assert y.dtype == torch.float16 and tuple(y.shape) == (M, N)
+        assert_bits_equal(H(y), O.perchannel_linear(x, w, sw, b), f"pc {M}x{N}x{K}")
+
+
+def test_perchannel_gemm_matches_linear():
+    M, N, K = 200, 384, 768
+    x, w, sw, b = synth_pc(M, N, K, 77)
+    q, sa = C.quantize_per_token(T(x))
+    y1 = C.perchannel_gemm(q, sa, T(w), T(sw), T(b))
+    y2 = C.perchannel_linear(T(x), T(w), T(sw), T(b))
+    assert_bits_equal(H(y1), H(y2))
+
+
+@pytest.mark.parametrize("N,K", [(40, 256), (130, 1024), (10240, 2560), (2560, 10240),
+                                 (100, 300), (7, 8)])
+def test_perchannel_mv(N, K):
+    x, w, sw, b = synth_pc(1, N, K, 500 + N + K)
+    y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
+    exp = O.perchannel_linear(x, w, sw, b)
+    # the kernel keeps the reference's lane / block / butterfly order at every shape
+    assert_bits_equal(y, exp, f"mv {N}x{K}")
+
+
+def test_bf16_and_fp32_inputs_roundtrip():
+    M, N, K = 70, 96, 256
+    x, w, sw, b = synth_pc(M, N, K, 9)
+    xb = torch.from_numpy(x.astype(np.float32)).to(DEV).to(torch.bfloat16)
+    y = C.perchannel_linear(xb, T(w), T(sw), T(b))
+    assert y.dtype == torch.bfloat16
+    x16 = xb.to(torch.float16).cpu().numpy()
+    exp = torch.from_numpy(O.perchannel_linear(x16, w, sw, b)).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), exp)
+    yf = C.perchannel_linear(T(x.astype(np.float32)), T(w), T(sw), T(b))
+    assert yf.dtype == torch.float32
+    assert_bits_equal(H(yf).astype(np.float16), O.perchannel_linear(x, w, sw, b))
+
+
+def test_full_size_config1_row_slices_and_determinism():
+    M, N, K = 4096, 10240, 2560
+    x, w, sw, b = synth_pc(M, N, K, 20261202, bias=False)
+    xd, wd, swd = T(x), T(w), T(sw)
+    y1 = C.perchannel_linear(xd, wd, swd)
+    y2 = C.perchannel_linear(xd, wd, swd)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16)), "non-deterministic"
+    yh = H(y1)
+    rows = np.r_[0:64, M - 64:M, np.random.default_rng(5).choice(M, 64, replace=False)]
+    exp = O.perchannel_linear(x[rows], w, sw, None)
+    assert_bits_equal(yh[rows], exp, "config1 rows")
+
+
+def test_full_size_down_proj_rows():
+    M, N, K = 1024, 2560, 10240
+    x, w, sw, b = synth_pc(M, N, K, 31, bias=True)
+    y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
+    rows = np.r_[0:32, M - 32:M]
+    assert_bits_equal(y[rows], O.perchannel_linear(x[rows], w, sw, b), "down rows")
+
+
+# --------------------------------------------------------------------------
+# a5/a6 per-group
+# --------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+@pytest.mark.parametrize("M,N,K", [(1, 72, 512), (1, 10240, 2560), (5, 48, 256), (16, 130, 512),
+                                   (64, 100, 1024), (65, 96, 512), (300, 520, 1024),
+                                   (130, 64, 320)])
+def test_pergroup_linear(gs, M, N, K):
+    if K % gs:
+        pytest.skip("K not a multiple of gs")
+    x = O.synth_activations(M, K, 40 + M + gs)
+    w = O.synth_weights_i8(N, K, 41 + N)
+    sw = O.synth_scales((K // gs, N), 42 + K)
+    b = (np.random.default_rng(43).standard_normal(N) * 0.1).astype(np.float16)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    exp = O.pergroup_linear(x, w, sw, gs, b)
+    if M > 64 or M == 1:
+        assert_bits_equal(y, exp, f"pg gs{gs} {M}x{N}x{K}")
+    else:
+        assert_f16_close(y, exp, what=f"pg gs{gs} {M}x{N}x{K}")
+
+
+# --------------------------------------------------------------------------
+# a7 W4A8 (reference layout) and the per-group int4 extension
+# --------------------------------------------------------------------------
+
+
+def test_w4_repack_matches_unpack():
+    rng = np.random.default_rng(3)
+    for K, N in [(2, 1), (64, 70), (130, 129), (4096, 256)]:
+        src = rng.integers(0, 256, (K // 2, N), dtype=np.uint8)
+        dst = H(C.repack_w4_ref(T(src)))
+        assert dst.shape == (N, K // 2)
+        np.testing.assert_array_equal(O.unpack_w4_lo_first(dst), O.unpack_w4_ref(src).T)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 32, 64), (9, 70, 160), (1, 12288, 4096),
+                                   (16, 4096, 12288), (64, 300, 1024), (100, 300, 1024),
+                                   (512, 640, 2048), (7, 33, 98)])
+def test_w4a8_linear_ref_layout(M, N, K):
+    x = O.synth_activations(M, K, 60 + M)
+    wf = np.random.default_rng(61 + N).standard_normal((K, N)).astype(np.float32)
+    packed, sw = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw)))
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw), f"w4 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("M,N,K", [(1, 48, 256), (16, 300, 1024), (17, 40, 512),
+                                   (100, 96, 512), (512, 640, 2048)])
+def test_w4a8_pergroup(gs, M, N, K):
+    x = O.synth_activations(M, K, 70 + M)
+    w4 = np.random.default_rng(71 + N).integers(-8, 8, (N, K), dtype=np.int8)
+    packed = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 72 + K).astype(np.float16)
+    y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
+    exp = O.w4a8_pergroup_linear(x, packed, sc, gs)
+    if M > 64:
+        assert_bits_equal(y, exp, f"w4g gs{gs} {M}x{N}x{K}")
+    else:
+        assert_f16_close(y, exp, what=f"w4g gs{gs} {M}x{N}x{K}")
+
+
+# --------------------------------------------------------------------------
+# committed golden fixtures
+# --------------------------------------------------------------------------
+
+
+def test_golden_fixtures(golden_cases):
+    d = golden_cases
+    for i in range(4):
+        x, w, sw, b = (d[f"pc{i}_{k}"] for k in ("x", "w", "sw", "bias"))
+        q, sa = C.quantize_per_token(T(x))
+        assert_bits_equal(H(q), d[f"pc{i}_q"])
+        assert_bits_equal(H(sa), d[f"pc{i}_sa"])
+        assert_bits_equal(H(C.perchannel_linear(T(x), T(w), T(sw), T(b))), d[f"pc{i}_y"])
+    for i in range(2):
+        x, w, sw, b = (d[f"mv{i}_{k}"] for k in ("x", "w", "sw", "bias"))
+        assert_bits_equal(H(C.perchannel_linear(T(x), T(w), T(sw), T(b))), d[f"mv{i}_y"])
+    for i in range(4):
+        x, w, sw, b = (d[f"pg{i}_{k}"] for k in ("x", "w", "sw", "bias"))
+        gs = int(d[f"pg{i}_gs"])
+        y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+        if x.shape[0] == 1:
+            assert_bits_equal(y, d[f"pg{i}_y"])
+        else:
+            assert_f16_close(y, d[f"pg{i}_y"])
+    for i in range(2):
+        x, p, sw = (d[f"w4r{i}_{k}"] for k in ("x", "packed", "sw"))
+        assert_bits_equal(H(C.w4a8_linear(T(x), T(p), T(sw))), d[f"w4r{i}_y"])
+    for i in range(2):
+        x, p, sc = (d[f"w4g{i}_{k}"] for k in ("x", "packed", "scale"))
+        gs = int(d[f"w4g{i}_gs"])
+        assert_f16_close(H(C.w4a8_pergroup_linear(T(x), T(p), T(sc), gs)), d[f"w4g{i}_y"])
+
+
+# --------------------------------------------------------------------------
+# modules, streams, errors on the device path
+# --------------------------------------------------------------------------
+
+
+def test_cider_linear_from_float_and_convert():
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(256, 96, bias=True).to(DEV).half()
+    for gs in (None, 64):
+        layer = C.CiderLinear.from_float(lin, target_group_size=gs)
+        x = torch.randn(3, 5, 256, device=DEV, dtype=torch.float16)
+        y = layer(x)
+        assert y.shape == (3, 5, 96)
+        wq = layer.w_int8.cpu().numpy()
+        sw = layer.scale_w.cpu().numpy()
+        b = layer.bias.cpu().numpy()
+        x2 = x.reshape(-1, 256).cpu().numpy()
+        exp = (O.perchannel_linear(x2, wq, sw, b) if gs is None
+               else O.pergroup_linear(x2, wq, sw, gs, b))
+        assert_f16_close(H(y).reshape(-1, 96), exp)
+    model = torch.nn.Sequential(torch.nn.Linear(128, 64), torch.nn.ReLU(),
+                                torch.nn.Sequential(torch.nn.Linear(64, 32))).to(DEV)
+    stats = C.convert_model(model, verbose=False)
+    assert stats["n_converted"] == 2
+    assert isinstance(model[0], C.CiderLinear) and isinstance(model[2][0], C.CiderLinear)
+    out = model(torch.randn(4, 128, device=DEV, dtype=torch.float16))
+    assert out.shape == (4, 32)
+
+
+def test_w4a8_module():
+    K, N = 256, 80
+    wf = np.random.default_rng(8).standard_normal((K, N)).astype(np.float32)
+    layer = C.W4A8Linear.from_weights(wf, device=DEV)
+    x = O.synth_activations(6, K, 81)
+    y = H(layer(T(x)))
+    packed, sw = O.pack_weight_int4(wf)
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw))
+
+
+def test_explicit_stream():
+    M, N, K = 130, 256, 512
+    x, w, sw, b = synth_pc(M, N, K, 5)
+    s = torch.cuda.Stream()
+    xd, wd, swd, bd = T(x), T(w), T(sw), T(b)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        y = C.perchannel_linear(xd, wd, swd, bd, stream=s)
+    s.synchronize()
+    assert_bits_equal(y.cpu().numpy(), O.perchannel_linear(x, w, sw, b))
+
+
+def test_device_errors():
+    x = torch.zeros(4, 64, device=DEV, dtype=torch.float16)
+    w = torch.zeros(8, 64, device=DEV, dtype=torch.int8)
+    s = torch.ones(8, device=DEV)
+    with pytest.raises(ValueError):
+        C.perchannel_linear(x[0], w, s)
+    with pytest.raises(ValueError):
+        C.perchannel_linear(x, w[:, :32], s)
+    with pytest.raises(ValueError):
+        C.pergroup_linear(x, w, torch.ones(1, 8, device=DEV), 100)
+    with pytest.raises(ValueError):
+        C.pergroup_linear(x, w, torch.ones(8, device=DEV), 64)
+    with pytest.raises(RuntimeError):
+        C.perchannel_linear(x.cpu(), w.cpu(), s.cpu())
+    y = C.perchannel_linear(x[:0], w, s)
+    assert tuple(y.shape) == (0, 8)
