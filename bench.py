@@ -138,7 +138,7 @@ def main():
         "kernels": {"quantize_ms": round(quant_avg, 4), "gemm_ms": round(gemm_avg, 4),
                     "gemm_tops": round(gemm_tops, 2),
                     "frac_of_int8_peak_whole_step": round(value_tops / INT8_PEAK_TOPS, 4)},
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<256,256,I8,PC>",
+        "roofline": {"bound": "mfma", "kernel": "gemm_dma_kernel<256,PC>",
                      "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TOPS", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4),
                      "traffic": load_traffic()},
