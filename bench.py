@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the M=1 decode leg")
     ap.add_argument("--seed", type=int, default=20261201)
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the default line, print one JSON line per configs[1] / "
+                         "configs[2] case (M sweep x shapes x scale modes)")
     return ap.parse_args()
 
 
@@ -82,6 +85,9 @@ def main():
     lib = _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.sweep:
+        sweep(torch, args, dev)
+        return
     M, N, K = args.M, args.N, args.K
     x, w, sw, bias = synth_inputs(torch, M, N, K, args.seed, dev)
     q = torch.empty((M, K), dtype=torch.int8, device=dev)
@@ -190,6 +196,76 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
             "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
             "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4),
             "bound": "hbm", "kernel": "mv_kernel<per-channel>"}
+
+
+def sweep(torch, args, dev):
+    """per-channel / per-group gs 128 and 64, M in {1,128,1024,4096,8192},
+    (N,K) in {(10240,2560),(2560,10240)}; configs[2]: W4A8 per-group gs 64 / 128,
+    (N,K) in {(12288,4096),(4096,12288)}, M in {1,16,512,4096}.  Timed through
+    cider_amd.ops with HIP events; weights rotate over >= 2x the MALL when a
+    call is memory-bound (M <= 64) so every launch streams from HBM."""
+    import cider_amd as C
+
+    def synth_x(M, K, seed):
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        x = torch.randn(M, K, generator=g)
+        x[:, torch.randperm(K, generator=g)[: K // 100]] *= 20.0
+        return x.to(torch.float16).to(dev)
+
+    def run(name, fn_for, M, N, K, wbytes, nbytes_alg, ops, mode):
+        copies = max(1, -(-2 * MALL_BYTES // wbytes) + 1) if M <= 64 else 1
+        fns = [fn_for(i) for i in range(copies)]
+        iters = max(20, 2 * copies)
+        for i in range(max(5, copies)):
+            fns[i % copies]()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(iters)]
+        for i in range(iters):
+            evs[i][0].record()
+            fns[i % copies]()
+            evs[i][1].record()
+        torch.cuda.synchronize()
+        ms = statistics.median([a.elapsed_time(b) for a, b in evs])
+        rec = {"case": name, "mode": mode, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+               "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+               "frac_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+               "gbs": round(nbytes_alg / (ms * 1e-3) / 1e9, 1),
+               "frac_hbm": round(nbytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+               "weight_copies": copies}
+        print(json.dumps(rec), flush=True)
+
+    g = torch.Generator(device="cpu").manual_seed(args.seed)
+    for (N, K) in [(10240, 2560), (2560, 10240)]:
+        for mode, gs in [("per-channel", 0), ("per-group-128", 128), ("per-group-64", 64)]:
+            nw = -(-2 * MALL_BYTES // (N * K)) + 1
+            ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+                  for _ in range(nw)]
+            sw = ((torch.rand(N, generator=g) * 9e-3 + 1e-3) if gs == 0 else
+                  (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3)).to(dev)
+            sbytes = 4 * N if gs == 0 else 4 * N * (K // gs)
+            for M in (1, 128, 1024, 4096, 8192):
+                x = synth_x(M, K, args.seed + M)
+                if gs == 0:
+                    fn_for = lambda i, x=x: (lambda: C.perchannel_linear(x, ws[i % nw], sw))
+                else:
+                    fn_for = lambda i, x=x, gs=gs: (lambda: C.pergroup_linear(x, ws[i % nw], sw, gs))
+                nbytes = N * K + 2 * M * K + sbytes + 2 * N + 2 * M * N
+                run("configs[1]", fn_for, M, N, K, N * K, nbytes, 2.0 * M * N * K, mode)
+            del ws
+    for (N, K) in [(12288, 4096), (4096, 12288)]:
+        for gs in (128, 64):
+            nw = -(-2 * MALL_BYTES // (N * K // 2)) + 1
+            pk = [torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).to(dev)
+                  for _ in range(nw)]
+            sc = (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3).to(torch.float16).to(dev)
+            for M in (1, 16, 512, 4096):
+                x = synth_x(M, K, args.seed + M)
+                fn_for = lambda i, x=x, gs=gs: (lambda: C.w4a8_pergroup_linear(x, pk[i % nw], sc, gs))
+                nbytes = N * K // 2 + 2 * M * K + 2 * N * (K // gs) + 2 * M * N
+                run("configs[2]", fn_for, M, N, K, N * K // 2, nbytes, 2.0 * M * N * K,
+                    f"w4a8-per-group-{gs}")
+            del pk
 
 
 def cpu_baseline(x, w, sw, bias, y, N, K):

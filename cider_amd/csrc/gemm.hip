@@ -372,7 +372,7 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
                    (a.sw == nullptr || aligned16(a.sw));
-  if (wf == W_I8 && epi != EPI_PG && vec && a.K % 64 == 0 && a.N % 8 == 0)
+  if (wf == W_I8 && epi != EPI_PG && vec && a.K % 128 == 0 && a.N % 8 == 0)
     return launch_gemm_dma(a, epi, s);  // LDS-DMA pipeline (gemm_dma.hip)
   if (epi == EPI_I32) return run_tiled<256, 256, W_I8, EPI_I32, false, 0>(a, vec, s);
   if (epi == EPI_PC) {
