@@ -18,9 +18,11 @@
 //     ones.  The butterfly over reference lanes 16, 8, 4, 2 is a shuffle over
 //     physical lanes 8, 4, 2, 1; offset 1 is the in-register sum of the pair.
 //   * x is staged once per workgroup in LDS (zero-padded to whole blocks);
-//     the weight stream is the only HBM traffic, with U blocks (U * 16 bytes
-//     per lane) in flight.  Per-group scales of the workgroup's rows are
-//     staged in LDS as well.
+//     its reads are issued first, the first 2U weight blocks right after, so
+//     the weight stream starts before the staging barrier.  Two register
+//     buffers of U blocks (U * 16 bytes per lane each) keep it in flight
+//     while blocks reduce.
+//     Per-group scales of the workgroup's rows are staged in LDS as well.
 //   * Rows per workgroup (4, 8 or 16) are chosen so the grid has enough
 //     waves to cover HBM latency on short-N shapes.
 #include "common.hpp"
@@ -76,59 +78,100 @@ __global__ __launch_bounds__(256) void mv_kernel(
   const bool live = n < N;
   const int8_t* wr = w + (int64_t)(live ? n : 0) * K;
 
-  // ---- stage x (and the per-group scales of this workgroup's rows)
-  if constexpr (XLDS) {
-    for (int e = tid; e < kp / 8; e += nthr) {
-      const int k = 8 * e;
-      i32x4 v;
-      if (VEC || k + 8 <= K) {
-        if (VEC || (((uintptr_t)(x + k) & 15) == 0)) {
-          v = ld16(x + k);
-        } else {
-          uint32_t t[4] = {0u, 0u, 0u, 0u};
-          for (int i = 0; i < 8; ++i) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
-          v = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
-        }
-      } else {
+  // weight slice of block b for this lane (16 bytes at 256 b + 16 j)
+  auto load_w = [&](int b, i32x4& v) {
+    if (VEC) {
+      // branch-free: a block index past the end re-reads the last block (its
+      // value is never consumed), so every load is issued unconditionally and
+      // the compiler can count outstanding loads exactly
+      v = ld16(wr + min(b, nb - 1) * 256 + 16 * j);
+      return;
+    }
+    const int k = b * 256 + 16 * j;
+    if (live && b < nb) {
+      {
         uint32_t t[4] = {0u, 0u, 0u, 0u};
-        for (int i = 0; i < 8; ++i)
-          if (k + i < K) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
+        for (int i = 0; i < 16; ++i)
+          if (k + i < K) t[i >> 2] |= (uint32_t)(uint8_t)wr[k + i] << (8 * (i & 3));
         v = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
       }
-      *reinterpret_cast<i32x4*>(xs + k) = v;
+    } else {
+      v = i32x4{0, 0, 0, 0};
+    }
+  };
+  // ---- stage x (and the per-group scales of this workgroup's rows).
+  // Order of issue: the x chunks (and scales) of this thread first, then the
+  // first 2U weight blocks, then the LDS stores.  Vector loads return in
+  // order, so the stores wait only for the short x reads, while the weight
+  // stream, the only HBM traffic, is already in flight across the barrier.
+  constexpr int XR = 4;  // x chunks (8 halves each) per thread held in registers
+  constexpr int SR = 4;  // per-group scales per thread held in registers
+  const int nchunk = kp / 8;
+  auto load_x = [&](int e) -> i32x4 {
+    const int k = 8 * e;
+    if (VEC || (k + 8 <= K && (((uintptr_t)(x + k) & 15) == 0))) return ld16(x + k);
+    uint32_t t[4] = {0u, 0u, 0u, 0u};
+    for (int i = 0; i < 8; ++i)
+      if (k + i < K) t[i >> 1] |= (uint32_t)x[k + i] << (16 * (i & 1));
+    return i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
+  };
+  auto load_s = [&](int e) -> float {
+    const int g = e / rows_per_wg, r = e % rows_per_wg;
+    return (n0 + r < N) ? sw[(int64_t)g * N + n0 + r] : 0.0f;
+  };
+  i32x4 xr[XR];
+  float sr[SR];
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      const int e = tid + q * nthr;
+      if (VEC)
+        xr[q] = ld16(x + 8 * min(e, nchunk - 1));  // unconditional, stored only if e < nchunk
+      else if (e < nchunk)
+        xr[q] = load_x(e);
     }
   }
   if constexpr (PG) {
-    for (int e = tid; e < G * rows_per_wg; e += nthr) {
-      const int g = e / rows_per_wg, r = e % rows_per_wg;
-      sws[e] = (n0 + r < N) ? sw[(int64_t)g * N + n0 + r] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * nthr;
+      if (e < G * rows_per_wg) sr[q] = load_s(e);
     }
+  }
+  i32x4 wa[U], wb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) load_w(u, wa[u]);
+  // VEC loads are unconditional (a branch here lets the compiler sink them
+  // past the staging barrier); the scalar path loads only what exists
+  if (VEC || U < nb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_w(U + u, wb[u]);
+  }
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      const int e = tid + q * nthr;
+      if (e < nchunk) *reinterpret_cast<i32x4*>(xs + 8 * e) = xr[q];
+    }
+    for (int e = tid + XR * nthr; e < nchunk; e += nthr)
+      *reinterpret_cast<i32x4*>(xs + 8 * e) = load_x(e);
+  }
+  if constexpr (PG) {
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * nthr;
+      if (e < G * rows_per_wg) sws[e] = sr[q];
+    }
+    for (int e = tid + SR * nthr; e < G * rows_per_wg; e += nthr) sws[e] = load_s(e);
   }
   if (XLDS || PG) __syncthreads();
 
   float r0 = 0.0f, r1 = 0.0f;  // chains of reference lanes 2j and 2j+1
-  for (int b = 0; b < nb; b += U) {
-    i32x4 wv[U];
+  auto consume = [&](int b0, const i32x4 (&wv)[U]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int k = (b + u) * 256 + 16 * j;
-      if (live && b + u < nb) {
-        if (VEC) {
-          wv[u] = ld16(wr + k);
-        } else {
-          uint32_t t[4] = {0u, 0u, 0u, 0u};
-          for (int i = 0; i < 16; ++i)
-            if (k + i < K) t[i >> 2] |= (uint32_t)(uint8_t)wr[k + i] << (8 * (i & 3));
-          wv[u] = i32x4{(int)t[0], (int)t[1], (int)t[2], (int)t[3]};
-        }
-      } else {
-        wv[u] = i32x4{0, 0, 0, 0};
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (b + u >= nb) break;
-      const int k = (b + u) * 256 + 16 * j;
+      if (b0 + u >= nb) break;
+      const int k = (b0 + u) * 256 + 16 * j;
       i32x4 xa, xb;
       if constexpr (XLDS) {
         xa = *reinterpret_cast<const i32x4*>(xs + k);
@@ -156,6 +199,20 @@ __global__ __launch_bounds__(256) void mv_kernel(
         r0 = r0 + d0;
         r1 = r1 + d1;
       }
+    }
+  };
+  // two register buffers: while one set of U blocks reduces, the other loads
+  for (int b = 0; b < nb; b += 2 * U) {
+    consume(b, wa);
+    if (b + U >= nb) break;
+    if (b + 2 * U < nb) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_w(b + 2 * U + u, wa[u]);
+    }
+    consume(b + U, wb);
+    if (b + 3 * U < nb) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load_w(b + 3 * U + u, wb[u]);
     }
   }
   // butterfly over reference lanes: offsets 16, 8, 4, 2 are physical 8, 4, 2, 1
@@ -197,9 +254,13 @@ template <bool PG, bool XLDS>
 hipError_t pick_u(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
                   uint16_t* y, int N, int K, int gs, bool vec, int rows, size_t lds,
                   hipStream_t s) {
+  // the prologue requests 2U blocks: U = ceil(nb / 2) up to 8 puts the whole
+  // row of a short-K shape in flight at once with no redundant loads
   const int nb = (K + 255) / 256;
-  if (nb <= 8) return run_mv<PG, XLDS, 8>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
-  return run_mv<PG, XLDS, 16>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  if (nb <= 8) return run_mv<PG, XLDS, 4>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  if (nb <= 10) return run_mv<PG, XLDS, 5>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  if (nb <= 12) return run_mv<PG, XLDS, 6>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
+  return run_mv<PG, XLDS, 8>(x, w, sw, bias, y, N, K, gs, vec, rows, lds, s);
 }
 
 }  // namespace
