@@ -1,8 +1,7 @@
 // Tiled int8 GEMM, main path for int8 weights with K % 128 == 0 and N % 8 == 0:
 // operands stream global -> LDS by gfx950's 16-byte LDS-DMA loads through a
-// 2-slot LDS ring of 128-byte k-stages, the MFMAs are v_mfma_i32_32x32x32_i8,
-// and the fp16 tile is staged through LDS so the output is written in whole
-// rows.
+// ring of k-stages, the MFMAs are v_mfma_i32_32x32x32_i8, and the fp16 tile
+// is staged through LDS so the output is written in whole rows.
 //
 // Reference semantics are those of gemm.hip (same epilogues, same fp32
 // operation order, bit-identical results):
@@ -12,36 +11,43 @@
 // would make the compiler wait for every LDS-DMA load in flight.)
 //
 // MI355X design
-//   * 256 threads = 4 waves (2 x 2); tile BM (m) x BN (n), BM, BN in
-//     {64, 128, 256}, chosen per shape so the grid covers the 256 CUs; at
-//     256 x 256 each wave owns a 128 x 128 sub-tile = 4 x 4 blocks of 32 x 32
-//     (16 int32 accumulators per lane per block, 256 AGPRs).  Weights are the MFMA A operand,
-//     activations the B operand.  128 x 128 per wave is the smallest wave
-//     tile whose LDS fragment traffic (64 B/clk/CU at full MFMA rate) plus the
-//     DMA fill (32 B/clk) stays inside LDS bandwidth (128 B/clk/CU).
-//   * K advances 128 bytes per stage; stage s lives in LDS slot s % NS, with
-//     NS = 2 at 256 x 256 up to 8 at 64 x 64 (as many stages as fit 128 KB).  Each
-//     wave moves its share of a stage with global_load_lds_dwordx4 (one
-//     instruction = 8 rows x 128 bytes, written contiguously to LDS at M0):
-//     no VGPR staging, no ds_write.  The loads are issued from inline asm, so
-//     the compiler does not wait for them; the kernel waits explicitly
-//     (s_waitcnt vmcnt(per-stage loads x younger stages)) before the barrier
-//     that publishes a stage.
-//   * A stage is four 32-wide k sub-steps.  The fragments of the next
-//     sub-step (8 ds_read_b128) are read while the current sub-step's 16
-//     MFMAs run.  The one barrier per stage sits before sub-step 3 of stage
-//     kt: it publishes stage kt + 1 (issued NS - 1 stages earlier) and frees
-//     the slot of stage kt, which then receives stage kt + NS.  128-byte stages
-//     halve the barriers and DMA issue slots per MFMA compared with 64-byte
-//     stages (measured: 154 vs 161 us at M=4096, N=10240, K=2560).
-//   * LDS rows are 128 bytes: chunk c of row r is stored in slot
-//     c ^ (r & 7) ^ ((r >> 3) & 1), a function of r mod 16 that keeps the
-//     16 rows of a fragment read in distinct banks; the DMA destination is
-//     contiguous, so each lane picks the global chunk of the slot it writes.
-//   * Epilogue (per-channel): each wave dequantizes its accumulators to fp16
-//     into a BM x BN LDS tile (rows padded by 16 bytes), then the workgroup
-//     stores whole 2*BN-byte rows with 16-byte lanes, so HBM sees full
-//     128-byte lines instead of 32-byte row fragments.
+//   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
+//     (n), BM, BN in {64, 128, 256}, chosen per shape so the grid covers the
+//     256 CUs; at 256 x 256 each wave owns a 128 x 128 sub-tile = 4 x 4 blocks
+//     of 32 x 32 (16 int32 accumulators per lane per block, 256 AGPRs).
+//     Weights are the MFMA A operand, activations the B operand.  128 x 128
+//     per wave is the smallest wave tile whose fragment reads (32 KB per wave
+//     per 128-byte stage, half of LDS bandwidth at full MFMA rate) leave room
+//     for the DMA fill.
+//   * K advances BK bytes per stage (128; 64 is kept for tuning); stage s
+//     lives in ring slot s % NS, NS = as many stages as fit the 160 KB LDS
+//     (2 at 256 x 256 x 128, up to 8 for small tiles).  Each wave moves its
+//     share of a stage with global_load_lds_dwordx4 (one instruction = 1 KB,
+//     written contiguously to LDS at M0): no VGPR staging, no ds_write.  The
+//     loads are issued from inline asm, so the compiler does not wait for
+//     them; every issue moves the same number of loads (a stage past the end
+//     reloads the last stage into a slot nobody reads), so the wait before
+//     each barrier is one constant s_waitcnt vmcnt.
+//   * A stage is BK / 32 k sub-steps of TN x TM MFMAs.  Each sub-step is one
+//     fixed instruction order (sched_barrier): MFMAs, with the next
+//     sub-step's fragment reads issued one per MFMA in the order they will be
+//     consumed, and after the barrier this wave's DMA loads of stage kt + NS
+//     spread one per MFMA.  Left to itself, the compiler regroups the reads
+//     next to the MFMAs that consume them and exposes LDS latency at every
+//     sub-step (measured 137 -> 124 us at M=4096, N=10240, K=2560).
+//   * The one barrier per stage sits before its last sub-step: it publishes
+//     stage kt + 1 and frees the slot of stage kt, which then receives stage
+//     kt + NS.
+//   * LDS rows are BK bytes; chunk c of row r is stored in slot
+//     c ^ ((r / (256 / BK)) % (BK / 16)): the 16 lanes LDS serves together
+//     read 16 consecutive rows at one chunk, and land in 16 distinct 16-byte
+//     bank groups.  The DMA destination is contiguous, so each lane picks the
+//     global chunk of the slot it writes.
+//   * Epilogue (per-channel): the tile's sw, sa and bias are requested at the
+//     start of the last stage and staged in LDS; each wave dequantizes its
+//     accumulators to fp16 into a BM x BN LDS tile (rows padded by 16 bytes),
+//     then the workgroup stores whole 2*BN-byte rows with 16-byte lanes, so
+//     HBM sees full 128-byte lines instead of 32-byte row fragments.
 //   * Rows past M or N are loaded from the last valid row (their results are
 //     never stored); K % 128 == 0 is required, so there is no K tail.
 #include "common.hpp"
@@ -51,10 +57,18 @@ namespace cider {
 
 namespace {
 
-__device__ __forceinline__ int swz16(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
   return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+// LDS slot of 16-byte chunk c in row r for rows of BK bytes.  The 16 lanes
+// that LDS serves together read 16 consecutive rows at one chunk; XOR-ing the
+// chunk with (r / (256 / BK)) mod (BK / 16) sends them to 16 distinct 16-byte
+// bank groups of the 256-byte bank window.
+template <int BK>
+__device__ __forceinline__ int swz(int r) {
+  return (r / (256 / BK)) % (BK / 16);
 }
 
 // 16 bytes per lane from global `src` to LDS at lds_base + 16 * lane.
@@ -87,24 +101,42 @@ __device__ __forceinline__ void wait_younger(int y) {
   }
 }
 
+constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
+
+template <int BM, int BN, int BK>
+struct DmaCfg {
+  static constexpr int CH = BK / 16;                // 16-byte chunks per LDS row
+  static constexpr int RPI = 1024 / BK;             // rows per DMA instruction
+  static constexpr int WI = BN / RPI / 4, XI = BM / RPI / 4;  // per wave
+  static constexpr int PS = WI + XI;                // vmcnt units per stage
+  static constexpr int SUBS = BK / 32;              // MFMA k sub-steps per stage
+  static constexpr int W_BYTES = BN * BK, X_BYTES = BM * BK, STAGE = W_BYTES + X_BYTES;
+  static constexpr int NS0 = kLdsBytes / STAGE;
+  static constexpr int NS = NS0 > 8 ? 8 : NS0;      // ring slots
+  static constexpr int RING = NS * STAGE;
+  static constexpr int OUT_LD = BN * 2 + 16;        // fp16 tile row pitch
+  static constexpr int OUT = BM * OUT_LD;
+  static constexpr int SCL = BN * 4 + BM * 4 + BN * 2;  // sw, sa, bias of the tile
+  static constexpr int EPI_BYTES = OUT + SCL;
+  static constexpr int SMEM = RING > EPI_BYTES ? RING : EPI_BYTES;
+  static_assert(WI >= 1 && XI >= 1, "tile too small for the DMA split");
+  static_assert(NS >= 2, "ring needs two slots");
+  static_assert(SMEM <= kLdsBytes, "LDS budget");
+  static_assert((NS - 2) * PS <= 63, "vmcnt range");
+};
+
 }  // namespace
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int BK, int EPI>
 __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   static_assert((BM == 64 || BM == 128 || BM == 256) && (BN == 64 || BN == 128 || BN == 256),
                 "tile shape");
-  constexpr int BK = 128;
+  static_assert(BK == 64 || BK == 128, "k stage");
+  using C = DmaCfg<BM, BN, BK>;
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-  constexpr int W_BYTES = BN * BK, X_BYTES = BM * BK, STAGE = W_BYTES + X_BYTES;
-  constexpr int WI = BN / 32, XI = BM / 32;  // DMA instructions (8 rows each) per wave
-  constexpr int PS = WI + XI;                 // vmcnt units per stage
-  // ring slots: as many 128-byte stages as fit in 128 KB (2..8), so small
-  // tiles, whose stages carry little MFMA work, keep more loads in flight
-  constexpr int NS0 = 131072 / STAGE;
-  constexpr int NS = NS0 < 2 ? 2 : (NS0 > 8 ? 8 : NS0);
-  constexpr int OUT_LD = BN * 2 + 16;
-  constexpr int RING = NS * STAGE, OUT = BM * OUT_LD;
-  __shared__ __attribute__((aligned(1024))) int8_t smem[RING > OUT ? RING : OUT];
+  constexpr int WI = C::WI, XI = C::XI, PS = C::PS, NS = C::NS, SUBS = C::SUBS;
+  constexpr int W_BYTES = C::W_BYTES, STAGE = C::STAGE, CH = C::CH, RPI = C::RPI;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[C::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -121,51 +153,54 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   const int m0 = (first_m + (t % per_group) % gm) * BM;
   const int n0 = ((t % per_group) / gm) * BN;
 
-  // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*8 .. +8;
-  // lane l writes row R0 + l/8, slot l%8 = chunk ^ swz(row mod 16).
+  // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*RPI ..
+  // + RPI; lane l writes row R0 + l / CH, slot l % CH, which holds global
+  // chunk slot ^ swz(row).
   const int8_t* wsrc[WI];
   const int8_t* xsrc[XI];
   {
-    const int rr = lane >> 3, slot = lane & 7;
+    const int rr = lane / CH, slot = lane % CH;
     const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
-      const int row = (wave * WI + i) * 8 + rr;
-      const int chunk = slot ^ swz16(row & 15);
+      const int row = (wave * WI + i) * RPI + rr;
       const int n = min(n0 + row, N - 1);
-      wsrc[i] = W + (int64_t)n * K + chunk * 16;
+      wsrc[i] = W + (int64_t)n * K + (slot ^ swz<BK>(row)) * 16;
     }
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
-      const int row = (wave * XI + i) * 8 + rr;
-      const int chunk = slot ^ swz16(row & 15);
+      const int row = (wave * XI + i) * RPI + rr;
       const int m = min(m0 + row, M - 1);
-      xsrc[i] = p.x + (int64_t)m * K + chunk * 16;
+      xsrc[i] = p.x + (int64_t)m * K + (slot ^ swz<BK>(row)) * 16;
     }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem);
-  auto issue = [&](int kt) {
-    const uint32_t sb = lds0 + (uint32_t)((kt % NS) * STAGE);
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < WI; ++i) dma16(wsrc[i] + k0, sb + (wave * WI + i) * 8 * BK);
-#pragma unroll
-    for (int i = 0; i < XI; ++i) dma16(xsrc[i] + k0, sb + W_BYTES + (wave * XI + i) * 8 * BK);
+  // DMA instruction d (0 .. PS-1) of this wave for stage st into ring slot
+  // `slot`: W rows first, then X rows.
+  auto dma_one = [&](int st, int slot, int d) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * STAGE);
+    const int k0 = st * BK;
+    if (d < WI)
+      dma16(wsrc[d < WI ? d : 0] + k0, sb + (wave * WI + d) * 1024);
+    else
+      dma16(xsrc[d >= WI ? d - WI : 0] + k0, sb + W_BYTES + (wave * XI + d - WI) * 1024);
   };
 
+  // fragment r (W blocks 0..TN-1, then X blocks) of k sub-step j in ring
+  // slot `slot`: lane l reads row l % 32 of the 32-row block, chunk
+  // 2j + l / 32 (the same k mapping for both operands)
   const int frow = lane & 31;
-  const int fsw = swz16(lane & 15);
-  auto read_sub = [&](int kt, int j, i32x4 (&wf)[TN], i32x4 (&xf)[TM]) {
-    const int8_t* Ws = smem + (kt % NS) * STAGE;
-    const int8_t* Xs = Ws + W_BYTES;
+  const int fsw = swz<BK>(lane & 15);
+  auto read_frag = [&](int slot, int j, int r, i32x4 (&wfn)[TN], i32x4 (&xfn)[TM]) {
+    const int8_t* Ws = smem + slot * STAGE;
     const int fs = ((2 * j + (lane >> 5)) ^ fsw) << 4;
-#pragma unroll
-    for (int a = 0; a < TN; ++a)
-      wf[a] = *reinterpret_cast<const i32x4*>(Ws + (wn * WN + a * 32 + frow) * BK + fs);
-#pragma unroll
-    for (int b = 0; b < TM; ++b)
-      xf[b] = *reinterpret_cast<const i32x4*>(Xs + (wm * WM + b * 32 + frow) * BK + fs);
+    if (r < TN)
+      wfn[r < TN ? r : 0] =
+          *reinterpret_cast<const i32x4*>(Ws + (wn * WN + r * 32 + frow) * BK + fs);
+    else
+      xfn[r >= TN ? r - TN : 0] = *reinterpret_cast<const i32x4*>(
+          Ws + W_BYTES + (wm * WM + (r - TN) * 32 + frow) * BK + fs);
   };
 
   i32x16 acc[TN][TM];
@@ -175,40 +210,83 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
     for (int b = 0; b < TM; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
-  auto compute = [&](const i32x4 (&wf)[TN], const i32x4 (&xf)[TM]) {
+
+  // One k sub-step: the TN*TM MFMAs on fragments (wc, xc).  Between them, in
+  // a fixed order (sched_barrier), go the reads of the next sub-step's
+  // fragments (slot rs, sub-step rj) into (wn_, xn) when rd, and this wave's
+  // DMA loads of stage dst into slot dsl when dma.  Each read is issued at
+  // least TN*TM - TN - TM MFMAs before its use, so no MFMA waits on LDS, and
+  // the DMA issue overlaps MFMAs instead of following the barrier on its own.
+  auto step = [&](const i32x4 (&wc)[TN], const i32x4 (&xc)[TM], bool rd, int rs, int rj,
+                  i32x4 (&wn_)[TN], i32x4 (&xn)[TM], bool dma, int dst, int dsl) {
+    constexpr int NMF = TN * TM, NR = TN + TM;
 #pragma unroll
-    for (int a = 0; a < TN; ++a)
+    for (int idx = 0; idx < NMF; ++idx) {
+      acc[idx / TM][idx % TM] = mfma32(wc[idx / TM], xc[idx % TM], acc[idx / TM][idx % TM]);
+      // reads go one per MFMA from the first (the rest after the last MFMA
+      // when there are more reads than MFMAs), in the order the next sub-step
+      // consumes them: W0, X0 .. X(TM-1), W1 .. W(TN-1)
+      if (rd) {
 #pragma unroll
-      for (int b = 0; b < TM; ++b) acc[a][b] = mfma32(wf[a], xf[b], acc[a][b]);
+        for (int q = 0; q < NR; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx)
+            read_frag(rs, rj, q == 0 ? 0 : (q <= TM ? TN + q - 1 : q - TM), wn_, xn);
+      }
+      if (dma) {
+#pragma unroll
+        for (int d = 0; d < PS; ++d)
+          if (d * NMF / PS == idx) dma_one(dst, dsl, d);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
 
   const int nk = K / BK;
-  i32x4 wf0[TN], xf0[TM], wf1[TN], xf1[TM];
-  if (nk > 0) {
-    const int pre = min(nk, NS);
-    for (int st = 0; st < pre; ++st) issue(st);
-    wait_younger<PS, NS - 1>(pre - 1);
+  i32x4 wf[2][TN], xf[2][TM];
+  // Prologue: stages 0 .. NS-1 into slots 0 .. NS-1.  Every issue moves PS
+  // loads per wave; a stage past the end reloads stage nk-1 into a slot that
+  // is never read, so the loads in flight at each wait are always the same
+  // count.
+#pragma unroll
+  for (int st = 0; st < NS; ++st)
+#pragma unroll
+    for (int d = 0; d < PS; ++d) dma_one(min(st, nk - 1), st, d);
+  wait_vmcnt<(NS - 1) * PS>();  // stage 0 landed (loads complete in order)
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < TN + TM; ++r) read_frag(0, 0, r, wf[0], xf[0]);
+
+  // Stage kt: sub-steps 0 .. SUBS-1.  The barrier before the last sub-step
+  // publishes stage kt+1 (NS-2 younger stages still in flight) and frees the
+  // slot of stage kt, which receives stage kt+NS during that sub-step.
+  for (int kt = 0; kt < nk - 1; ++kt) {
+    const int sl = kt % NS, sl1 = (kt + 1) % NS;
+#pragma unroll
+    for (int j = 0; j < SUBS - 1; ++j)
+      step(wf[j & 1], xf[j & 1], true, sl, j + 1, wf[(j + 1) & 1], xf[(j + 1) & 1], false, 0, 0);
+    wait_vmcnt<(NS - 2) * PS>();
     __syncthreads();
-    read_sub(0, 0, wf0, xf0);
+    step(wf[(SUBS - 1) & 1], xf[(SUBS - 1) & 1], true, sl1, 0, wf[0], xf[0], true,
+         min(kt + NS, nk - 1), sl);
   }
-  // stage kt: sub-steps 0..3; the barrier before sub-step 3 publishes stage
-  // kt+1 (issued NS-1 stages earlier) and frees the slot of stage kt, which
-  // receives stage kt+NS.
-  for (int kt = 0; kt < nk; ++kt) {
-    read_sub(kt, 1, wf1, xf1);
-    compute(wf0, xf0);
-    read_sub(kt, 2, wf0, xf0);
-    compute(wf1, xf1);
-    read_sub(kt, 3, wf1, xf1);
-    compute(wf0, xf0);
-    if (kt + 1 < nk) {
-      wait_younger<PS, NS - 2>(min(nk - 1, kt + NS - 1) - (kt + 1));
-      __syncthreads();
-      if (kt + NS < nk) issue(kt + NS);
-      read_sub(kt + 1, 0, wf0, xf0);
-    }
-    compute(wf1, xf1);
+  // Last stage.  The per-channel epilogue's scales are requested here, so
+  // their latency hides behind the last MFMAs; indices are clamped, so the
+  // loads are unconditional.
+  float sw_t = 0.0f, sa_t = 0.0f;
+  uint16_t b_t = 0;
+  if constexpr (EPI == EPI_PC) {
+    sw_t = reinterpret_cast<const float*>(p.sw)[min(n0 + tid % BN, N - 1)];
+    sa_t = p.sa[min(m0 + tid % BM, M - 1)];
+    if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
   }
+  {
+    const int sl = (nk - 1) % NS;
+#pragma unroll
+    for (int j = 0; j < SUBS - 1; ++j)
+      step(wf[j & 1], xf[j & 1], true, sl, j + 1, wf[(j + 1) & 1], xf[(j + 1) & 1], false, 0, 0);
+    step(wf[(SUBS - 1) & 1], xf[(SUBS - 1) & 1], false, 0, 0, wf[0], xf[0], false, 0, 0);
+  }
+  wait_vmcnt<0>();  // the reloads past the end land before LDS is reused
 
   // ---- epilogue: lane holds, per 32x32 block and group g, 4 consecutive n
   //      n = nblk + 8g + 4 (lane / 32) + [0..3] of row m = mblk + lane % 32
@@ -230,32 +308,31 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
         }
     }
   } else {
-    __syncthreads();  // every wave is done with the ring: reuse it for the tile
+    // LDS after the ring is released: [0, OUT) fp16 tile, then sw, sa, bias
+    float* ssw = reinterpret_cast<float*>(smem + C::OUT);
+    float* ssa = ssw + BN;
+    uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + BM);
+    __syncthreads();  // every wave is done with the ring
+    if (tid < BN) {
+      ssw[tid] = sw_t;
+      sbias[tid] = b_t;
+    }
+    if (tid < BM) ssa[tid] = sa_t;
+    __syncthreads();
     float sam[TM];
 #pragma unroll
-    for (int b = 0; b < TM; ++b) {
-      const int m = m0 + wm * WM + b * 32 + frow;
-      sam[b] = m < M ? p.sa[m] : 0.0f;
-    }
+    for (int b = 0; b < TM; ++b) sam[b] = ssa[wm * WM + b * 32 + frow];
 #pragma unroll
     for (int a = 0; a < TN; ++a) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int nl = wn * WN + a * 32 + 8 * g + 4 * h;  // column in tile
-        const int n = n0 + nl;
-        float swv[4] = {0.f, 0.f, 0.f, 0.f}, bv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (n < N) {  // N % 8 == 0 on this path: n < N implies n + 3 < N
-          const f32x4 v = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.sw) + n);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) swv[r] = v[r];
-          if (p.bias) {
-            const i32x2 bb = ld8(p.bias + n);
-            bv[0] = h2f((uint16_t)((uint32_t)bb[0] & 0xffffu));
-            bv[1] = h2f((uint16_t)((uint32_t)bb[0] >> 16));
-            bv[2] = h2f((uint16_t)((uint32_t)bb[1] & 0xffffu));
-            bv[3] = h2f((uint16_t)((uint32_t)bb[1] >> 16));
-          }
-        }
+        const f32x4 swv = *reinterpret_cast<const f32x4*>(ssw + nl);
+        const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+        const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
+                             h2f((uint16_t)((uint32_t)bb[0] >> 16)),
+                             h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
+                             h2f((uint16_t)((uint32_t)bb[1] >> 16))};
 #pragma unroll
         for (int b = 0; b < TM; ++b) {
           const int ml = wm * WM + b * 32 + frow;  // row in tile
@@ -267,7 +344,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
             if (p.bias) v = v + bv[r];
             o[r] = f2h(v);
           }
-          *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
+          *reinterpret_cast<i32x2*>(smem + ml * C::OUT_LD + nl * 2) =
               i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
         }
       }
@@ -282,17 +359,17 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
       const int m = m0 + rr;
       if (m < M && n < N)
         *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
-            *reinterpret_cast<const i32x4*>(smem + rr * OUT_LD + cl * 2);
+            *reinterpret_cast<const i32x4*>(smem + rr * C::OUT_LD + cl * 2);
     }
   }
 }
 
 namespace {
 
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int BK, int EPI>
 hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  gemm_dma_kernel<BM, BN, EPI><<<tiles, 256, 0, s>>>(a);
+  gemm_dma_kernel<BM, BN, BK, EPI><<<tiles, 256, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -315,11 +392,11 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
     }
   }
   switch (best) {
-    case 0: return run_dma<256, 256, EPI>(a, s);
-    case 1: return run_dma<128, 256, EPI>(a, s);
-    case 2: return run_dma<128, 128, EPI>(a, s);
-    case 3: return run_dma<64, 128, EPI>(a, s);
-    default: return run_dma<64, 64, EPI>(a, s);
+    case 0: return run_dma<256, 256, 128, EPI>(a, s);
+    case 1: return run_dma<128, 256, 128, EPI>(a, s);
+    case 2: return run_dma<128, 128, 128, EPI>(a, s);
+    case 3: return run_dma<64, 128, 128, EPI>(a, s);
+    default: return run_dma<64, 64, 128, EPI>(a, s);
   }
 }
 
