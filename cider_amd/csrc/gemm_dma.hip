@@ -127,8 +127,26 @@ struct DmaCfg {
 
 }  // namespace
 
+// Tile (m0, n0) of region t of a grid of BM x BN tiles over columns
+// [n_begin, n_end): tiles are taken in groups of GROUP_M tile rows, n-major
+// inside a group, so consecutive tiles share weight columns in L2.
+template <int BM, int BN>
+__device__ __forceinline__ void tile_coords(int t, int M, int n_begin, int n_end, int& m0,
+                                            int& n0) {
+  constexpr int GROUP_M = 4;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (n_end - n_begin + BN - 1) / BN;
+  const int per_group = GROUP_M * tiles_n;
+  const int grp = t / per_group;
+  const int first_m = grp * GROUP_M;
+  const int gm = min(tiles_m - first_m, GROUP_M);
+  m0 = (first_m + (t % per_group) % gm) * BM;
+  n0 = n_begin + ((t % per_group) / gm) * BN;
+}
+
+// One BM x BN output tile over the whole K.  smem: DmaCfg::SMEM bytes of LDS.
 template <int BM, int BN, int BK, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
+__device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const int n0,
+                                         int8_t* __restrict__ smem) {
   static_assert((BM == 64 || BM == 128 || BM == 256) && (BN == 64 || BN == 128 || BN == 256),
                 "tile shape");
   static_assert(BK == 64 || BK == 128, "k stage");
@@ -136,22 +154,11 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
   constexpr int WI = C::WI, XI = C::XI, PS = C::PS, NS = C::NS, SUBS = C::SUBS;
   constexpr int W_BYTES = C::W_BYTES, STAGE = C::STAGE, CH = C::CH, RPI = C::RPI;
-  __shared__ __attribute__((aligned(1024))) int8_t smem[C::SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int M = p.M, N = p.N, K = p.K;
-
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
-  constexpr int GROUP_M = 4;
-  const int per_group = GROUP_M * tiles_n;
-  const int grp = t / per_group;
-  const int first_m = grp * GROUP_M;
-  const int gm = min(tiles_m - first_m, GROUP_M);
-  const int m0 = (first_m + (t % per_group) % gm) * BM;
-  const int n0 = ((t % per_group) / gm) * BN;
 
   // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*RPI ..
   // + RPI; lane l writes row R0 + l / CH, slot l % CH, which holds global
@@ -364,6 +371,36 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   }
 }
 
+// Uniform grid: one BM x BN tile per workgroup.
+template <int BM, int BN, int BK, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK>::SMEM];
+  int m0, n0;
+  tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), p.M, 0, p.N, m0, n0);
+  dma_tile<BM, BN, BK, EPI>(p, m0, n0, smem);
+}
+
+// Two tile sizes in one grid, so that the last round of workgroups is not
+// half empty: workgroups [0, nbig) take 256 x 256 tiles of columns
+// [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
+// many tiles of half the work.  Workgroups start in index order, so the small
+// tiles form the last round; each region has its own XCD remap.
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
+                                                                int nsplit) {
+  constexpr int S1 = DmaCfg<256, 256, 128>::SMEM, S2 = DmaCfg<128, 256, 128>::SMEM;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
+  const int b = blockIdx.x;
+  int m0, n0;
+  if (b < nbig) {
+    tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
+    dma_tile<256, 256, 128, EPI>(p, m0, n0, smem);
+  } else {
+    tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
+    dma_tile<128, 256, 128, EPI>(p, m0, n0, smem);
+  }
+}
+
 namespace {
 
 template <int BM, int BN, int BK, int EPI>
@@ -373,10 +410,43 @@ hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <int EPI>
 hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
-  // Estimated time = rounds of 256 workgroups x tile area / tile efficiency
-  // (MFMA work per LDS byte falls with the tile); ties go to the larger tile.
+  const int cus = num_cus();
+  // 256 x 256 tiles whose last round is at most half full and made of whole
+  // tile columns: cover those columns with 128 x 256 tiles instead, so the
+  // last round runs on (up to) every CU with half-length tiles.
+  {
+    const int tm = (a.M + 255) / 256, tn = (a.N + 255) / 256;
+    const int64_t T = (int64_t)tm * tn;
+    const int R = (int)(T % cus);
+    if (T > cus && R > 0 && 2 * R <= cus && R % tm == 0) {
+      const int tail_cols = R / tm;
+      const int nsplit = (tn - tail_cols) * 256;
+      const int nbig = (int)(T - R);
+      const int nsmall = ((a.M + 127) / 128) * tail_cols;
+      gemm_dma_mixed_kernel<EPI><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
+      return hipGetLastError();
+    }
+  }
+  // Otherwise one tile size: estimated time = rounds of `cus` workgroups x
+  // tile area / tile efficiency (MFMA work per LDS byte falls with the
+  // tile); ties go to the larger tile.
   struct Cand { int bm, bn; double eff; };
   static const Cand cands[] = {{256, 256, 1.0}, {128, 256, 0.8}, {128, 128, 0.6},
                                {64, 128, 0.45}, {64, 64, 0.3}};
@@ -385,7 +455,7 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
   for (int i = 0; i < 5; ++i) {
     const int64_t tiles =
         (int64_t)((a.M + cands[i].bm - 1) / cands[i].bm) * ((a.N + cands[i].bn - 1) / cands[i].bn);
-    const double cost = (double)((tiles + 255) / 256) * cands[i].bm * cands[i].bn / cands[i].eff;
+    const double cost = (double)((tiles + cus - 1) / cus) * cands[i].bm * cands[i].bn / cands[i].eff;
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = i;

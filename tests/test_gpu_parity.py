@@ -98,7 +98,8 @@ def test_int8_matmul_reference_shapes(bitexact_shapes):
 
 
 @pytest.mark.parametrize("M,N,K", [(65, 64, 64), (256, 256, 128), (300, 520, 384),
-                                   (1000, 130, 1000), (2, 3, 1), (70, 90, 17)])
+                                   (1000, 130, 1000), (2, 3, 1), (70, 90, 17),
+                                   (2048, 10240, 128)])
 def test_int8_matmul_more_shapes(M, N, K):
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
@@ -124,11 +125,14 @@ def test_int8_matmul_extremes():
 # Shapes cover every GEMM variant: skinny (M <= 64), the register-staged tiled
 # kernel (K % 128 != 0 or N % 8 != 0) and the LDS-DMA kernel at each tile the
 # dispatcher picks: 64x64 (M=128/300/257), 128x128 (M=2048, N=2048),
-# 128x256 (M=1024, N=10240), 256x256 (the full-size tests below).
+# 128x256 (M=1024, N=10240), 256x256 (the full-size tests below), and the
+# mixed 256x256 + 128x256 grid (M=2048, N=10240; M=1000, N=16640 with a
+# partial last tile row).
 @pytest.mark.parametrize("M,N,K", [(2, 16, 64), (7, 33, 130), (16, 1000, 2560), (33, 257, 513),
                                    (64, 128, 256), (65, 200, 320), (128, 10240, 2560),
                                    (300, 1000, 1024), (257, 512, 4096), (100, 70, 100),
-                                   (1024, 10240, 2560), (2048, 2048, 1024), (600, 8192, 768)])
+                                   (1024, 10240, 2560), (2048, 2048, 1024), (600, 8192, 768),
+                                   (2048, 10240, 256), (1000, 16640, 128)])
 def test_perchannel_linear_bitexact(M, N, K):
     for bias in (True, False):
         x, w, sw, b = synth_pc(M, N, K, 1000 + M + N + K, bias)
