@@ -47,6 +47,10 @@ def parse():
     ap.add_argument("--K", type=int, default=2560)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the M=1 decode leg")
+    ap.add_argument("--qwen3", action="store_true",
+                    help="instead of the default line, print one JSON line for configs[3]: "
+                         "Qwen3-8B-shaped W8A8 stack, 2048-token prefill + 128 greedy "
+                         "decode steps (decode step captured as a HIP graph)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run three 256 MiB device-to-device copies, the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
@@ -92,6 +96,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.sweep:
         sweep(torch, args, dev)
+        return
+    if args.qwen3:
+        bench_qwen3(torch, args, dev)
         return
     M, N, K = args.M, args.N, args.K
     x, w, sw, bias = synth_inputs(torch, M, N, K, args.seed, dev)
@@ -328,6 +335,66 @@ def cpu_model():
     except OSError:
         pass
     return "unknown"
+
+
+def bench_qwen3(torch, args, dev):
+    """random-init Qwen3-8B-shaped stack (cider_amd/qwen3.py), all
+    projections W8A8 per-channel; prefill of 2048 synthetic ids uniform over
+    the vocabulary, then 128 greedy decode steps, each one replay of a HIP
+    graph of the whole step (MV linears, attention over the device-resident
+    KV cache, fp16 lm_head, argmax)."""
+    from cider_amd import qwen3 as Q
+    cfg = Q.QWEN3_8B
+    L, steps = 2048, 128
+    t0 = time.perf_counter()
+    m = Q.Qwen3(cfg, max_len=L + steps + 1, seed=args.seed, device=dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    ids = torch.randint(0, cfg.vocab_size, (L,), device=dev, generator=gen)
+    stream = torch.cuda.current_stream(dev)
+    m.prefill(ids)  # warm-up
+    torch.cuda.synchronize()
+    reps = 3
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    e[0].record(stream)
+    for _ in range(reps):
+        logits = m.prefill(ids)
+    e[1].record(stream)
+    torch.cuda.synchronize()
+    prefill_ms = e[0].elapsed_time(e[1]) / reps
+    first = torch.argmax(logits[-1].float()).reshape(1)
+    state = {"tok": first.clone(), "pos": torch.tensor([L], device=dev),
+             "i": torch.zeros(1, dtype=torch.int64, device=dev),
+             "out": torch.zeros(steps, dtype=torch.int64, device=dev)}
+    g, _ = m.capture_decode(state)
+    e[0].record(stream)
+    for _ in range(steps):
+        g.replay()
+    e[1].record(stream)
+    torch.cuda.synchronize()
+    decode_ms = e[0].elapsed_time(e[1]) / steps
+    out = state["out"].cpu()
+    macs = cfg.linear_macs_per_token()
+    w_bytes = macs + cfg.vocab_size * cfg.hidden_size * 2  # int8 linears + fp16 lm_head
+    print(json.dumps({
+        "metric": "Qwen3-8B-shaped W8A8 stack: prefill ms (2048 tokens), decode ms/token",
+        "value": round(prefill_ms, 3), "unit": "ms", "higher_is_better": False,
+        "n_gpus": 1, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "configs[3]: 36 layers, hidden 4096, intermediate 12288, "
+                               "32 q / 8 kv heads of 128, vocab 151936 (fp16 lm_head), "
+                               "random init, prefill 2048 ids + 128 greedy decode steps",
+                   "seed": args.seed},
+        "prefill": {"ms": round(prefill_ms, 3), "tokens_per_s": round(L / prefill_ms * 1e3, 1),
+                    "linear_tops": round(2 * L * macs / (prefill_ms * 1e-3) / 1e12, 1)},
+        "decode": {"ms_per_token": round(decode_ms, 4),
+                   "tokens_per_s": round(1e3 / decode_ms, 1),
+                   "weight_gbs": round(w_bytes / (decode_ms * 1e-3) / 1e9, 1),
+                   "steps": steps, "graph": True,
+                   "tokens_distinct": int(out.unique().numel())},
+        "build_s": round(build_s, 1),
+    }), flush=True)
 
 
 def gemm_kernel_name(M, N, K, dev):

@@ -18,7 +18,7 @@ from typing import Optional
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 
 
 def set_mode(mode: str):
@@ -69,15 +69,42 @@ class CiderLinear(torch.nn.Module):
         self.group_size = group_size
         self._in_features = in_features
         self._out_features = out_features
+        self._ws_cache = {}
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape
         x2 = x.reshape(-1, self._in_features)
-        if self._mode == "per_channel":
+        if (self._mode == "per_channel" and x2.dtype == torch.float16 and x2.is_cuda
+                and x2.is_contiguous() and x2.device == self.w_int8.device):
+            y = self._perchannel_direct(x2)
+        elif self._mode == "per_channel":
             y = ops.perchannel_linear(x2, self.w_int8, self.scale_w, self.bias)
         else:
             y = ops.pergroup_linear(x2, self.w_int8, self.scale_w, self.group_size, self.bias)
         return y.reshape(*orig_shape[:-1], self._out_features)
+
+    def _perchannel_direct(self, x2: torch.Tensor) -> torch.Tensor:
+        """Per-channel call straight into the C ABI for the common case (fp16,
+        contiguous, same device): the buffers are already in the library's
+        types, so only the output and the workspace are allocated.  The
+        launch goes to the current stream, so it can be captured in a graph."""
+        lib = _lib.load()
+        M = x2.shape[0]
+        N, K = self._out_features, self._in_features
+        dev = x2.device
+        nb = self._ws_cache.get(M)
+        if nb is None:
+            nb = _lib.workspace_bytes(_lib.CIDER_OP_PERCHANNEL, M, N, K, 0)
+            self._ws_cache[M] = nb
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev) if nb else None
+        rc = lib.cider_perchannel_linear(
+            x2.data_ptr(), self.w_int8.data_ptr(), self.scale_w.data_ptr(), self.bias.data_ptr(),
+            y.data_ptr(), ws.data_ptr() if ws is not None else None, nb, M, N, K,
+            torch.cuda.current_stream(dev).cuda_stream)
+        if rc != 0:
+            _lib.check(rc)
+        return y
 
     @staticmethod
     def from_float(layer: torch.nn.Module, target_group_size: Optional[int] = None,
