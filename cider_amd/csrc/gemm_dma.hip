@@ -51,57 +51,13 @@
 //   * Rows past M or N are loaded from the last valid row (their results are
 //     never stored); K % 128 == 0 is required, so there is no K tail.
 #include "common.hpp"
+#include "dma_common.hpp"
 #include "kernels.hpp"
 
 namespace cider {
 
 namespace {
 
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-__device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-
-// LDS slot of 16-byte chunk c in row r for rows of BK bytes.  The 16 lanes
-// that LDS serves together read 16 consecutive rows at one chunk; XOR-ing the
-// chunk with (r / (256 / BK)) mod (BK / 16) sends them to 16 distinct 16-byte
-// bank groups of the 256-byte bank window.
-template <int BK>
-__device__ __forceinline__ int swz(int r) {
-  return (r / (256 / BK)) % (BK / 16);
-}
-
-// 16 bytes per lane from global `src` to LDS at lds_base + 16 * lane.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-  asm volatile(
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %0, off"
-      :
-      : "v"(src), "s"(lds_base)
-      : "memory", "m0");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Waits until at most y * PS LDS-DMA loads of this wave are outstanding,
-// y <= Y (the immediate must be a compile-time constant).
-template <int PS, int Y>
-__device__ __forceinline__ void wait_younger(int y) {
-  if constexpr (Y == 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (y >= Y)
-      wait_vmcnt<Y * PS>();
-    else
-      wait_younger<PS, Y - 1>(y);
-  }
-}
-
-constexpr int kLdsBytes = 160 * 1024;  // gfx950 LDS per workgroup
 
 template <int BM, int BN, int BK>
 struct DmaCfg {
@@ -126,22 +82,6 @@ struct DmaCfg {
 };
 
 }  // namespace
-
-// Tile (m0, n0) of region t of a grid of BM x BN tiles over columns
-// [n_begin, n_end): tiles are taken in groups of GROUP_M tile rows, n-major
-// inside a group, so consecutive tiles share weight columns in L2.
-template <int BM, int BN>
-__device__ __forceinline__ void tile_coords(int t, int M, int n_begin, int n_end, int& m0,
-                                            int& n0) {
-  constexpr int GROUP_M = 4;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (n_end - n_begin + BN - 1) / BN;
-  const int per_group = GROUP_M * tiles_n;
-  const int grp = t / per_group;
-  const int first_m = grp * GROUP_M;
-  const int gm = min(tiles_m - first_m, GROUP_M);
-  m0 = (first_m + (t % per_group) % gm) * BM;
-  n0 = n_begin + ((t % per_group) / gm) * BN;
-}
 
 // One BM x BN output tile over the whole K.  smem: DmaCfg::SMEM bytes of LDS.
 template <int BM, int BN, int BK, int EPI>
@@ -410,21 +350,6 @@ hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int num_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 template <int EPI>
 hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
   const int cus = num_cus();
@@ -471,6 +396,21 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device).
+int num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
 // Eligible: int8 weights, EPI_I32 or EPI_PC, K % 128 == 0, N % 8 == 0,
 // 16-byte aligned operands.

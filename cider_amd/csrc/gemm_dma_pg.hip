@@ -1,0 +1,430 @@
+// Per-group int8 GEMM on the LDS-DMA pipeline (int8 weights, K % 128 == 0,
+// N % 8 == 0, M > 64).  The dispatcher sends gs = 128 here; gs = 64 compiles
+// and is bit-exact too, but its four accumulator sets spill.
+//
+// Reference semantics (cider/kernels/pergroup_int8_gemm.metal:90-191), kept
+// operation for operation, so results are bit-identical to the restatement:
+//   D_g[m,n] = sum over the gs k of group g of qa[m,k] * w[n,k]   (exact int32)
+//   acc      = +0.0;  acc = acc + f32(f32(D_g) * sw[g,n])  for g = 0, 1, ...
+//   y[m,n]   = h(f32(acc * sa[m]) [+ f32(bias[n])])
+//
+// MI355X design
+//   * Tile 128 x 128, 4 waves of 64 x 64 (TM = TN = 2 blocks of 32 x 32),
+//     v_mfma_i32_32x32x32_i8; operands reach LDS by global_load_lds_dwordx4
+//     through a 4-slot ring of 128-byte k-stages,
+//     with the constant-count waits, swizzle and fixed-order sub-steps of
+//     the per-channel kernel (gemm_dma.hip).
+//   * Group accumulators: int32 sets per group, 2 * (groups per stage) of
+//     them (2 at gs = 128, 4 at gs = 64; 64 accumulators per lane each at
+//     the 128 x 128 tile, all in AGPRs).  A group's first MFMA takes C = 0 (an
+//     inline constant), so starting a group costs nothing.  The groups of
+//     stage kt are flushed during stage kt+1, interleaved with its MFMAs in the
+//     same fixed order, into the 64 fp32 accumulators per lane: 4 VALU ops per
+//     accumulator and group (read, convert, multiply by the scale, add),
+//     groups in order.  Every set is read a whole stage after its last MFMA,
+//     so the flush never waits on the matrix pipe.  The flush is the VALU
+//     bound of the kernel: 2x the MFMA time at gs = 128, 4x at gs = 64.
+//     Stage 0 flushes the zero sets of "stage -1" with stage 0's scales
+//     (adding +0.0); the last stage flushes its own groups after its MFMAs.
+//   * Scales: wave 0 DMAs the scale rows of a stage's groups (sw[g, n0..n0+127])
+//     into an 8-slot LDS ring of its own, so a row stays in LDS until its
+//     group has been flushed during the next stage.  Wave 0 therefore moves one
+//     more load per stage than the others, and waits with its own count.
+//   * Epilogue: sa and bias are requested during the last stage; acc * sa
+//     (+ bias) is converted to fp16, staged in LDS and stored in whole rows.
+#include "common.hpp"
+#include "dma_common.hpp"
+#include "kernels.hpp"
+
+#include <type_traits>
+
+namespace cider {
+
+namespace {
+
+// Geometry of a BM x 128 tile (BM = 256 or 128), 4 waves of (BM / 2) x 64.
+template <int BM>
+struct PgCfg {
+  static constexpr int BN = 128, BK = 128;
+  static constexpr int WM = BM / 2, WN = 64, TM = WM / 32, TN = 2;
+  static constexpr int CH = BK / 16, RPI = 1024 / BK;        // 8, 8
+  static constexpr int WI = BN / RPI / 4;                    // DMA instructions (W rows)
+  static constexpr int XI = BM / RPI / 4;                    // DMA instructions (X rows)
+  static constexpr int PS = WI + XI;                         // per wave and stage (+1 on wave 0)
+  static constexpr int W_BYTES = BN * BK;
+  static constexpr int STAGE = (BN + BM) * BK;
+  static constexpr int SSLOT = 1024, SNS = 8;                // scale ring
+  static constexpr int NS0 = (kLdsBytes - SNS * SSLOT) / STAGE;
+  static constexpr int NS = NS0 > 4 ? 4 : NS0;               // operand ring
+  static constexpr int RING = NS * STAGE;
+  static constexpr int SMEM = RING + SNS * SSLOT;
+  static constexpr int OUT_LD = BN * 2 + 16;
+  static constexpr int OUT = BM * OUT_LD;
+  static_assert(OUT + BM * 4 + BN * 2 <= RING, "epilogue staging fits the ring");
+  static_assert(SMEM <= kLdsBytes, "LDS budget");
+  static_assert(NS >= 2 && (NS - 1) * (PS + 1) <= 63, "vmcnt range");
+};
+
+template <int V>
+using ic = std::integral_constant<int, V>;
+
+}  // namespace
+
+template <int BM, int GS, bool SWH>
+__global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
+  static_assert(GS == 64 || GS == 128, "group size");
+  using C = PgCfg<BM>;
+  constexpr int PG_BM = BM, PG_BN = C::BN, PG_BK = C::BK, PG_WM = C::WM, PG_WN = C::WN;
+  constexpr int PG_TM = C::TM, PG_TN = C::TN, PG_CH = C::CH, PG_RPI = C::RPI;
+  constexpr int PG_WI = C::WI, PG_XI = C::XI, PG_PS = C::PS, PG_W_BYTES = C::W_BYTES;
+  constexpr int PG_STAGE = C::STAGE, PG_NS = C::NS, PG_RING = C::RING, PG_SSLOT = C::SSLOT;
+  constexpr int PG_SNS = C::SNS, PG_SMEM = C::SMEM, PG_OUT_LD = C::OUT_LD, PG_OUT = C::OUT;
+  constexpr int SUBG = GS / 32;              // k sub-steps per group
+  constexpr int GPS = PG_BK / GS;            // groups per stage
+  constexpr int ESZ = SWH ? 2 : 4;           // scale element bytes
+  constexpr int CPR = PG_BN * ESZ / 16;      // 16-byte chunks per scale row
+  constexpr int ROWB = PG_BN * ESZ;          // bytes per scale row in LDS
+  constexpr int NMF = PG_TN * PG_TM;         // MFMAs per sub-step
+  constexpr int NR = PG_TN + PG_TM;          // fragment reads per sub-step
+  constexpr int NCOMBO = PG_TN * 4;          // (block a, quad q) scale combos
+  constexpr int CPS = NCOMBO / SUBG;         // combos flushed per sub-step
+  constexpr int EPS = CPS * PG_TM * 4;       // accumulators flushed per sub-step
+  static_assert(EPS % NMF == 0, "flush split");
+  static_assert(CPR * 16 * GPS <= PG_SSLOT && 64 / CPR >= GPS, "scale rows per stage");
+  __shared__ __attribute__((aligned(1024))) int8_t smem[PG_SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave & 1, wn = wave >> 1;
+  const int h = lane >> 5;
+  const int M = p.M, N = p.N, K = p.K;
+  const int G = K / GS;
+  const int nk = K / PG_BK;
+  int m0, n0;
+  tile_coords<PG_BM, PG_BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
+
+  const int8_t* wsrc[PG_WI];
+  const int8_t* xsrc[PG_XI];
+  {
+    const int rr = lane / PG_CH, slot = lane % PG_CH;
+    const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
+#pragma unroll
+    for (int i = 0; i < PG_WI; ++i) {
+      const int row = (wave * PG_WI + i) * PG_RPI + rr;
+      wsrc[i] = W + (int64_t)min(n0 + row, N - 1) * K + (slot ^ swz<PG_BK>(row)) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < PG_XI; ++i) {
+      const int row = (wave * PG_XI + i) * PG_RPI + rr;
+      xsrc[i] = p.x + (int64_t)min(m0 + row, M - 1) * K + (slot ^ swz<PG_BK>(row)) * 16;
+    }
+  }
+  // scale DMA (wave 0): lane l moves chunk l % CPR of row l / CPR of a stage's
+  // scale block; rows past the stage's groups (or past G) repeat a valid row
+  const int srow = lane / CPR;
+  const int8_t* ssrc =
+      reinterpret_cast<const int8_t*>(p.sw) +
+      (int64_t)min(n0 + (lane % CPR) * (16 / ESZ), N - 16 / ESZ) * ESZ;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem);
+
+  auto dma_stage = [&](int st, int slot) __attribute__((always_inline)) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
+    const int k0 = st * PG_BK;
+#pragma unroll
+    for (int i = 0; i < PG_WI; ++i) dma16(wsrc[i] + k0, sb + (wave * PG_WI + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < PG_XI; ++i)
+      dma16(xsrc[i] + k0, sb + PG_W_BYTES + (wave * PG_XI + i) * 1024);
+  };
+  auto dma_one = [&](int st, int slot, int d) __attribute__((always_inline)) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
+    const int k0 = st * PG_BK;
+    if (d < PG_WI)
+      dma16(wsrc[d < PG_WI ? d : 0] + k0, sb + (wave * PG_WI + d) * 1024);
+    else
+      dma16(xsrc[d >= PG_WI ? d - PG_WI : 0] + k0,
+            sb + PG_W_BYTES + (wave * PG_XI + d - PG_WI) * 1024);
+  };
+  auto dma_scales = [&](int st) __attribute__((always_inline)) {
+    const int g = min(st * GPS + srow, G - 1);
+    dma16(ssrc + (int64_t)g * N * ESZ, lds0 + PG_RING + (uint32_t)((st % PG_SNS) * PG_SSLOT));
+  };
+
+  const int frow = lane & 31;
+  const int fsw = swz<PG_BK>(lane & 15);
+  auto read_frag = [&](int slot, int j, int r, i32x4 (&wfn)[PG_TN], i32x4 (&xfn)[PG_TM])
+                       __attribute__((always_inline)) {
+    const int8_t* Ws = smem + slot * PG_STAGE;
+    const int fs = ((2 * j + h) ^ fsw) << 4;
+    if (r < PG_TN)
+      wfn[r < PG_TN ? r : 0] =
+          *reinterpret_cast<const i32x4*>(Ws + (wn * PG_WN + r * 32 + frow) * PG_BK + fs);
+    else
+      xfn[r >= PG_TN ? r - PG_TN : 0] = *reinterpret_cast<const i32x4*>(
+          Ws + PG_W_BYTES + (wm * PG_WM + (r - PG_TN) * 32 + frow) * PG_BK + fs);
+  };
+
+  // Group accumulator sets: the GPS groups of an even stage use sets
+  // 0 .. GPS-1, those of an odd stage GPS .. 2*GPS-1.  All groups of stage kt
+  // are flushed during stage kt+1, so every set is read a whole stage after
+  // its last MFMA.
+  constexpr int NSET = 2 * GPS;
+  constexpr int EPC = PG_TM * 4;        // accumulators per (a, q) combo
+  constexpr int CPSS = NCOMBO / 4;      // combos flushed per sub-step
+  constexpr int EPM = CPSS * EPC / NMF; // accumulators flushed after each MFMA
+  static_assert(CPSS * 4 == NCOMBO && (CPSS * EPC) % NMF == 0, "flush split");
+  i32x16 D[NSET][PG_TN][PG_TM];
+  float facc[PG_TN][PG_TM][16];
+#pragma unroll
+  for (int a = 0; a < PG_TN; ++a)
+#pragma unroll
+    for (int b = 0; b < PG_TM; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+#pragma unroll
+        for (int c = 0; c < NSET; ++c) D[c][a][b][r] = 0;
+        facc[a][b][r] = 0.0f;
+      }
+
+  // the 4 scales of combo (a, q) of group `row` of stage st:
+  // n = wn*64 + 32a + 8q + 4h + [0..3]
+  auto read_scales = [&](int st, int row, int combo, float (&sv)[4])
+                         __attribute__((always_inline)) {
+    const int8_t* base = smem + PG_RING + (st % PG_SNS) * PG_SSLOT + row * ROWB;
+    const int nl = wn * PG_WN + (combo / 4) * 32 + 8 * (combo % 4) + 4 * h;
+    if constexpr (SWH) {
+      const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
+      sv[0] = h2f((uint16_t)((uint32_t)v[0] & 0xffffu));
+      sv[1] = h2f((uint16_t)((uint32_t)v[0] >> 16));
+      sv[2] = h2f((uint16_t)((uint32_t)v[1] & 0xffffu));
+      sv[3] = h2f((uint16_t)((uint32_t)v[1] >> 16));
+    } else {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(base + nl * 4);
+      sv[0] = v[0];
+      sv[1] = v[1];
+      sv[2] = v[2];
+      sv[3] = v[3];
+    }
+  };
+
+  // One k sub-step in a fixed order (sched_barrier): the MFMAs into set CS
+  // (C = 0 when `first`), the next sub-step's fragment reads one per MFMA in
+  // consumption order (rd), this wave's DMA loads of stage dst into slot dsl
+  // (dma), and the flush of combos J*CPSS .. + CPSS of every group of stage
+  // fst from sets FS .. FS+GPS-1, groups in order (EPM accumulators after
+  // each MFMA; a combo's scales are read one MFMA ahead of its first use).
+  auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto FSc, auto Jc,
+                  const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs, int rj,
+                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int fst)
+                  __attribute__((always_inline)) {
+    constexpr int CS = decltype(CSc)::value, FS = decltype(FSc)::value, J = decltype(Jc)::value;
+    constexpr bool first = decltype(firstc)::value != 0;
+    constexpr bool rd = decltype(rdc)::value != 0;
+    constexpr bool dma = decltype(dmac)::value != 0;
+    float sv[CPSS][GPS][4];
+#pragma unroll
+    for (int g = 0; g < GPS; ++g) read_scales(fst, g, J * CPSS, sv[0][g]);
+#pragma unroll
+    for (int idx = 0; idx < NMF; ++idx) {
+#pragma unroll
+      for (int c = 1; c < CPSS; ++c)
+        if ((c * EPC / EPM > 0 ? c * EPC / EPM - 1 : 0) == idx) {
+#pragma unroll
+          for (int g = 0; g < GPS; ++g) read_scales(fst, g, J * CPSS + c, sv[c][g]);
+        }
+      const int a = idx / PG_TM, b = idx % PG_TM;
+      if constexpr (first)
+        D[CS][a][b] = mfma32(wc[a], xc[b], i32x16{});
+      else
+        D[CS][a][b] = mfma32(wc[a], xc[b], D[CS][a][b]);
+      if constexpr (rd) {
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx)
+            read_frag(rs, rj, q == 0 ? 0 : (q <= PG_TM ? PG_TN + q - 1 : q - PG_TM), wn_, xn);
+      }
+      if constexpr (dma) {
+#pragma unroll
+        for (int d = 0; d < PG_PS; ++d)
+          if (d * NMF / PG_PS == idx) dma_one(dst, dsl, d);
+        if (idx == 0 && wave == 0) dma_scales(dst);
+      }
+#pragma unroll
+      for (int e = idx * EPM; e < (idx + 1) * EPM; ++e) {
+        const int c = e / EPC, bb = (e / 4) % PG_TM, rr = e % 4;
+        const int combo = J * CPSS + c;
+        const int aa = combo / 4, r = 4 * (combo % 4) + rr;
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) {
+          const float t = (float)D[FS + g][aa][bb][r] * sv[c][g][rr];
+          facc[aa][bb][r] = facc[aa][bb][r] + t;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto wait_stage = [&]() __attribute__((always_inline)) {
+    if (wave == 0)
+      wait_vmcnt<(PG_NS - 2) * (PG_PS + 1)>();
+    else
+      wait_vmcnt<(PG_NS - 2) * PG_PS>();
+  };
+
+  i32x4 wf[2][PG_TN], xf[2][PG_TM];
+  // Prologue: stages 0 .. NS-1 (a stage past the end reloads stage nk-1 into
+  // a slot nobody reads, so every stage issue moves the same loads).
+#pragma unroll
+  for (int st = 0; st < PG_NS; ++st) {
+    dma_stage(min(st, nk - 1), st);
+    if (wave == 0) dma_scales(min(st, nk - 1));
+  }
+  if (wave == 0)
+    wait_vmcnt<(PG_NS - 1) * (PG_PS + 1)>();
+  else
+    wait_vmcnt<(PG_NS - 1) * PG_PS>();
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_frag(0, 0, r, wf[0], xf[0]);
+
+  float sa_t = 0.0f;
+  uint16_t b_t = 0;
+
+  // Stage kt at position HALF (0 or 1) of a 2-stage period that starts at an
+  // even kt, so set indices are compile-time.  It flushes stage kt-1 (at
+  // kt = 0: the zero sets of "stage -1" with stage 0's scales, adding +0.0).
+  // LAST: the final stage (no barrier or DMA; requests sa and bias; then
+  // flushes its own groups).
+  auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
+    constexpr int HALF = decltype(halfc)::value;
+    constexpr bool LAST = decltype(lastc)::value != 0;
+    constexpr int FS = (1 - HALF) * GPS;
+    const int sl = kt % PG_NS;
+    const int fst = max(kt - 1, 0);
+    if constexpr (LAST) {
+      sa_t = p.sa[min(m0 + tid % PG_BM, M - 1)];
+      if (p.bias) b_t = p.bias[min(n0 + tid % PG_BN, N - 1)];
+    }
+#define PG_SUB(J)                                                                            \
+  {                                                                                          \
+    constexpr int CS = HALF * GPS + (J) / SUBG;                                              \
+    if constexpr ((J) < 3) {                                                                 \
+      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<0>{}, ic<FS>{}, ic<(J)>{},        \
+           wf[(J) & 1], xf[(J) & 1], sl, (J) + 1, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0,  \
+           0, fst);                                                                          \
+    } else if constexpr (!LAST) {                                                            \
+      wait_stage();                                                                          \
+      __syncthreads();                                                                       \
+      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<1>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
+           xf[1], (kt + 1) % PG_NS, 0, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, fst);      \
+    } else {                                                                                 \
+      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<0>{}, ic<0>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
+           xf[1], 0, 0, wf[0], xf[0], 0, 0, fst);                                            \
+    }                                                                                        \
+  }
+    PG_SUB(0)
+    PG_SUB(1)
+    PG_SUB(2)
+    PG_SUB(3)
+#undef PG_SUB
+    if constexpr (LAST) {
+      // flush this stage's own groups, in order
+#pragma unroll
+      for (int combo = 0; combo < NCOMBO; ++combo) {
+        float sv[GPS][4];
+#pragma unroll
+        for (int g = 0; g < GPS; ++g) read_scales(kt, g, combo, sv[g]);
+        const int aa = combo / 4, q = combo % 4;
+#pragma unroll
+        for (int bb = 0; bb < PG_TM; ++bb)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int g = 0; g < GPS; ++g) {
+              const float t = (float)D[HALF * GPS + g][aa][bb][4 * q + rr] * sv[g][rr];
+              facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+            }
+      }
+    }
+  };
+
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    stage(kt, ic<0>{}, ic<0>{});
+    stage(kt + 1, ic<1>{}, ic<0>{});
+  }
+  if (kt + 1 < nk) {
+    stage(kt, ic<0>{}, ic<0>{});
+    stage(kt + 1, ic<1>{}, ic<1>{});
+  } else {
+    stage(kt, ic<0>{}, ic<1>{});
+  }
+  wait_vmcnt<0>();  // reloads past the end land before LDS is reused
+
+  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
+  float* ssa = reinterpret_cast<float*>(smem + PG_OUT);
+  uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + PG_BM);
+  __syncthreads();  // every wave is done with the ring
+  if (tid < PG_BM) ssa[tid] = sa_t;
+  if (tid < PG_BN) sbias[tid] = b_t;
+  __syncthreads();
+#pragma unroll
+  for (int a = 0; a < PG_TN; ++a) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = wn * PG_WN + a * 32 + 8 * q + 4 * h;
+      const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+      const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[0] >> 16)),
+                           h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[1] >> 16))};
+#pragma unroll
+      for (int b = 0; b < PG_TM; ++b) {
+        const int ml = wm * PG_WM + b * 32 + frow;
+        const float sam = ssa[ml];
+        uint16_t o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = facc[a][b][4 * q + r] * sam;
+          if (p.bias) v = v + bv[r];
+          o[r] = f2h(v);
+        }
+        *reinterpret_cast<i32x2*>(smem + ml * PG_OUT_LD + nl * 2) =
+            i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int LPR = PG_BN / 8, RPS = 64 / LPR;
+  const int cl = (lane % LPR) * 8;
+  const int n = n0 + cl;
+#pragma unroll 4
+  for (int rr = wave * RPS + lane / LPR; rr < PG_BM; rr += 4 * RPS) {
+    const int m = m0 + rr;
+    if (m < M && n < N)
+      *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
+          *reinterpret_cast<const i32x4*>(smem + rr * PG_OUT_LD + cl * 2);
+  }
+}
+
+// Eligible: int8 weights, per-group gs 64 / 128, K % 128 == 0, N % 8 == 0,
+// 16-byte aligned operands (launch_gemm checks).
+hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, hipStream_t s) {
+  constexpr int BM = 128;
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + 127) / 128);
+  if (gs == 64) {
+    if (sw_half)
+      gemm_dma_pg_kernel<BM, 64, true><<<tiles, 256, 0, s>>>(a);
+    else
+      gemm_dma_pg_kernel<BM, 64, false><<<tiles, 256, 0, s>>>(a);
+  } else {
+    if (sw_half)
+      gemm_dma_pg_kernel<BM, 128, true><<<tiles, 256, 0, s>>>(a);
+    else
+      gemm_dma_pg_kernel<BM, 128, false><<<tiles, 256, 0, s>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace cider

@@ -200,10 +200,14 @@ def test_full_size_down_proj_rows():
 # --------------------------------------------------------------------------
 
 
+# M > 64 with K % 128 == 0 and N % 8 == 0 runs the LDS-DMA per-group kernel
+# at gs = 128 (one k-stage (K=128), two (K=256), an odd count (K=384), ragged
+# M and N); gs 64 / 256 and K=320 run the register-staged kernel.
 @pytest.mark.parametrize("gs", [64, 128, 256])
 @pytest.mark.parametrize("M,N,K", [(1, 72, 512), (1, 10240, 2560), (5, 48, 256), (16, 130, 512),
                                    (64, 100, 1024), (65, 96, 512), (300, 520, 1024),
-                                   (130, 64, 320)])
+                                   (130, 64, 320), (128, 256, 128), (200, 1024, 256),
+                                   (257, 136, 384)])
 def test_pergroup_linear(gs, M, N, K):
     if K % gs:
         pytest.skip("K not a multiple of gs")
@@ -217,6 +221,19 @@ def test_pergroup_linear(gs, M, N, K):
         assert_bits_equal(y, exp, f"pg gs{gs} {M}x{N}x{K}")
     else:
         assert_f16_close(y, exp, what=f"pg gs{gs} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("M,N,K", [(1024, 10240, 2560), (512, 2560, 10240)])
+def test_pergroup_full_size_rows(gs, M, N, K):
+    x = O.synth_activations(M, K, 50 + gs)
+    w = O.synth_weights_i8(N, K, 51)
+    sw = O.synth_scales((K // gs, N), 52)
+    b = (np.random.default_rng(53).standard_normal(N) * 0.1).astype(np.float16)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    rows = np.r_[0:16, M - 16:M]
+    exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
+    assert_bits_equal(y[rows], exp, f"pg gs{gs} {M}x{N}x{K} rows")
 
 
 # --------------------------------------------------------------------------
