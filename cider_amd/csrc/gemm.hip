@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs p) {
 
 hipError_t launch_skinny(const GemmArgs& a, int wf, int epi, bool sw_half,
                          int gs, hipStream_t s);
-hipError_t launch_gemm_dma(const GemmArgs& a, int epi, hipStream_t s);
+hipError_t launch_gemm_dma(const GemmArgs& a, int epi, int wf, hipStream_t s);
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, hipStream_t s);
 
 namespace {
@@ -373,8 +373,8 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
                    (a.sw == nullptr || aligned16(a.sw));
-  if (wf == W_I8 && epi != EPI_PG && vec && a.K % 128 == 0 && a.N % 8 == 0)
-    return launch_gemm_dma(a, epi, s);  // LDS-DMA pipeline (gemm_dma.hip)
+  if (epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 && a.N % 8 == 0)
+    return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)
   // gs = 128 on the LDS-DMA per-group kernel; gs = 64 needs four group
   // accumulator sets there, which spill, so it stays on the register-staged
   // kernel (faster for it)

@@ -1,12 +1,15 @@
-// Tiled int8 GEMM, main path for int8 weights with K % 128 == 0 and N % 8 == 0:
-// operands stream global -> LDS by gfx950's 16-byte LDS-DMA loads through a
-// ring of k-stages, the MFMAs are v_mfma_i32_32x32x32_i8, and the fp16 tile
-// is staged through LDS so the output is written in whole rows.
+// Tiled int8 GEMM, main path for int8 weights (int32 and per-channel
+// epilogues) and int4 weights (per-channel, the reference W4A8) with
+// K % 128 == 0 and N % 8 == 0: operands stream global -> LDS by gfx950's
+// 16-byte LDS-DMA loads through a ring of k-stages, the MFMAs are
+// v_mfma_i32_32x32x32_i8, and the fp16 tile is staged through LDS so the
+// output is written in whole rows.
 //
 // Reference semantics are those of gemm.hip (same epilogues, same fp32
 // operation order, bit-identical results):
 //   EPI_I32 cider/kernels/w8a8_matmul.metal:301-453
 //   EPI_PC  cider/kernels/w8a8_matmul.metal:63-81
+//   int4    cider/kernels/w4a8_matmul.metal:47-89,189-246 (no bias)
 // (Per-group stays on the register-staged kernel: its in-loop scale loads
 // would make the compiler wait for every LDS-DMA load in flight.)
 //
@@ -48,25 +51,37 @@
 //     accumulators to fp16 into a BM x BN LDS tile (rows padded by 16 bytes),
 //     then the workgroup stores whole 2*BN-byte rows with 16-byte lanes, so
 //     HBM sees full 128-byte lines instead of 32-byte row fragments.
+//   * int4 weights: a k-stage of a weight row is 64 bytes of nibbles (the ring
+//     then holds 3 stages at 256 x 256).  One ds_read_b128 per W block brings
+//     the 32 nibbles of a pair of sub-steps; each sub-step's 16 are unpacked
+//     to int8 in registers (sign extension by xor/sub, byte permute) one
+//     sub-step ahead of their MFMAs.  The k mapping of a pair puts lane half h
+//     on k 64p + 32h + [0, 32), identically for both operands, so the int32
+//     dot products are exact.
 //   * Rows past M or N are loaded from the last valid row (their results are
 //     never stored); K % 128 == 0 is required, so there is no K tail.
 #include "common.hpp"
 #include "dma_common.hpp"
 #include "kernels.hpp"
 
+#include <type_traits>
+
 namespace cider {
 
 namespace {
 
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int WF = W_I8>
 struct DmaCfg {
-  static constexpr int CH = BK / 16;                // 16-byte chunks per LDS row
-  static constexpr int RPI = 1024 / BK;             // rows per DMA instruction
-  static constexpr int WI = BN / RPI / 4, XI = BM / RPI / 4;  // per wave
+  static constexpr int CH = BK / 16;                // 16-byte chunks per X row
+  static constexpr int RPI = 1024 / BK;             // X rows per DMA instruction
+  static constexpr int WB = (WF == W_I4) ? BK / 2 : BK;  // weight bytes per row and stage
+  static constexpr int CHW = WB / 16;               // 16-byte chunks per W row
+  static constexpr int RPIW = 1024 / WB;            // W rows per DMA instruction
+  static constexpr int WI = BN / RPIW / 4, XI = BM / RPI / 4;  // per wave
   static constexpr int PS = WI + XI;                // vmcnt units per stage
   static constexpr int SUBS = BK / 32;              // MFMA k sub-steps per stage
-  static constexpr int W_BYTES = BN * BK, X_BYTES = BM * BK, STAGE = W_BYTES + X_BYTES;
+  static constexpr int W_BYTES = BN * WB, X_BYTES = BM * BK, STAGE = W_BYTES + X_BYTES;
   static constexpr int NS0 = kLdsBytes / STAGE;
   static constexpr int NS = NS0 > 8 ? 8 : NS0;      // ring slots
   static constexpr int RING = NS * STAGE;
@@ -78,47 +93,65 @@ struct DmaCfg {
   static_assert(WI >= 1 && XI >= 1, "tile too small for the DMA split");
   static_assert(NS >= 2, "ring needs two slots");
   static_assert(SMEM <= kLdsBytes, "LDS budget");
-  static_assert((NS - 2) * PS <= 63, "vmcnt range");
+  static_assert((NS - 2) * PS <= 63 && (NS - 1) * PS <= 63, "vmcnt range");
 };
+
+// 8 bytes of packed int4 (element 2i in the low nibble of byte i) -> 16 int8
+// in element order.
+__device__ __forceinline__ i32x4 unpack_w4_8(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  unpack_w4_word(w0, a, b);
+  unpack_w4_word(w1, c, d);
+  return i32x4{(int)a, (int)b, (int)c, (int)d};
+}
+
+template <int V>
+using icst = std::integral_constant<int, V>;
 
 }  // namespace
 
 // One BM x BN output tile over the whole K.  smem: DmaCfg::SMEM bytes of LDS.
-template <int BM, int BN, int BK, int EPI>
+// WF = W_I8: weights int8 [N, K]; W_I4: packed int4 [N, K/2] (element k in
+// byte k/2, low nibble first, two's complement), unpacked in registers.
+template <int BM, int BN, int BK, int EPI, int WF = W_I8>
 __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const int n0,
                                          int8_t* __restrict__ smem) {
   static_assert((BM == 64 || BM == 128 || BM == 256) && (BN == 64 || BN == 128 || BN == 256),
                 "tile shape");
   static_assert(BK == 64 || BK == 128, "k stage");
-  using C = DmaCfg<BM, BN, BK>;
+  static_assert(WF == W_I8 || BK == 128, "int4 weights use 128-byte k-stages");
+  using C = DmaCfg<BM, BN, BK, WF>;
+  constexpr bool W4 = (WF == W_I4);
   constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
   constexpr int WI = C::WI, XI = C::XI, PS = C::PS, NS = C::NS, SUBS = C::SUBS;
   constexpr int W_BYTES = C::W_BYTES, STAGE = C::STAGE, CH = C::CH, RPI = C::RPI;
+  constexpr int WB = C::WB, CHW = C::CHW, RPIW = C::RPIW;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
   const int M = p.M, N = p.N, K = p.K;
+  const int h = lane >> 5;
 
-  // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*RPI ..
-  // + RPI; lane l writes row R0 + l / CH, slot l % CH, which holds global
-  // chunk slot ^ swz(row).
+  // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*RPIW ..
+  // + RPIW (X: RPI); lane l writes row R0 + l / CHW, slot l % CHW, which holds
+  // global chunk slot ^ swz(row).
   const int8_t* wsrc[WI];
   const int8_t* xsrc[XI];
   {
-    const int rr = lane / CH, slot = lane % CH;
     const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
+    const int64_t ldw = W4 ? (K >> 1) : K;
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
-      const int row = (wave * WI + i) * RPI + rr;
+      const int row = (wave * WI + i) * RPIW + lane / CHW;
       const int n = min(n0 + row, N - 1);
-      wsrc[i] = W + (int64_t)n * K + (slot ^ swz<BK>(row)) * 16;
+      wsrc[i] = W + (int64_t)n * ldw + ((lane % CHW) ^ swz<WB>(row)) * 16;
     }
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
-      const int row = (wave * XI + i) * RPI + rr;
+      const int row = (wave * XI + i) * RPI + lane / CH;
       const int m = min(m0 + row, M - 1);
-      xsrc[i] = p.x + (int64_t)m * K + (slot ^ swz<BK>(row)) * 16;
+      xsrc[i] = p.x + (int64_t)m * K + ((lane % CH) ^ swz<BK>(row)) * 16;
     }
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
@@ -127,27 +160,37 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   // `slot`: W rows first, then X rows.
   auto dma_one = [&](int st, int slot, int d) {
     const uint32_t sb = lds0 + (uint32_t)(slot * STAGE);
-    const int k0 = st * BK;
     if (d < WI)
-      dma16(wsrc[d < WI ? d : 0] + k0, sb + (wave * WI + d) * 1024);
+      dma16(wsrc[d < WI ? d : 0] + st * WB, sb + (wave * WI + d) * 1024);
     else
-      dma16(xsrc[d >= WI ? d - WI : 0] + k0, sb + W_BYTES + (wave * XI + d - WI) * 1024);
+      dma16(xsrc[d >= WI ? d - WI : 0] + st * BK,
+            sb + W_BYTES + (wave * XI + d - WI) * 1024);
   };
 
-  // fragment r (W blocks 0..TN-1, then X blocks) of k sub-step j in ring
-  // slot `slot`: lane l reads row l % 32 of the 32-row block, chunk
-  // 2j + l / 32 (the same k mapping for both operands)
+  // k mapping of sub-step j for lane half h (the same for both operands):
+  //   int8 weights: k in [32 j + 16 h, + 16)               (X chunk 2j + h)
+  //   int4 weights: k in [64 (j/2) + 32 h + 16 (j%2), + 16) (X chunk
+  //     4 (j/2) + 2h + j%2; W4 chunk 2 (j/2) + h holds the pair's 32 nibbles,
+  //     read once per pair, half j%2 unpacked per sub-step)
   const int frow = lane & 31;
-  const int fsw = swz<BK>(lane & 15);
-  auto read_frag = [&](int slot, int j, int r, i32x4 (&wfn)[TN], i32x4 (&xfn)[TM]) {
+  auto x_chunk = [&](int j) { return W4 ? 4 * (j / 2) + 2 * h + (j % 2) : 2 * j + h; };
+  auto read_x = [&](int slot, int j, int b, i32x4 (&xfn)[TM]) {
+    const int8_t* Xs = smem + slot * STAGE + W_BYTES;
+    const int row = wm * WM + b * 32 + frow;
+    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + ((x_chunk(j) ^ swz<BK>(row)) << 4));
+  };
+  // int8: fragment of W block a for sub-step j;  int4: the raw 16-byte chunk
+  // of W block a for the sub-step pair j / 2
+  auto read_w = [&](int slot, int j, int a, i32x4 (&dst)[TN]) {
     const int8_t* Ws = smem + slot * STAGE;
-    const int fs = ((2 * j + (lane >> 5)) ^ fsw) << 4;
-    if (r < TN)
-      wfn[r < TN ? r : 0] =
-          *reinterpret_cast<const i32x4*>(Ws + (wn * WN + r * 32 + frow) * BK + fs);
-    else
-      xfn[r >= TN ? r - TN : 0] = *reinterpret_cast<const i32x4*>(
-          Ws + W_BYTES + (wm * WM + (r - TN) * 32 + frow) * BK + fs);
+    const int row = wn * WN + a * 32 + frow;
+    const int c = W4 ? 2 * (j / 2) + h : 2 * j + h;
+    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * WB + ((c ^ swz<WB>(row)) << 4));
+  };
+  i32x4 raw[TN];  // int4 only: packed chunks of the current sub-step pair
+  auto unpack_half = [&](int a, int half, i32x4 (&dst)[TN]) {
+    dst[a] = half == 0 ? unpack_w4_8((uint32_t)raw[a][0], (uint32_t)raw[a][1])
+                       : unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
   };
 
   i32x16 acc[TN][TM];
@@ -158,28 +201,55 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
 
-  // One k sub-step: the TN*TM MFMAs on fragments (wc, xc).  Between them, in
-  // a fixed order (sched_barrier), go the reads of the next sub-step's
-  // fragments (slot rs, sub-step rj) into (wn_, xn) when rd, and this wave's
-  // DMA loads of stage dst into slot dsl when dma.  Each read is issued at
-  // least TN*TM - TN - TM MFMAs before its use, so no MFMA waits on LDS, and
-  // the DMA issue overlaps MFMAs instead of following the barrier on its own.
-  auto step = [&](const i32x4 (&wc)[TN], const i32x4 (&xc)[TM], bool rd, int rs, int rj,
-                  i32x4 (&wn_)[TN], i32x4 (&xn)[TM], bool dma, int dst, int dsl) {
+  // One k sub-step in a fixed instruction order (sched_barrier): the TN*TM
+  // MFMAs on fragments (wc, xc); between them the operands of the next
+  // sub-step JN (from slot rs) when rd, and this wave's DMA loads of stage dst
+  // into slot dsl when dma.  int8: the next fragments are read one per MFMA
+  // in the order they will be consumed (W0, X0 .. X(TM-1), W1 ..), each at
+  // least TN*TM - TN - TM MFMAs before its use.  int4: the X fragments are
+  // read first; when JN starts a new pair the raw W chunks are read next and
+  // unpacked in the last TN MFMA slots, otherwise the second half of the
+  // chunks already held is unpacked.  Left to itself the compiler regroups
+  // the reads next to the MFMAs that consume them and exposes LDS latency.
+  auto step = [&](auto JNc, auto rdc, auto dmac, const i32x4 (&wc)[TN], const i32x4 (&xc)[TM],
+                  int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst, int dsl) {
+    constexpr int JN = decltype(JNc)::value;
+    constexpr bool rd = decltype(rdc)::value != 0, dma = decltype(dmac)::value != 0;
     constexpr int NMF = TN * TM, NR = TN + TM;
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
       acc[idx / TM][idx % TM] = mfma32(wc[idx / TM], xc[idx % TM], acc[idx / TM][idx % TM]);
-      // reads go one per MFMA from the first (the rest after the last MFMA
-      // when there are more reads than MFMAs), in the order the next sub-step
-      // consumes them: W0, X0 .. X(TM-1), W1 .. W(TN-1)
-      if (rd) {
+      if constexpr (rd && !W4) {
 #pragma unroll
         for (int q = 0; q < NR; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx)
-            read_frag(rs, rj, q == 0 ? 0 : (q <= TM ? TN + q - 1 : q - TM), wn_, xn);
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q == 0)
+              read_w(rs, JN, 0, wn_);
+            else if (q <= TM)
+              read_x(rs, JN, q - 1, xn);
+            else
+              read_w(rs, JN, q - TM, wn_);
+          }
       }
-      if (dma) {
+      if constexpr (rd && W4) {
+        constexpr bool new_pair = (JN % 2) == 0;
+        constexpr int NRD = TM + (new_pair ? TN : 0);
+#pragma unroll
+        for (int q = 0; q < NRD; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q < TM)
+              read_x(rs, JN, q, xn);
+            else
+              read_w(rs, JN, q - TM, raw);
+          }
+#pragma unroll
+        for (int a = 0; a < TN; ++a) {
+          constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
+          if ((first_slot + a < NMF ? first_slot + a : NMF - 1) == idx)
+            unpack_half(a, JN % 2, wn_);
+        }
+      }
+      if constexpr (dma) {
 #pragma unroll
         for (int d = 0; d < PS; ++d)
           if (d * NMF / PS == idx) dma_one(dst, dsl, d);
@@ -201,21 +271,44 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   wait_vmcnt<(NS - 1) * PS>();  // stage 0 landed (loads complete in order)
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < TN + TM; ++r) read_frag(0, 0, r, wf[0], xf[0]);
+  for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
+#pragma unroll
+  for (int a = 0; a < TN; ++a) {
+    if constexpr (W4) {
+      read_w(0, 0, a, raw);
+      unpack_half(a, 0, wf[0]);
+    } else {
+      read_w(0, 0, a, wf[0]);
+    }
+  }
 
   // Stage kt: sub-steps 0 .. SUBS-1.  The barrier before the last sub-step
   // publishes stage kt+1 (NS-2 younger stages still in flight) and frees the
   // slot of stage kt, which receives stage kt+NS during that sub-step.
-  for (int kt = 0; kt < nk - 1; ++kt) {
-    const int sl = kt % NS, sl1 = (kt + 1) % NS;
-#pragma unroll
-    for (int j = 0; j < SUBS - 1; ++j)
-      step(wf[j & 1], xf[j & 1], true, sl, j + 1, wf[(j + 1) & 1], xf[(j + 1) & 1], false, 0, 0);
-    wait_vmcnt<(NS - 2) * PS>();
-    __syncthreads();
-    step(wf[(SUBS - 1) & 1], xf[(SUBS - 1) & 1], true, sl1, 0, wf[0], xf[0], true,
-         min(kt + NS, nk - 1), sl);
+  auto stage_body = [&](int kt, auto lastc) {
+    constexpr bool LAST = decltype(lastc)::value != 0;
+    const int sl = kt % NS;
+#define DMA_SUB(J)                                                                          \
+  if constexpr ((J) < SUBS - 1) {                                                           \
+    step(icst<(J) + 1>{}, icst<1>{}, icst<0>{}, wf[(J) & 1], xf[(J) & 1], sl,               \
+         wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0);                                       \
+  } else if constexpr (!LAST) {                                                             \
+    wait_vmcnt<(NS - 2) * PS>();                                                            \
+    __syncthreads();                                                                        \
+    step(icst<0>{}, icst<1>{}, icst<1>{}, wf[(J) & 1], xf[(J) & 1], (kt + 1) % NS, wf[0],   \
+         xf[0], min(kt + NS, nk - 1), sl);                                                  \
+  } else {                                                                                  \
+    step(icst<0>{}, icst<0>{}, icst<0>{}, wf[(J) & 1], xf[(J) & 1], 0, wf[0], xf[0], 0, 0); \
   }
+    DMA_SUB(0)
+    DMA_SUB(1)
+    if constexpr (SUBS == 4) {
+      DMA_SUB(2)
+      DMA_SUB(3)
+    }
+#undef DMA_SUB
+  };
+  for (int kt = 0; kt < nk - 1; ++kt) stage_body(kt, icst<0>{});
   // Last stage.  The per-channel epilogue's scales are requested here, so
   // their latency hides behind the last MFMAs; indices are clamped, so the
   // loads are unconditional.
@@ -226,18 +319,11 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     sa_t = p.sa[min(m0 + tid % BM, M - 1)];
     if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
   }
-  {
-    const int sl = (nk - 1) % NS;
-#pragma unroll
-    for (int j = 0; j < SUBS - 1; ++j)
-      step(wf[j & 1], xf[j & 1], true, sl, j + 1, wf[(j + 1) & 1], xf[(j + 1) & 1], false, 0, 0);
-    step(wf[(SUBS - 1) & 1], xf[(SUBS - 1) & 1], false, 0, 0, wf[0], xf[0], false, 0, 0);
-  }
+  stage_body(nk - 1, icst<1>{});
   wait_vmcnt<0>();  // the reloads past the end land before LDS is reused
 
   // ---- epilogue: lane holds, per 32x32 block and group g, 4 consecutive n
   //      n = nblk + 8g + 4 (lane / 32) + [0..3] of row m = mblk + lane % 32
-  const int h = lane >> 5;
   if constexpr (EPI == EPI_I32) {
 #pragma unroll
     for (int b = 0; b < TM; ++b) {
@@ -312,12 +398,12 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 }
 
 // Uniform grid: one BM x BN tile per workgroup.
-template <int BM, int BN, int BK, int EPI>
+template <int BM, int BN, int BK, int EPI, int WF>
 __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
-  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK>::SMEM];
+  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK, WF>::SMEM];
   int m0, n0;
   tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), p.M, 0, p.N, m0, n0);
-  dma_tile<BM, BN, BK, EPI>(p, m0, n0, smem);
+  dma_tile<BM, BN, BK, EPI, WF>(p, m0, n0, smem);
 }
 
 // Two tile sizes in one grid, so that the last round of workgroups is not
@@ -325,32 +411,32 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
 // [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
 // many tiles of half the work.  Workgroups start in index order, so the small
 // tiles form the last round; each region has its own XCD remap.
-template <int EPI>
+template <int EPI, int WF>
 __global__ __launch_bounds__(256, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
                                                                 int nsplit) {
-  constexpr int S1 = DmaCfg<256, 256, 128>::SMEM, S2 = DmaCfg<128, 256, 128>::SMEM;
+  constexpr int S1 = DmaCfg<256, 256, 128, WF>::SMEM, S2 = DmaCfg<128, 256, 128, WF>::SMEM;
   __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
   const int b = blockIdx.x;
   int m0, n0;
   if (b < nbig) {
     tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
-    dma_tile<256, 256, 128, EPI>(p, m0, n0, smem);
+    dma_tile<256, 256, 128, EPI, WF>(p, m0, n0, smem);
   } else {
     tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
-    dma_tile<128, 256, 128, EPI>(p, m0, n0, smem);
+    dma_tile<128, 256, 128, EPI, WF>(p, m0, n0, smem);
   }
 }
 
 namespace {
 
-template <int BM, int BN, int BK, int EPI>
+template <int BM, int BN, int BK, int EPI, int WF = W_I8>
 hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  gemm_dma_kernel<BM, BN, BK, EPI><<<tiles, 256, 0, s>>>(a);
+  gemm_dma_kernel<BM, BN, BK, EPI, WF><<<tiles, 256, 0, s>>>(a);
   return hipGetLastError();
 }
 
-template <int EPI>
+template <int EPI, int WF>
 hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
   const int cus = num_cus();
   // 256 x 256 tiles whose last round is at most half full and made of whole
@@ -365,7 +451,7 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
       const int nsplit = (tn - tail_cols) * 256;
       const int nbig = (int)(T - R);
       const int nsmall = ((a.M + 127) / 128) * tail_cols;
-      gemm_dma_mixed_kernel<EPI><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
+      gemm_dma_mixed_kernel<EPI, WF><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
       return hipGetLastError();
     }
   }
@@ -387,11 +473,11 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
     }
   }
   switch (best) {
-    case 0: return run_dma<256, 256, 128, EPI>(a, s);
-    case 1: return run_dma<128, 256, 128, EPI>(a, s);
-    case 2: return run_dma<128, 128, 128, EPI>(a, s);
-    case 3: return run_dma<64, 128, 128, EPI>(a, s);
-    default: return run_dma<64, 64, 128, EPI>(a, s);
+    case 0: return run_dma<256, 256, 128, EPI, WF>(a, s);
+    case 1: return run_dma<128, 256, 128, EPI, WF>(a, s);
+    case 2: return run_dma<128, 128, 128, EPI, WF>(a, s);
+    case 3: return run_dma<64, 128, 128, EPI, WF>(a, s);
+    default: return run_dma<64, 64, 128, EPI, WF>(a, s);
   }
 }
 
@@ -412,11 +498,12 @@ int num_cus() {
   return cache[dev];
 }
 
-// Eligible: int8 weights, EPI_I32 or EPI_PC, K % 128 == 0, N % 8 == 0,
-// 16-byte aligned operands.
-hipError_t launch_gemm_dma(const GemmArgs& a, int epi, hipStream_t s) {
-  if (epi == EPI_I32) return pick_tile<EPI_I32>(a, s);
-  return pick_tile<EPI_PC>(a, s);
+// Eligible: EPI_I32 or EPI_PC with int8 weights, EPI_PC with int4 weights;
+// K % 128 == 0, N % 8 == 0, 16-byte aligned operands (launch_gemm checks).
+hipError_t launch_gemm_dma(const GemmArgs& a, int epi, int wf, hipStream_t s) {
+  if (wf == W_I4) return pick_tile<EPI_PC, W_I4>(a, s);
+  if (epi == EPI_I32) return pick_tile<EPI_I32, W_I8>(a, s);
+  return pick_tile<EPI_PC, W_I8>(a, s);
 }
 
 }  // namespace cider

@@ -250,15 +250,29 @@ def test_w4_repack_matches_unpack():
         np.testing.assert_array_equal(O.unpack_w4_lo_first(dst), O.unpack_w4_ref(src).T)
 
 
+# M > 64, K % 128 == 0, N % 8 == 0 runs the LDS-DMA kernel with int4 weights
+# (512x640, 256x1024, 300x136 with an odd stage count, 2048x10240 on the mixed
+# grid); N % 8 != 0 the register-staged kernel; M <= 64 the skinny kernel.
 @pytest.mark.parametrize("M,N,K", [(1, 32, 64), (9, 70, 160), (1, 12288, 4096),
                                    (16, 4096, 12288), (64, 300, 1024), (100, 300, 1024),
-                                   (512, 640, 2048), (7, 33, 98)])
+                                   (512, 640, 2048), (7, 33, 98), (256, 1024, 512),
+                                   (300, 136, 384), (2048, 10240, 256)])
 def test_w4a8_linear_ref_layout(M, N, K):
     x = O.synth_activations(M, K, 60 + M)
     wf = np.random.default_rng(61 + N).standard_normal((K, N)).astype(np.float32)
     packed, sw = O.pack_weight_int4(wf)
     y = H(C.w4a8_linear(T(x), T(packed), T(sw)))
     assert_bits_equal(y, O.w4a8_linear(x, packed, sw), f"w4 {M}x{N}x{K}")
+
+
+def test_w4a8_full_size_rows():
+    M, N, K = 4096, 12288, 4096
+    x = O.synth_activations(M, K, 62)
+    wf = np.random.default_rng(63).standard_normal((K, N)).astype(np.float32)
+    packed, sw = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw)))
+    rows = np.r_[0:16, M - 16:M]
+    assert_bits_equal(y[rows], O.w4a8_linear(x[rows], packed, sw), "w4 full-size rows")
 
 
 @pytest.mark.parametrize("gs", [64, 128])
