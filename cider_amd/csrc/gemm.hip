@@ -349,7 +349,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs p) {
 hipError_t launch_skinny(const GemmArgs& a, int wf, int epi, bool sw_half,
                          int gs, hipStream_t s);
 hipError_t launch_gemm_dma(const GemmArgs& a, int epi, int wf, hipStream_t s);
-hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, hipStream_t s);
+hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s);
 
 namespace {
 
@@ -378,8 +378,8 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
   // gs = 128 on the LDS-DMA per-group kernel; gs = 64 needs four group
   // accumulator sets there, which spill, so it stays on the register-staged
   // kernel (faster for it)
-  if (wf == W_I8 && epi == EPI_PG && gs == 128 && vec && a.K % 128 == 0 && a.N % 8 == 0)
-    return launch_gemm_dma_pg(a, gs, sw_half, s);  // gemm_dma_pg.hip
+  if (epi == EPI_PG && gs == 128 && vec && a.K % 128 == 0 && a.N % 8 == 0)
+    return launch_gemm_dma_pg(a, gs, sw_half, wf, s);  // gemm_dma_pg.hip
   if (epi == EPI_I32) return run_tiled<256, 256, W_I8, EPI_I32, false, 0>(a, vec, s);
   if (epi == EPI_PC) {
     if (wf == W_I4) return run_tiled<256, 256, W_I4, EPI_PC, false, 0>(a, vec, s);

@@ -42,38 +42,59 @@ namespace cider {
 
 namespace {
 
-// Geometry of a BM x 128 tile (BM = 256 or 128), 4 waves of (BM / 2) x 64.
-template <int BM>
+// Geometry of a BM x BN tile, 4 waves of (BM / 2) x (BN / 2); int8 or packed
+// int4 weights (WF); OCC workgroups per CU share the LDS.
+template <int BM, int BN_, int WF, int OCC>
 struct PgCfg {
-  static constexpr int BN = 128, BK = 128;
-  static constexpr int WM = BM / 2, WN = 64, TM = WM / 32, TN = 2;
-  static constexpr int CH = BK / 16, RPI = 1024 / BK;        // 8, 8
-  static constexpr int WI = BN / RPI / 4;                    // DMA instructions (W rows)
+  static constexpr int BN = BN_, BK = 128;
+  static constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  static constexpr int CH = BK / 16, RPI = 1024 / BK;        // X: 8 chunks, 8 rows per DMA
+  static constexpr int WB = (WF == W_I4) ? BK / 2 : BK;      // weight bytes per row and stage
+  static constexpr int CHW = WB / 16, RPIW = 1024 / WB;
+  static constexpr int WI = BN / RPIW / 4;                   // DMA instructions (W rows)
   static constexpr int XI = BM / RPI / 4;                    // DMA instructions (X rows)
   static constexpr int PS = WI + XI;                         // per wave and stage (+1 on wave 0)
-  static constexpr int W_BYTES = BN * BK;
-  static constexpr int STAGE = (BN + BM) * BK;
+  static constexpr int W_BYTES = BN * WB;
+  static constexpr int STAGE = W_BYTES + BM * BK;
   static constexpr int SSLOT = 1024, SNS = 8;                // scale ring
-  static constexpr int NS0 = (kLdsBytes - SNS * SSLOT) / STAGE;
+  static constexpr int LDS = kLdsBytes / OCC;
+  static constexpr int NS0 = (LDS - SNS * SSLOT) / STAGE;
   static constexpr int NS = NS0 > 4 ? 4 : NS0;               // operand ring
   static constexpr int RING = NS * STAGE;
   static constexpr int SMEM = RING + SNS * SSLOT;
   static constexpr int OUT_LD = BN * 2 + 16;
   static constexpr int OUT = BM * OUT_LD;
+  static_assert(WI >= 1 && XI >= 1 && TN >= 1, "tile too small for the DMA split");
   static_assert(OUT + BM * 4 + BN * 2 <= RING, "epilogue staging fits the ring");
-  static_assert(SMEM <= kLdsBytes, "LDS budget");
+  static_assert(SMEM <= LDS, "LDS budget");
   static_assert(NS >= 2 && (NS - 1) * (PS + 1) <= 63, "vmcnt range");
 };
+
+// 8 bytes of packed int4 (element 2i in the low nibble of byte i) -> 16 int8
+// in element order.
+__device__ __forceinline__ i32x4 pg_unpack_w4_8(uint32_t w0, uint32_t w1) {
+  uint32_t a, b, c, d;
+  unpack_w4_word(w0, a, b);
+  unpack_w4_word(w1, c, d);
+  return i32x4{(int)a, (int)b, (int)c, (int)d};
+}
 
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// Dispatched tile: 128 x 64 with two workgroups per CU (each workgroup's
+// waits hide behind the other's VALU flush; the int32 group sets then fit in
+// VGPRs, so the flush reads them without v_accvgpr_read).
+constexpr int PG_LAUNCH_BN = 64, PG_LAUNCH_OCC = 2;
+
 }  // namespace
 
-template <int BM, int GS, bool SWH>
-__global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
+template <int BM, int BN, int GS, bool SWH, int WF, int OCC>
+__global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128, "group size");
-  using C = PgCfg<BM>;
+  using C = PgCfg<BM, BN, WF, OCC>;
+  constexpr bool W4 = (WF == W_I4);
+  constexpr int WB = C::WB, CHW = C::CHW, RPIW = C::RPIW;
   constexpr int PG_BM = BM, PG_BN = C::BN, PG_BK = C::BK, PG_WM = C::WM, PG_WN = C::WN;
   constexpr int PG_TM = C::TM, PG_TN = C::TN, PG_CH = C::CH, PG_RPI = C::RPI;
   constexpr int PG_WI = C::WI, PG_XI = C::XI, PG_PS = C::PS, PG_W_BYTES = C::W_BYTES;
@@ -91,6 +112,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
   constexpr int EPS = CPS * PG_TM * 4;       // accumulators flushed per sub-step
   static_assert(EPS % NMF == 0, "flush split");
   static_assert(CPR * 16 * GPS <= PG_SSLOT && 64 / CPR >= GPS, "scale rows per stage");
+  static_assert(NCOMBO % 4 == 0, "whole combos per sub-step");
   __shared__ __attribute__((aligned(1024))) int8_t smem[PG_SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -106,17 +128,17 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
   const int8_t* wsrc[PG_WI];
   const int8_t* xsrc[PG_XI];
   {
-    const int rr = lane / PG_CH, slot = lane % PG_CH;
     const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
+    const int64_t ldw = W4 ? (K >> 1) : K;
 #pragma unroll
     for (int i = 0; i < PG_WI; ++i) {
-      const int row = (wave * PG_WI + i) * PG_RPI + rr;
-      wsrc[i] = W + (int64_t)min(n0 + row, N - 1) * K + (slot ^ swz<PG_BK>(row)) * 16;
+      const int row = (wave * PG_WI + i) * RPIW + lane / CHW;
+      wsrc[i] = W + (int64_t)min(n0 + row, N - 1) * ldw + ((lane % CHW) ^ swz<WB>(row)) * 16;
     }
 #pragma unroll
     for (int i = 0; i < PG_XI; ++i) {
-      const int row = (wave * PG_XI + i) * PG_RPI + rr;
-      xsrc[i] = p.x + (int64_t)min(m0 + row, M - 1) * K + (slot ^ swz<PG_BK>(row)) * 16;
+      const int row = (wave * PG_XI + i) * PG_RPI + lane / PG_CH;
+      xsrc[i] = p.x + (int64_t)min(m0 + row, M - 1) * K + ((lane % PG_CH) ^ swz<PG_BK>(row)) * 16;
     }
   }
   // scale DMA (wave 0): lane l moves chunk l % CPR of row l / CPR of a stage's
@@ -130,20 +152,18 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
 
   auto dma_stage = [&](int st, int slot) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
-    const int k0 = st * PG_BK;
 #pragma unroll
-    for (int i = 0; i < PG_WI; ++i) dma16(wsrc[i] + k0, sb + (wave * PG_WI + i) * 1024);
+    for (int i = 0; i < PG_WI; ++i) dma16(wsrc[i] + st * WB, sb + (wave * PG_WI + i) * 1024);
 #pragma unroll
     for (int i = 0; i < PG_XI; ++i)
-      dma16(xsrc[i] + k0, sb + PG_W_BYTES + (wave * PG_XI + i) * 1024);
+      dma16(xsrc[i] + st * PG_BK, sb + PG_W_BYTES + (wave * PG_XI + i) * 1024);
   };
   auto dma_one = [&](int st, int slot, int d) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
-    const int k0 = st * PG_BK;
     if (d < PG_WI)
-      dma16(wsrc[d < PG_WI ? d : 0] + k0, sb + (wave * PG_WI + d) * 1024);
+      dma16(wsrc[d < PG_WI ? d : 0] + st * WB, sb + (wave * PG_WI + d) * 1024);
     else
-      dma16(xsrc[d >= PG_WI ? d - PG_WI : 0] + k0,
+      dma16(xsrc[d >= PG_WI ? d - PG_WI : 0] + st * PG_BK,
             sb + PG_W_BYTES + (wave * PG_XI + d - PG_WI) * 1024);
   };
   auto dma_scales = [&](int st) __attribute__((always_inline)) {
@@ -151,18 +171,28 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
     dma16(ssrc + (int64_t)g * N * ESZ, lds0 + PG_RING + (uint32_t)((st % PG_SNS) * PG_SSLOT));
   };
 
+  // k mapping of sub-step j for lane half h (the same for both operands):
+  //   int8 weights: k in [32 j + 16 h, + 16)               (X chunk 2j + h)
+  //   int4 weights: k in [64 (j/2) + 32 h + 16 (j%2), + 16) (X chunk
+  //     4 (j/2) + 2h + j%2; the W4 chunk 2 (j/2) + h holds the pair's 32
+  //     nibbles, read once per pair, half j%2 unpacked per sub-step)
   const int frow = lane & 31;
-  const int fsw = swz<PG_BK>(lane & 15);
-  auto read_frag = [&](int slot, int j, int r, i32x4 (&wfn)[PG_TN], i32x4 (&xfn)[PG_TM])
-                       __attribute__((always_inline)) {
+  auto read_x = [&](int slot, int j, int b, i32x4 (&xfn)[PG_TM]) __attribute__((always_inline)) {
+    const int8_t* Xs = smem + slot * PG_STAGE + PG_W_BYTES;
+    const int row = wm * PG_WM + b * 32 + frow;
+    const int c = W4 ? 4 * (j / 2) + 2 * h + (j % 2) : 2 * j + h;
+    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * PG_BK + ((c ^ swz<PG_BK>(row)) << 4));
+  };
+  auto read_w = [&](int slot, int j, int a, i32x4 (&dst)[PG_TN]) __attribute__((always_inline)) {
     const int8_t* Ws = smem + slot * PG_STAGE;
-    const int fs = ((2 * j + h) ^ fsw) << 4;
-    if (r < PG_TN)
-      wfn[r < PG_TN ? r : 0] =
-          *reinterpret_cast<const i32x4*>(Ws + (wn * PG_WN + r * 32 + frow) * PG_BK + fs);
-    else
-      xfn[r >= PG_TN ? r - PG_TN : 0] = *reinterpret_cast<const i32x4*>(
-          Ws + PG_W_BYTES + (wm * PG_WM + (r - PG_TN) * 32 + frow) * PG_BK + fs);
+    const int row = wn * PG_WN + a * 32 + frow;
+    const int c = W4 ? 2 * (j / 2) + h : 2 * j + h;
+    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * WB + ((c ^ swz<WB>(row)) << 4));
+  };
+  i32x4 raw[PG_TN];  // int4 only: packed chunks of the current sub-step pair
+  auto unpack_half = [&](int a, int half, i32x4 (&dst)[PG_TN]) __attribute__((always_inline)) {
+    dst[a] = half == 0 ? pg_unpack_w4_8((uint32_t)raw[a][0], (uint32_t)raw[a][1])
+                       : pg_unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
   };
 
   // Group accumulator sets: the GPS groups of an even stage use sets
@@ -208,41 +238,72 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
     }
   };
 
-  // One k sub-step in a fixed order (sched_barrier): the MFMAs into set CS
+  // Scales of the flush, double-buffered by sub-step: sub-step j flushes
+  // combos j*CPSS .. + CPSS with sv[j & 1] and reads the next sub-step's
+  // into sv[(j + 1) & 1], a whole sub-step ahead of their use.
+  float sv[2][CPSS][GPS][4];
+  auto read_sub_scales = [&](int st, int j, float (&dst)[CPSS][GPS][4])
+                             __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < CPSS; ++c)
+#pragma unroll
+      for (int g = 0; g < GPS; ++g) read_scales(st, g, j * CPSS + c, dst[c][g]);
+  };
+
+  // One k sub-step J in a fixed order (sched_barrier): the MFMAs into set CS
   // (C = 0 when `first`), the next sub-step's fragment reads one per MFMA in
-  // consumption order (rd), this wave's DMA loads of stage dst into slot dsl
-  // (dma), and the flush of combos J*CPSS .. + CPSS of every group of stage
-  // fst from sets FS .. FS+GPS-1, groups in order (EPM accumulators after
-  // each MFMA; a combo's scales are read one MFMA ahead of its first use).
+  // consumption order (rd) together with its flush scales (stage nst), this
+  // wave's DMA loads of stage dst into slot dsl (dma), and the flush of combos
+  // J*CPSS .. + CPSS of every group of the previous stage from sets
+  // FS .. FS+GPS-1, groups in order (EPM accumulators after each MFMA).
   auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto FSc, auto Jc,
-                  const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs, int rj,
-                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int fst)
+                  const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs,
+                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int nst)
                   __attribute__((always_inline)) {
     constexpr int CS = decltype(CSc)::value, FS = decltype(FSc)::value, J = decltype(Jc)::value;
+    constexpr int JN = (J + 1) % 4;  // the sub-step whose operands are read
     constexpr bool first = decltype(firstc)::value != 0;
     constexpr bool rd = decltype(rdc)::value != 0;
     constexpr bool dma = decltype(dmac)::value != 0;
-    float sv[CPSS][GPS][4];
-#pragma unroll
-    for (int g = 0; g < GPS; ++g) read_scales(fst, g, J * CPSS, sv[0][g]);
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
-#pragma unroll
-      for (int c = 1; c < CPSS; ++c)
-        if ((c * EPC / EPM > 0 ? c * EPC / EPM - 1 : 0) == idx) {
-#pragma unroll
-          for (int g = 0; g < GPS; ++g) read_scales(fst, g, J * CPSS + c, sv[c][g]);
-        }
       const int a = idx / PG_TM, b = idx % PG_TM;
       if constexpr (first)
         D[CS][a][b] = mfma32(wc[a], xc[b], i32x16{});
       else
         D[CS][a][b] = mfma32(wc[a], xc[b], D[CS][a][b]);
-      if constexpr (rd) {
+      if constexpr (rd && !W4) {
 #pragma unroll
         for (int q = 0; q < NR; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx)
-            read_frag(rs, rj, q == 0 ? 0 : (q <= PG_TM ? PG_TN + q - 1 : q - PG_TM), wn_, xn);
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q == 0)
+              read_w(rs, JN, 0, wn_);
+            else if (q <= PG_TM)
+              read_x(rs, JN, q - 1, xn);
+            else
+              read_w(rs, JN, q - PG_TM, wn_);
+          }
+      }
+      if constexpr (rd && W4) {
+        constexpr bool new_pair = (JN % 2) == 0;
+        constexpr int NRD = PG_TM + (new_pair ? PG_TN : 0);
+#pragma unroll
+        for (int q = 0; q < NRD; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q < PG_TM)
+              read_x(rs, JN, q, xn);
+            else
+              read_w(rs, JN, q - PG_TM, raw);
+          }
+#pragma unroll
+        for (int a2 = 0; a2 < PG_TN; ++a2) {
+          constexpr int first_slot = new_pair ? (NMF > PG_TN ? NMF - PG_TN : 0) : 0;
+          if ((first_slot + a2 < NMF ? first_slot + a2 : NMF - 1) == idx)
+            unpack_half(a2, JN % 2, wn_);
+        }
+      }
+      if constexpr (rd) {
+        if (idx == 0) read_sub_scales(nst, JN, sv[JN & 1]);
       }
       if constexpr (dma) {
 #pragma unroll
@@ -257,7 +318,7 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
         const int aa = combo / 4, r = 4 * (combo % 4) + rr;
 #pragma unroll
         for (int g = 0; g < GPS; ++g) {
-          const float t = (float)D[FS + g][aa][bb][r] * sv[c][g][rr];
+          const float t = (float)D[FS + g][aa][bb][r] * sv[J & 1][c][g][rr];
           facc[aa][bb][r] = facc[aa][bb][r] + t;
         }
       }
@@ -286,7 +347,18 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
     wait_vmcnt<(PG_NS - 1) * PG_PS>();
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < NR; ++r) read_frag(0, 0, r, wf[0], xf[0]);
+  for (int b = 0; b < PG_TM; ++b) read_x(0, 0, b, xf[0]);
+#pragma unroll
+  for (int a = 0; a < PG_TN; ++a) {
+    if constexpr (W4) {
+      read_w(0, 0, a, raw);
+      unpack_half(a, 0, wf[0]);
+    } else {
+      read_w(0, 0, a, wf[0]);
+    }
+  }
+
+  read_sub_scales(0, 0, sv[0]);  // stage 0 flushes the zero sets with stage 0's scales
 
   float sa_t = 0.0f;
   uint16_t b_t = 0;
@@ -311,16 +383,15 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
     constexpr int CS = HALF * GPS + (J) / SUBG;                                              \
     if constexpr ((J) < 3) {                                                                 \
       step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<0>{}, ic<FS>{}, ic<(J)>{},        \
-           wf[(J) & 1], xf[(J) & 1], sl, (J) + 1, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0,  \
-           0, fst);                                                                          \
+           wf[(J) & 1], xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, fst);    \
     } else if constexpr (!LAST) {                                                            \
       wait_stage();                                                                          \
       __syncthreads();                                                                       \
       step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<1>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
-           xf[1], (kt + 1) % PG_NS, 0, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, fst);      \
+           xf[1], (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, kt);          \
     } else {                                                                                 \
       step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<0>{}, ic<0>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
-           xf[1], 0, 0, wf[0], xf[0], 0, 0, fst);                                            \
+           xf[1], 0, wf[0], xf[0], 0, 0, 0);                                                 \
     }                                                                                        \
   }
     PG_SUB(0)
@@ -410,19 +481,27 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_pg_kernel(const GemmArgs p) {
 
 // Eligible: int8 weights, per-group gs 64 / 128, K % 128 == 0, N % 8 == 0,
 // 16-byte aligned operands (launch_gemm checks).
-hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, hipStream_t s) {
-  constexpr int BM = 128;
-  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + 127) / 128);
-  if (gs == 64) {
-    if (sw_half)
-      gemm_dma_pg_kernel<BM, 64, true><<<tiles, 256, 0, s>>>(a);
+hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
+  constexpr int BM = 128, BN = PG_LAUNCH_BN, OCC = PG_LAUNCH_OCC;
+  // gs = 64 (four group sets) spills at this occupancy; the dispatcher sends
+  // it to the register-staged kernel
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  if (wf == W_I4) {
+    // int4 weights come with fp16 group scales ([K/gs, N])
+    if (gs == 64)
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, OCC><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, 64, false><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, OCC><<<tiles, 256, 0, s>>>(a);
+  } else if (gs == 64) {
+    if (sw_half)
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
+    else
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
   } else {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, 128, true><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, 128, false><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
   }
   return hipGetLastError();
 }

@@ -275,9 +275,13 @@ def test_w4a8_full_size_rows():
     assert_bits_equal(y[rows], O.w4a8_linear(x[rows], packed, sw), "w4 full-size rows")
 
 
+# gs = 128 with M > 64, K % 128 == 0 and N % 8 == 0 runs the LDS-DMA
+# per-group kernel with int4 weights (100x96, 512x640, one stage at K=128, an
+# odd stage count at K=384).
 @pytest.mark.parametrize("gs", [64, 128])
 @pytest.mark.parametrize("M,N,K", [(1, 48, 256), (16, 300, 1024), (17, 40, 512),
-                                   (100, 96, 512), (512, 640, 2048)])
+                                   (100, 96, 512), (512, 640, 2048), (128, 256, 128),
+                                   (257, 136, 384)])
 def test_w4a8_pergroup(gs, M, N, K):
     x = O.synth_activations(M, K, 70 + M)
     w4 = np.random.default_rng(71 + N).integers(-8, 8, (N, K), dtype=np.int8)
@@ -289,6 +293,19 @@ def test_w4a8_pergroup(gs, M, N, K):
         assert_bits_equal(y, exp, f"w4g gs{gs} {M}x{N}x{K}")
     else:
         assert_f16_close(y, exp, what=f"w4g gs{gs} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+def test_w4a8_pergroup_full_size_rows(gs):
+    M, N, K = 4096, 12288, 4096
+    x = O.synth_activations(M, K, 73 + gs)
+    w4 = np.random.default_rng(74).integers(-8, 8, (N, K), dtype=np.int8)
+    packed = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 75).astype(np.float16)
+    y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
+    rows = np.r_[0:16, M - 16:M]
+    exp = O.w4a8_pergroup_linear(x[rows], packed, sc, gs)
+    assert_bits_equal(y[rows], exp, f"w4g gs{gs} full-size rows")
 
 
 # --------------------------------------------------------------------------
