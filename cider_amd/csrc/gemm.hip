@@ -375,10 +375,9 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                    (a.sw == nullptr || aligned16(a.sw));
   if (epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 && a.N % 8 == 0)
     return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)
-  // gs = 128 on the LDS-DMA per-group kernel; gs = 64 needs four group
-  // accumulator sets there, which spill, so it stays on the register-staged
-  // kernel (faster for it)
-  if (epi == EPI_PG && gs == 128 && vec && a.K % 128 == 0 && a.N % 8 == 0)
+  // per-group gs 64 / 128 on the LDS-DMA per-group kernel (gs 256 and other
+  // shapes on the register-staged kernel)
+  if (epi == EPI_PG && (gs == 64 || gs == 128) && vec && a.K % 128 == 0 && a.N % 8 == 0)
     return launch_gemm_dma_pg(a, gs, sw_half, wf, s);  // gemm_dma_pg.hip
   if (epi == EPI_I32) return run_tiled<256, 256, W_I8, EPI_I32, false, 0>(a, vec, s);
   if (epi == EPI_PC) {

@@ -14,18 +14,22 @@
 //     through a 4-slot ring of 128-byte k-stages,
 //     with the constant-count waits, swizzle and fixed-order sub-steps of
 //     the per-channel kernel (gemm_dma.hip).
-//   * Group accumulators: int32 sets per group, 2 * (groups per stage) of
-//     them (2 at gs = 128, 4 at gs = 64; 64 accumulators per lane each at
-//     the 128 x 128 tile, all in AGPRs).  A group's first MFMA takes C = 0 (an
-//     inline constant), so starting a group costs nothing.  The groups of
-//     stage kt are flushed during stage kt+1, interleaved with its MFMAs in the
-//     same fixed order, into the 64 fp32 accumulators per lane: 4 VALU ops per
-//     accumulator and group (read, convert, multiply by the scale, add),
-//     groups in order.  Every set is read a whole stage after its last MFMA,
-//     so the flush never waits on the matrix pipe.  The flush is the VALU
-//     bound of the kernel: 2x the MFMA time at gs = 128, 4x at gs = 64.
-//     Stage 0 flushes the zero sets of "stage -1" with stage 0's scales
-//     (adding +0.0); the last stage flushes its own groups after its MFMAs.
+//   * Group accumulators: two int32 sets alternate by group.  A group's first
+//     MFMA takes C = 0 (an inline constant), so starting a group costs
+//     nothing.  While group g accumulates, group g-1 is flushed into the fp32
+//     accumulators, a slice per sub-step interleaved with group g's MFMAs in
+//     the same fixed order: 4 VALU ops per accumulator (convert, multiply by
+//     the scale, add; a register read when the set lives in AGPRs).  The
+//     flush is the VALU bound of the kernel: about 2x the MFMA time at
+//     gs = 128, 4x at gs = 64.  Before the first group the other set is zero
+//     and its "scales" are group 0's, so the first flush adds +0.0; the last
+//     stage flushes the last group after its MFMAs.
+//   * Tile 128 x 64.  gs = 128 runs two workgroups per CU: the sets and the
+//     fp32 accumulators then fit in VGPRs, and one workgroup's LDS / barrier
+//     waits hide behind the other's flush.  gs = 64 (twice the flush per
+//     sub-step) runs one workgroup per CU, where it needs no spill: a spill
+//     reload is a vector-memory load the compiler tracks, and waiting for it
+//     would also wait for every LDS-DMA load in flight.
 //   * Scales: wave 0 DMAs the scale rows of a stage's groups (sw[g, n0..n0+127])
 //     into an 8-slot LDS ring of its own, so a row stays in LDS until its
 //     group has been flushed during the next stage.  Wave 0 therefore moves one
@@ -82,10 +86,12 @@ __device__ __forceinline__ i32x4 pg_unpack_w4_8(uint32_t w0, uint32_t w1) {
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-// Dispatched tile: 128 x 64 with two workgroups per CU (each workgroup's
-// waits hide behind the other's VALU flush; the int32 group sets then fit in
-// VGPRs, so the flush reads them without v_accvgpr_read).
-constexpr int PG_LAUNCH_BN = 64, PG_LAUNCH_OCC = 2;
+// Dispatched tile: 128 x 64.  gs = 128 runs two workgroups per CU (each
+// workgroup's waits hide behind the other's flush; the int32 group sets then
+// fit in VGPRs, so the flush reads them without v_accvgpr_read).  gs = 64
+// does not fit 256 registers that way (a spill would make the compiler wait
+// for every LDS-DMA load in flight), so it runs one workgroup per CU.
+constexpr int PG_LAUNCH_BN = 64;
 
 }  // namespace
 
@@ -195,16 +201,15 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
                        : pg_unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
   };
 
-  // Group accumulator sets: the GPS groups of an even stage use sets
-  // 0 .. GPS-1, those of an odd stage GPS .. 2*GPS-1.  All groups of stage kt
-  // are flushed during stage kt+1, so every set is read a whole stage after
-  // its last MFMA.
-  constexpr int NSET = 2 * GPS;
-  constexpr int EPC = PG_TM * 4;        // accumulators per (a, q) combo
-  constexpr int CPSS = NCOMBO / 4;      // combos flushed per sub-step
-  constexpr int EPM = CPSS * EPC / NMF; // accumulators flushed after each MFMA
-  static_assert(CPSS * 4 == NCOMBO && (CPSS * EPC) % NMF == 0, "flush split");
-  i32x16 D[NSET][PG_TN][PG_TM];
+  // Two int32 group sets alternate by group (set = group parity); while
+  // group g accumulates, group g-1 is flushed, CPF of its scale combos per
+  // sub-step over the SUBG sub-steps of group g.  Before the first group the
+  // other set is zero and its "scales" are group 0's, so that flush adds +0.0.
+  constexpr int EPC = PG_TM * 4;          // accumulators per (a, q) combo
+  constexpr int CPF = NCOMBO / SUBG;      // combos flushed per sub-step
+  constexpr int EPM = CPF * EPC / NMF;    // accumulators flushed after each MFMA
+  static_assert(CPF * SUBG == NCOMBO && (CPF * EPC) % NMF == 0, "flush split");
+  i32x16 D[2][PG_TN][PG_TM];
   float facc[PG_TN][PG_TM][16];
 #pragma unroll
   for (int a = 0; a < PG_TN; ++a)
@@ -212,16 +217,16 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
     for (int b = 0; b < PG_TM; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-#pragma unroll
-        for (int c = 0; c < NSET; ++c) D[c][a][b][r] = 0;
+        D[0][a][b][r] = 0;
+        D[1][a][b][r] = 0;
         facc[a][b][r] = 0.0f;
       }
 
-  // the 4 scales of combo (a, q) of group `row` of stage st:
-  // n = wn*64 + 32a + 8q + 4h + [0..3]
-  auto read_scales = [&](int st, int row, int combo, float (&sv)[4])
-                         __attribute__((always_inline)) {
-    const int8_t* base = smem + PG_RING + (st % PG_SNS) * PG_SSLOT + row * ROWB;
+  // the 4 scales of combo (a, q) of group g (clamped at 0):
+  // n = wn*WN + 32a + 8q + 4h + [0..3]
+  auto read_scales = [&](int g, int combo, float (&sv)[4]) __attribute__((always_inline)) {
+    g = max(g, 0);
+    const int8_t* base = smem + PG_RING + ((g / GPS) % PG_SNS) * PG_SSLOT + (g % GPS) * ROWB;
     const int nl = wn * PG_WN + (combo / 4) * 32 + 8 * (combo % 4) + 4 * h;
     if constexpr (SWH) {
       const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
@@ -237,34 +242,34 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
       sv[3] = v[3];
     }
   };
-
-  // Scales of the flush, double-buffered by sub-step: sub-step j flushes
-  // combos j*CPSS .. + CPSS with sv[j & 1] and reads the next sub-step's
-  // into sv[(j + 1) & 1], a whole sub-step ahead of their use.
-  float sv[2][CPSS][GPS][4];
-  auto read_sub_scales = [&](int st, int j, float (&dst)[CPSS][GPS][4])
+  // Scales of the flush.  gs = 128: double-buffered by sub-step (sub-step j
+  // flushes with sv[j & 1] and reads the next sub-step's into sv[(j+1) & 1]).
+  // gs = 64 at two workgroups per CU (twice the combos per sub-step): one
+  // buffer, read at the start of the sub-step, to save registers.
+  constexpr bool SVDB = (GS == 128) || (OCC == 1);
+  float sv[SVDB ? 2 : 1][CPF][4];
+  auto read_sub_scales = [&](int g, int slice, float (&dst)[CPF][4])
                              __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < CPSS; ++c)
-#pragma unroll
-      for (int g = 0; g < GPS; ++g) read_scales(st, g, j * CPSS + c, dst[c][g]);
+    for (int c = 0; c < CPF; ++c) read_scales(g, slice * CPF + c, dst[c]);
   };
 
-  // One k sub-step J in a fixed order (sched_barrier): the MFMAs into set CS
-  // (C = 0 when `first`), the next sub-step's fragment reads one per MFMA in
-  // consumption order (rd) together with its flush scales (stage nst), this
-  // wave's DMA loads of stage dst into slot dsl (dma), and the flush of combos
-  // J*CPSS .. + CPSS of every group of the previous stage from sets
-  // FS .. FS+GPS-1, groups in order (EPM accumulators after each MFMA).
-  auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto FSc, auto Jc,
+  // One k sub-step J of the stage in a fixed order (sched_barrier): the
+  // MFMAs into set CS (C = 0 when `first`), the next sub-step's fragment
+  // reads one per MFMA in consumption order (rd) together with its flush
+  // scales (group ng, slice ns), this wave's DMA loads of stage dst into slot
+  // dsl (dma), and the flush of slice SL of the previous group from set
+  // 1 - CS (EPM accumulators after each MFMA).
+  auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto SLc, auto Jc,
                   const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs,
-                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int nst)
-                  __attribute__((always_inline)) {
-    constexpr int CS = decltype(CSc)::value, FS = decltype(FSc)::value, J = decltype(Jc)::value;
+                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int ng, int ns,
+                  int cg) __attribute__((always_inline)) {
+    constexpr int CS = decltype(CSc)::value, SL = decltype(SLc)::value, J = decltype(Jc)::value;
     constexpr int JN = (J + 1) % 4;  // the sub-step whose operands are read
     constexpr bool first = decltype(firstc)::value != 0;
     constexpr bool rd = decltype(rdc)::value != 0;
     constexpr bool dma = decltype(dmac)::value != 0;
+    if constexpr (!SVDB) read_sub_scales(cg, SL, sv[0]);
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
       const int a = idx / PG_TM, b = idx % PG_TM;
@@ -302,8 +307,8 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
             unpack_half(a2, JN % 2, wn_);
         }
       }
-      if constexpr (rd) {
-        if (idx == 0) read_sub_scales(nst, JN, sv[JN & 1]);
+      if constexpr (rd && SVDB) {
+        if (idx == 0) read_sub_scales(ng, ns, sv[JN & 1]);
       }
       if constexpr (dma) {
 #pragma unroll
@@ -314,13 +319,10 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
 #pragma unroll
       for (int e = idx * EPM; e < (idx + 1) * EPM; ++e) {
         const int c = e / EPC, bb = (e / 4) % PG_TM, rr = e % 4;
-        const int combo = J * CPSS + c;
+        const int combo = SL * CPF + c;
         const int aa = combo / 4, r = 4 * (combo % 4) + rr;
-#pragma unroll
-        for (int g = 0; g < GPS; ++g) {
-          const float t = (float)D[FS + g][aa][bb][r] * sv[J & 1][c][g][rr];
-          facc[aa][bb][r] = facc[aa][bb][r] + t;
-        }
+        const float t = (float)D[1 - CS][aa][bb][r] * sv[SVDB ? (J & 1) : 0][c][rr];
+        facc[aa][bb][r] = facc[aa][bb][r] + t;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -358,40 +360,44 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
     }
   }
 
-  read_sub_scales(0, 0, sv[0]);  // stage 0 flushes the zero sets with stage 0's scales
+  if constexpr (SVDB) read_sub_scales(-1, 0, sv[0]);  // first flush: zero set, group 0's scales
 
   float sa_t = 0.0f;
   uint16_t b_t = 0;
 
   // Stage kt at position HALF (0 or 1) of a 2-stage period that starts at an
-  // even kt, so set indices are compile-time.  It flushes stage kt-1 (at
-  // kt = 0: the zero sets of "stage -1" with stage 0's scales, adding +0.0).
+  // even kt, so group parities are compile-time.  Sub-step J belongs to
+  // group kt*GPS + J/SUBG and flushes slice J % SUBG of the group before it.
   // LAST: the final stage (no barrier or DMA; requests sa and bias; then
-  // flushes its own groups).
+  // flushes its own last group).
   auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
     constexpr int HALF = decltype(halfc)::value;
     constexpr bool LAST = decltype(lastc)::value != 0;
-    constexpr int FS = (1 - HALF) * GPS;
     const int sl = kt % PG_NS;
-    const int fst = max(kt - 1, 0);
     if constexpr (LAST) {
       sa_t = p.sa[min(m0 + tid % PG_BM, M - 1)];
       if (p.bias) b_t = p.bias[min(n0 + tid % PG_BN, N - 1)];
     }
+    // flushed group of sub-step J of stage k: k*GPS + J/SUBG - 1
 #define PG_SUB(J)                                                                            \
   {                                                                                          \
-    constexpr int CS = HALF * GPS + (J) / SUBG;                                              \
+    constexpr int S = 4 * HALF + (J);                                                        \
+    constexpr int CS = (S / SUBG) & 1;                                                       \
+    constexpr bool FIRST = (S % SUBG) == 0;                                                  \
+    constexpr int SL = S % SUBG;                                                             \
     if constexpr ((J) < 3) {                                                                 \
-      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<0>{}, ic<FS>{}, ic<(J)>{},        \
-           wf[(J) & 1], xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, fst);    \
+      step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[(J) & 1],       \
+           xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0,                      \
+           kt * GPS + ((J) + 1) / SUBG - 1, ((J) + 1) % SUBG, kt * GPS + (J) / SUBG - 1);    \
     } else if constexpr (!LAST) {                                                            \
       wait_stage();                                                                          \
       __syncthreads();                                                                       \
-      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<1>{}, ic<1>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
-           xf[1], (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, kt);          \
+      step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1],      \
+           (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, (kt + 1) * GPS - 1,  \
+           0, kt * GPS + (J) / SUBG - 1);                                                    \
     } else {                                                                                 \
-      step(ic<CS>{}, ic<((J) % SUBG == 0)>{}, ic<0>{}, ic<0>{}, ic<FS>{}, ic<(J)>{}, wf[1], \
-           xf[1], 0, wf[0], xf[0], 0, 0, 0);                                                 \
+      step(ic<CS>{}, ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1], 0,    \
+           wf[0], xf[0], 0, 0, 0, 0, kt * GPS + (J) / SUBG - 1);                             \
     }                                                                                        \
   }
     PG_SUB(0)
@@ -400,22 +406,21 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
     PG_SUB(3)
 #undef PG_SUB
     if constexpr (LAST) {
-      // flush this stage's own groups, in order
+      // flush the last group (set of sub-step 3), in order
+      constexpr int CSL = ((4 * HALF + 3) / SUBG) & 1;
+      const int gl = G - 1;
 #pragma unroll
       for (int combo = 0; combo < NCOMBO; ++combo) {
-        float sv[GPS][4];
-#pragma unroll
-        for (int g = 0; g < GPS; ++g) read_scales(kt, g, combo, sv[g]);
+        float s4[4];
+        read_scales(gl, combo, s4);
         const int aa = combo / 4, q = combo % 4;
 #pragma unroll
         for (int bb = 0; bb < PG_TM; ++bb)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-            for (int g = 0; g < GPS; ++g) {
-              const float t = (float)D[HALF * GPS + g][aa][bb][4 * q + rr] * sv[g][rr];
-              facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
-            }
+          for (int rr = 0; rr < 4; ++rr) {
+            const float t = (float)D[CSL][aa][bb][4 * q + rr] * s4[rr];
+            facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+          }
       }
     }
   };
@@ -482,26 +487,24 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
 // Eligible: int8 weights, per-group gs 64 / 128, K % 128 == 0, N % 8 == 0,
 // 16-byte aligned operands (launch_gemm checks).
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
-  constexpr int BM = 128, BN = PG_LAUNCH_BN, OCC = PG_LAUNCH_OCC;
-  // gs = 64 (four group sets) spills at this occupancy; the dispatcher sends
-  // it to the register-staged kernel
+  constexpr int BM = 128, BN = PG_LAUNCH_BN;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (wf == W_I4) {
     // int4 weights come with fp16 group scales ([K/gs, N])
     if (gs == 64)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, 2><<<tiles, 256, 0, s>>>(a);
   } else if (gs == 64) {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1><<<tiles, 256, 0, s>>>(a);
   } else {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, 2><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, OCC><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, 2><<<tiles, 256, 0, s>>>(a);
   }
   return hipGetLastError();
 }

@@ -201,8 +201,8 @@ def test_full_size_down_proj_rows():
 
 
 # M > 64 with K % 128 == 0 and N % 8 == 0 runs the LDS-DMA per-group kernel
-# at gs = 128 (one k-stage (K=128), two (K=256), an odd count (K=384), ragged
-# M and N); gs 64 / 256 and K=320 run the register-staged kernel.
+# at gs 64 / 128 (one k-stage (K=128), two (K=256), an odd count (K=384),
+# ragged M and N); gs 256 and K=320 run the register-staged kernel.
 @pytest.mark.parametrize("gs", [64, 128, 256])
 @pytest.mark.parametrize("M,N,K", [(1, 72, 512), (1, 10240, 2560), (5, 48, 256), (16, 130, 512),
                                    (64, 100, 1024), (65, 96, 512), (300, 520, 1024),
@@ -275,9 +275,9 @@ def test_w4a8_full_size_rows():
     assert_bits_equal(y[rows], O.w4a8_linear(x[rows], packed, sw), "w4 full-size rows")
 
 
-# gs = 128 with M > 64, K % 128 == 0 and N % 8 == 0 runs the LDS-DMA
-# per-group kernel with int4 weights (100x96, 512x640, one stage at K=128, an
-# odd stage count at K=384).
+# M > 64, K % 128 == 0 and N % 8 == 0 runs the LDS-DMA per-group kernel with
+# int4 weights (100x96, 512x640, one stage at K=128, an odd stage count at
+# K=384).
 @pytest.mark.parametrize("gs", [64, 128])
 @pytest.mark.parametrize("M,N,K", [(1, 48, 256), (16, 300, 1024), (17, 40, 512),
                                    (100, 96, 512), (512, 640, 2048), (128, 256, 128),
