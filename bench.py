@@ -226,10 +226,21 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
 def sweep(torch, args, dev):
     """per-channel / per-group gs 128 and 64, M in {1,128,1024,4096,8192},
     (N,K) in {(10240,2560),(2560,10240)}; configs[2]: W4A8 per-group gs 64 / 128,
-    (N,K) in {(12288,4096),(4096,12288)}, M in {1,16,512,4096}.  Timed through
-    cider_amd.ops with HIP events; weights rotate over >= 2x the MALL when a
-    call is memory-bound (M <= 64) so every launch streams from HBM."""
-    import cider_amd as C
+    (N,K) in {(12288,4096),(4096,12288)}, M in {1,16,512,4096}.
+
+    Each case is the whole linear (per-token quantize + GEMM, or the MV at
+    M == 1) called through the C ABI with preallocated output and workspace.
+    A run of calls is captured in a HIP graph and replayed, so the time per
+    call is GPU time, free of Python and launch overhead.  Weights rotate over
+    >= 2x the MALL when a call is memory-bound (M <= 64) so every call streams
+    them from HBM."""
+    from cider_amd import _lib
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    stream = torch.cuda.current_stream(dev)
+
+    def cur():  # the current stream (graph capture runs on a stream of its own)
+        return vp(torch.cuda.current_stream(dev).cuda_stream)
 
     def synth_x(M, K, seed):
         g = torch.Generator(device="cpu").manual_seed(seed)
@@ -237,60 +248,90 @@ def sweep(torch, args, dev):
         x[:, torch.randperm(K, generator=g)[: K // 100]] *= 20.0
         return x.to(torch.float16).to(dev)
 
-    def run(name, fn_for, M, N, K, wbytes, nbytes_alg, ops, mode):
-        copies = max(1, -(-2 * MALL_BYTES // wbytes) + 1) if M <= 64 else 1
-        fns = [fn_for(i) for i in range(copies)]
-        iters = max(20, 2 * copies)
-        for i in range(max(5, copies)):
-            fns[i % copies]()
+    def run(name, call_for, ncopies, M, N, K, nbytes_alg, ops, mode):
+        reps = max(24, 2 * ncopies)
+        for i in range(max(4, ncopies)):
+            call_for(i % ncopies)
         torch.cuda.synchronize()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(iters)]
-        for i in range(iters):
-            evs[i][0].record()
-            fns[i % copies]()
-            evs[i][1].record()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(reps):
+                call_for(i % ncopies)
+        g.replay()
         torch.cuda.synchronize()
-        ms = statistics.median([a.elapsed_time(b) for a, b in evs])
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) / reps)
+        ms = statistics.median(times)
         rec = {"case": name, "mode": mode, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
                "tops": round(ops / (ms * 1e-3) / 1e12, 1),
                "frac_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
                "gbs": round(nbytes_alg / (ms * 1e-3) / 1e9, 1),
                "frac_hbm": round(nbytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-               "weight_copies": copies}
+               "weight_copies": ncopies, "timing": "HIP graph of %d calls" % reps}
+        del g
         print(json.dumps(rec), flush=True)
+
+    def copies_for(M, wbytes):
+        return max(1, -(-2 * MALL_BYTES // wbytes) + 1) if M <= 64 else 1
 
     g = torch.Generator(device="cpu").manual_seed(args.seed)
     for (N, K) in [(10240, 2560), (2560, 10240)]:
+        nw = -(-2 * MALL_BYTES // (N * K)) + 1
+        ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+              for _ in range(nw)]
+        bias = torch.zeros(N, dtype=torch.float16, device=dev)
         for mode, gs in [("per-channel", 0), ("per-group-128", 128), ("per-group-64", 64)]:
-            nw = -(-2 * MALL_BYTES // (N * K)) + 1
-            ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
-                  for _ in range(nw)]
             sw = ((torch.rand(N, generator=g) * 9e-3 + 1e-3) if gs == 0 else
                   (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3)).to(dev)
             sbytes = 4 * N if gs == 0 else 4 * N * (K // gs)
             for M in (1, 128, 1024, 4096, 8192):
                 x = synth_x(M, K, args.seed + M)
+                y = torch.empty((M, N), dtype=torch.float16, device=dev)
+                op = _lib.CIDER_OP_PERCHANNEL if gs == 0 else _lib.CIDER_OP_PERGROUP
+                nb = _lib.workspace_bytes(op, M, N, K, gs)
+                wsp = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
                 if gs == 0:
-                    fn_for = lambda i, x=x: (lambda: C.perchannel_linear(x, ws[i % nw], sw))
+                    def call_for(i, x=x, y=y, wsp=wsp, nb=nb, sw=sw, M=M):
+                        _lib.check(lib.cider_perchannel_linear(
+                            vp(x.data_ptr()), vp(ws[i].data_ptr()), vp(sw.data_ptr()),
+                            vp(bias.data_ptr()), vp(y.data_ptr()), vp(wsp.data_ptr()), nb,
+                            M, N, K, cur()))
                 else:
-                    fn_for = lambda i, x=x, gs=gs: (lambda: C.pergroup_linear(x, ws[i % nw], sw, gs))
+                    def call_for(i, x=x, y=y, wsp=wsp, nb=nb, sw=sw, M=M, gs=gs):
+                        _lib.check(lib.cider_pergroup_linear(
+                            vp(x.data_ptr()), vp(ws[i].data_ptr()), vp(sw.data_ptr()),
+                            vp(bias.data_ptr()), vp(y.data_ptr()), vp(wsp.data_ptr()), nb,
+                            M, N, K, gs, cur()))
                 nbytes = N * K + 2 * M * K + sbytes + 2 * N + 2 * M * N
-                run("configs[1]", fn_for, M, N, K, N * K, nbytes, 2.0 * M * N * K, mode)
-            del ws
+                run("configs[1]", call_for, copies_for(M, N * K), M, N, K, nbytes,
+                    2.0 * M * N * K, mode)
+        del ws
     for (N, K) in [(12288, 4096), (4096, 12288)]:
+        nw = -(-2 * MALL_BYTES // (N * K // 2)) + 1
+        pk = [torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).to(dev)
+              for _ in range(nw)]
         for gs in (128, 64):
-            nw = -(-2 * MALL_BYTES // (N * K // 2)) + 1
-            pk = [torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).to(dev)
-                  for _ in range(nw)]
             sc = (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3).to(torch.float16).to(dev)
             for M in (1, 16, 512, 4096):
                 x = synth_x(M, K, args.seed + M)
-                fn_for = lambda i, x=x, gs=gs: (lambda: C.w4a8_pergroup_linear(x, pk[i % nw], sc, gs))
+                y = torch.empty((M, N), dtype=torch.float16, device=dev)
+                nb = _lib.workspace_bytes(_lib.CIDER_OP_W4A8_PERGROUP, M, N, K, gs)
+                wsp = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+
+                def call_for(i, x=x, y=y, wsp=wsp, nb=nb, sc=sc, M=M, gs=gs):
+                    _lib.check(lib.cider_w4a8_pergroup_linear(
+                        vp(x.data_ptr()), vp(pk[i].data_ptr()), vp(sc.data_ptr()), None,
+                        vp(y.data_ptr()), vp(wsp.data_ptr()), nb, M, N, K, gs, cur()))
                 nbytes = N * K // 2 + 2 * M * K + 2 * N * (K // gs) + 2 * M * N
-                run("configs[2]", fn_for, M, N, K, N * K // 2, nbytes, 2.0 * M * N * K,
-                    f"w4a8-per-group-{gs}")
-            del pk
+                run("configs[2]", call_for, copies_for(M, N * K // 2), M, N, K, nbytes,
+                    2.0 * M * N * K, f"w4a8-per-group-{gs}")
+        del pk
 
 
 def cpu_baseline(x, w, sw, bias, y, N, K):

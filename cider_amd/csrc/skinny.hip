@@ -10,9 +10,13 @@
 // MI355X design
 //   * A workgroup (4 waves) owns 16 weight rows n and all M (<= 16*TM) rows
 //     of x.  The four waves split K into contiguous ranges; every lane loads
-//     its 16-byte weight slice straight from HBM into the MFMA "A" register
-//     (no LDS round trip: each weight byte is used by TM MFMAs only), with U
-//     k-steps of loads in flight per lane.
+//     its weight slice straight from HBM into the MFMA "A" register (no LDS
+//     round trip: each weight byte is used by TM MFMAs only).  Two register
+//     buffers of U k-steps alternate, so the next batch is in flight while
+//     the current one reduces.
+//   * Per-group scales of the workgroup's 16 columns (all groups) are staged
+//     in LDS at the start; their loads are issued before the first weight
+//     batch, so the flush never waits on a global load inside the loop.
 //   * Per-channel / int32: the four int32 partial accumulators are summed
 //     through LDS (exact, order-free) and wave 0 runs the epilogue.
 //   * Per-group: each wave flushes its groups into an fp32 chain in group
@@ -40,9 +44,12 @@ __device__ __forceinline__ float load_scale1(const void* base, int64_t idx) {
 
 template <int TM, int WF, int EPI, bool SWH, int GS, bool VEC>
 __global__ __launch_bounds__(kThreads) void skinny_kernel(const GemmArgs p) {
-  constexpr int U = (TM == 1) ? 8 : 4;                 // k-steps in flight
+  constexpr int U = (TM == 1) ? 8 : 4;                 // k-steps per batch
   constexpr int SUB = (EPI == EPI_PG) ? GS / 64 : 1;   // k-steps per group
+  constexpr int SR = 8;                                // scale loads per thread in registers
   __shared__ __attribute__((aligned(16))) int32_t red[4][TM][kWave][4];
+  // per-group scales of this workgroup's 16 columns, [group][column] in fp32
+  extern __shared__ __attribute__((aligned(16))) float ssc[];
 
   // The wave index must be a scalar: branches on k (group start / end) then
   // stay uniform.  MFMA ignores EXEC, so an MFMA under a divergent branch
@@ -63,18 +70,24 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const GemmArgs p) {
   const int kb0 = min(wave * gper * SUB, nkb);
   const int kb1 = min((wave + 1) * gper * SUB, nkb);
 
-  i32x4 acc[TM];
-  float facc[TM][4];
+  // ---- per-group scales: requested first, so the LDS stores below wait
+  // only for them while the first weight batch is already in flight
+  const int G = (EPI == EPI_PG) ? K / GS : 0;
+  float sr[SR];
+  auto load_sc = [&](int e) -> float {
+    const int g = e >> 4, c = e & 15;
+    return (n0 + c < N) ? load_scale1<SWH>(p.sw, (int64_t)g * N + n0 + c) : 0.0f;
+  };
+  if constexpr (EPI == EPI_PG) {
 #pragma unroll
-  for (int b = 0; b < TM; ++b) {
-    acc[b] = i32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int r = 0; r < 4; ++r) facc[b][r] = 0.0f;
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * kThreads;
+      if (e < G * 16) sr[q] = load_sc(e);
+    }
   }
-  const int ncol = n0 + 4 * lq;  // first output column of this lane
 
-  for (int kb = kb0; kb < kb1; kb += U) {
-    i32x4 wv[U], xv[U][TM];
+  // one batch of U k-steps starting at kb: weight fragments and x fragments
+  auto load_batch = [&](int kb, i32x4 (&wv)[U], i32x4 (&xv)[U][TM]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = kb + u;
@@ -90,10 +103,7 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const GemmArgs p) {
           { const i32x2 v = ld8(W + (int64_t)nw * ldw + byte); raw = i32x4{v[0], v[1], 0, 0}; }
         else
           raw = load_bytes_partial(W + (int64_t)nw * ldw + byte, nb < 8 ? nb : 8);
-        uint32_t o0, o1, o2, o3;
-        unpack_w4_word((uint32_t)raw[0], o0, o1);
-        unpack_w4_word((uint32_t)raw[1], o2, o3);
-        wv[u] = i32x4{(int)o0, (int)o1, (int)o2, (int)o3};
+        wv[u] = raw;  // unpacked at consumption
       } else {
         const int kk = k * 64 + 16 * lq;
         const int nb = (in && nw < N) ? K - kk : 0;
@@ -117,25 +127,41 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const GemmArgs p) {
           xv[u][b] = load_bytes_partial(X + (int64_t)m * K + kk, nb < 16 ? nb : 16);
       }
     }
+  };
+
+  i32x4 acc[TM];
+  float facc[TM][4];
+#pragma unroll
+  for (int b = 0; b < TM; ++b) {
+    acc[b] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) facc[b][r] = 0.0f;
+  }
+  const int ncol = n0 + 4 * lq;  // first output column of this lane
+
+  auto consume = [&](int kb, const i32x4 (&wv)[U], const i32x4 (&xv)[U][TM]) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = kb + u;
       if (k >= kb1) break;  // uniform
+      i32x4 wf = wv[u];
+      if constexpr (WF == W_I4) {
+        uint32_t o0, o1, o2, o3;
+        unpack_w4_word((uint32_t)wv[u][0], o0, o1);
+        unpack_w4_word((uint32_t)wv[u][1], o2, o3);
+        wf = i32x4{(int)o0, (int)o1, (int)o2, (int)o3};
+      }
       if constexpr (EPI == EPI_PG) {
         const bool first = (k % SUB) == 0, last = (k % SUB) == SUB - 1;
         if (first) {
 #pragma unroll
-          for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wv[u], xv[u][b], i32x4{0, 0, 0, 0});
+          for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wf, xv[u][b], i32x4{0, 0, 0, 0});
         } else {
 #pragma unroll
-          for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wv[u], xv[u][b], acc[b]);
+          for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wf, xv[u][b], acc[b]);
         }
         if (last) {
-          const int64_t grow = (int64_t)(k / SUB) * N;
-          float swv[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            swv[r] = (ncol + r < N) ? load_scale1<SWH>(p.sw, grow + ncol + r) : 0.0f;
+          const f32x4 swv = *reinterpret_cast<const f32x4*>(&ssc[(k / SUB) * 16 + 4 * lq]);
 #pragma unroll
           for (int b = 0; b < TM; ++b)
 #pragma unroll
@@ -146,9 +172,29 @@ __global__ __launch_bounds__(kThreads) void skinny_kernel(const GemmArgs p) {
         }
       } else {
 #pragma unroll
-        for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wv[u], xv[u][b], acc[b]);
+        for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(wf, xv[u][b], acc[b]);
       }
     }
+  };
+
+  // ---- two register buffers: the next batch loads while this one reduces
+  i32x4 wa[U], xa[U][TM], wb[U], xb[U][TM];
+  load_batch(kb0, wa, xa);
+  if constexpr (EPI == EPI_PG) {
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * kThreads;
+      if (e < G * 16) ssc[e] = sr[q];
+    }
+    for (int e = tid + SR * kThreads; e < G * 16; e += kThreads) ssc[e] = load_sc(e);
+    __syncthreads();
+  }
+  for (int kb = kb0; kb < kb1; kb += 2 * U) {
+    if (kb + U < kb1) load_batch(kb + U, wb, xb);
+    consume(kb, wa, xa);
+    if (kb + U >= kb1) break;
+    if (kb + 2 * U < kb1) load_batch(kb + 2 * U, wa, xa);
+    consume(kb + U, wb, xb);
   }
 
   // ---- combine the four K ranges
@@ -223,10 +269,13 @@ namespace {
 template <int TM, int WF, int EPI, bool SWH, int GS>
 hipError_t run_skinny(const GemmArgs& a, bool vec, hipStream_t s) {
   const int grid = (a.N + 15) / 16;
+  // per-group: the workgroup's 16 columns of every group's scales in LDS
+  const size_t lds = (EPI == EPI_PG) ? (size_t)(a.K / GS) * 16 * sizeof(float) : 0;
+  if (lds > 64 * 1024) return hipErrorInvalidValue;
   if (vec)
-    skinny_kernel<TM, WF, EPI, SWH, GS, true><<<grid, kThreads, 0, s>>>(a);
+    skinny_kernel<TM, WF, EPI, SWH, GS, true><<<grid, kThreads, lds, s>>>(a);
   else
-    skinny_kernel<TM, WF, EPI, SWH, GS, false><<<grid, kThreads, 0, s>>>(a);
+    skinny_kernel<TM, WF, EPI, SWH, GS, false><<<grid, kThreads, lds, s>>>(a);
   return hipGetLastError();
 }
 
