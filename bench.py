@@ -51,6 +51,9 @@ def parse():
                     help="instead of the default line, print one JSON line for configs[3]: "
                          "Qwen3-8B-shaped W8A8 stack, 2048-token prefill + 128 greedy "
                          "decode steps (decode step captured as a HIP graph)")
+    ap.add_argument("--torch-producers", action="store_true",
+                    help="with --qwen3: run RMSNorm, SwiGLU, q/k norm + RoPE and decode "
+                         "attention as PyTorch ops instead of the fused HIP kernels (A/B)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run three 256 MiB device-to-device copies, the known-size "
                          "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling")
@@ -388,7 +391,8 @@ def bench_qwen3(torch, args, dev):
     cfg = Q.QWEN3_8B
     L, steps = 2048, 128
     t0 = time.perf_counter()
-    m = Q.Qwen3(cfg, max_len=L + steps + 1, seed=args.seed, device=dev)
+    m = Q.Qwen3(cfg, max_len=L + steps + 1, seed=args.seed, device=dev,
+                fused=not args.torch_producers)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     gen = torch.Generator(device=dev)
@@ -434,6 +438,9 @@ def bench_qwen3(torch, args, dev):
                    "weight_gbs": round(w_bytes / (decode_ms * 1e-3) / 1e9, 1),
                    "steps": steps, "graph": True,
                    "tokens_distinct": int(out.unique().numel())},
+        "producers": ("pytorch ops" if args.torch_producers else
+                      "fused HIP kernels (RMSNorm/SwiGLU + quantize, q/k norm + RoPE, "
+                      "decode attention)"),
         "build_s": round(build_s, 1),
     }), flush=True)
 

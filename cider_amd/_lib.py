@@ -38,6 +38,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
 _SZ = ctypes.c_size_t
+_F = ctypes.c_float
 
 # name -> (restype, argtypes); exactly the symbols declared in include/cider_hip.h
 SIGNATURES = {
@@ -52,6 +53,12 @@ SIGNATURES = {
     "cider_w4_repack_ref": (_I, [_P, _P, _I64, _I64, _P]),
     "cider_w4a8_linear": (_I, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _P]),
     "cider_w4a8_pergroup_linear": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I, _P]),
+    "cider_rmsnorm_quantize": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _I64, _I64, _P]),
+    "cider_silu_mul_quantize": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
+    "cider_qk_norm_rope": (_I, [_P, _P, _P, _F, _P, _P, _I64, _P, _P, _P, _P, _P,
+                                _I64, _I64, _I64, _I64, _I64, _P]),
+    "cider_attn_decode_workspace_bytes": (_SZ, [_I64, _I64]),
+    "cider_attn_decode": (_I, [_P, _P, _P, _P, _F, _P, _SZ, _P, _I64, _I64, _I64, _I64, _P]),
 }
 
 _lib = None

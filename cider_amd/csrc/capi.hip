@@ -282,4 +282,135 @@ int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
   return hip_status(cider::launch_gemm(g, cider::W_I4, cider::EPI_PG, true, group_size, s), fn);
 }
 
+// ---- producers of the linear's input and the decode attention -------------
+
+namespace {
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int check_rows(const char* fn, int64_t M, int64_t K, const char* kname) {
+  CIDER_TRY(check_dims(fn, M, 1, K));
+  if (K % 8 != 0)
+    return fail(CIDER_E_INVALID, "%s: %s=%lld must be a multiple of 8", fn, kname, (long long)K);
+  return CIDER_OK;
+}
+
+}  // namespace
+
+int cider_rmsnorm_quantize(const void* x_f16, const void* add_f16, void* sum_f16,
+                           const void* w_f16, float eps, void* y_f16, int8_t* q, float* sa,
+                           int64_t M, int64_t K, void* stream) {
+  static const char* fn = "cider_rmsnorm_quantize";
+  CIDER_TRY(check_rows(fn, M, K, "K"));
+  if (!(eps >= 0.0f)) return fail(CIDER_E_INVALID, "%s: eps must be >= 0", fn);
+  if (y_f16 == nullptr && q == nullptr)
+    return fail(CIDER_E_INVALID, "%s: neither y nor q requested", fn);
+  if (add_f16 != nullptr && sum_f16 == nullptr)
+    return fail(CIDER_E_INVALID, "%s: add given without sum", fn);
+  if (M == 0 || K == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", true));
+  CIDER_TRY(need(fn, w_f16, "w", true));
+  CIDER_TRY(need(fn, sa, "sa", q != nullptr));
+  if (!aligned16(x_f16) || !aligned16(add_f16) || !aligned16(sum_f16) || !aligned16(w_f16) ||
+      !aligned16(y_f16) || ((uintptr_t)q & 7) != 0)
+    return fail(CIDER_E_INVALID, "%s: fp16 arrays must be 16-byte and q 8-byte aligned", fn);
+  if (y_f16 != nullptr && (y_f16 == x_f16 || y_f16 == sum_f16))
+    return fail(CIDER_E_INVALID, "%s: y must not alias x or sum", fn);
+  return hip_status(
+      cider::launch_rmsnorm(reinterpret_cast<const uint16_t*>(x_f16),
+                            reinterpret_cast<const uint16_t*>(add_f16),
+                            reinterpret_cast<uint16_t*>(sum_f16),
+                            reinterpret_cast<const uint16_t*>(w_f16), eps,
+                            reinterpret_cast<uint16_t*>(y_f16), q, sa, (int)M, (int)K,
+                            (hipStream_t)stream),
+      fn);
+}
+
+int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* sa, int64_t M,
+                            int64_t I, void* stream) {
+  static const char* fn = "cider_silu_mul_quantize";
+  CIDER_TRY(check_rows(fn, M, I, "I"));
+  if (2 * I > kMaxDim) return fail(CIDER_E_INVALID, "%s: I above 2^29", fn);
+  if (y_f16 == nullptr && q == nullptr)
+    return fail(CIDER_E_INVALID, "%s: neither y nor q requested", fn);
+  if (M == 0 || I == 0) return ok();
+  CIDER_TRY(need(fn, gu_f16, "gate_up", true));
+  CIDER_TRY(need(fn, sa, "sa", q != nullptr));
+  if (!aligned16(gu_f16) || !aligned16(y_f16) || ((uintptr_t)q & 7) != 0)
+    return fail(CIDER_E_INVALID, "%s: fp16 arrays must be 16-byte and q 8-byte aligned", fn);
+  return hip_status(cider::launch_silu_mul(reinterpret_cast<const uint16_t*>(gu_f16),
+                                           reinterpret_cast<uint16_t*>(y_f16), q, sa, (int)M,
+                                           (int)I, (hipStream_t)stream),
+                    fn);
+}
+
+int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16, const void* k_norm_w_f16,
+                       float eps, const void* cos_f16, const void* sin_f16, int64_t P,
+                       const int64_t* rope_row, const int64_t* slot, void* q_out_f16,
+                       void* kT_cache_f16, void* v_cache_f16, int64_t L, int64_t H, int64_t KV,
+                       int64_t D, int64_t T, void* stream) {
+  static const char* fn = "cider_qk_norm_rope";
+  if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
+  if (L < 0 || H <= 0 || KV <= 0 || T <= 0 || P <= 0 || L > kMaxDim || H + 2 * KV > 4096 ||
+      T > kMaxDim || P > kMaxDim || L * (H + 2 * KV) > ((int64_t)1 << 31) - 4)
+    return fail(CIDER_E_INVALID, "%s: bad sizes (L=%lld H=%lld KV=%lld T=%lld P=%lld)", fn,
+                (long long)L, (long long)H, (long long)KV, (long long)T, (long long)P);
+  if (!(eps >= 0.0f)) return fail(CIDER_E_INVALID, "%s: eps must be >= 0", fn);
+  if (L == 0) return ok();
+  CIDER_TRY(need(fn, qkv_f16, "qkv", true));
+  CIDER_TRY(need(fn, q_norm_w_f16, "q_norm_w", true));
+  CIDER_TRY(need(fn, k_norm_w_f16, "k_norm_w", true));
+  CIDER_TRY(need(fn, cos_f16, "cos", true));
+  CIDER_TRY(need(fn, sin_f16, "sin", true));
+  CIDER_TRY(need(fn, rope_row, "rope_row", true));
+  CIDER_TRY(need(fn, slot, "slot", true));
+  CIDER_TRY(need(fn, q_out_f16, "q_out", true));
+  CIDER_TRY(need(fn, kT_cache_f16, "kT_cache", true));
+  CIDER_TRY(need(fn, v_cache_f16, "v_cache", true));
+  return hip_status(
+      cider::launch_qk_norm_rope(
+          reinterpret_cast<const uint16_t*>(qkv_f16),
+          reinterpret_cast<const uint16_t*>(q_norm_w_f16),
+          reinterpret_cast<const uint16_t*>(k_norm_w_f16), eps,
+          reinterpret_cast<const uint16_t*>(cos_f16), reinterpret_cast<const uint16_t*>(sin_f16),
+          P, rope_row, slot, reinterpret_cast<uint16_t*>(q_out_f16),
+          reinterpret_cast<uint16_t*>(kT_cache_f16), reinterpret_cast<uint16_t*>(v_cache_f16),
+          (int)L, (int)H, (int)KV, T, (hipStream_t)stream),
+      fn);
+}
+
+size_t cider_attn_decode_workspace_bytes(int64_t H, int64_t T) {
+  if (H <= 0 || T <= 0 || H > 4096 || T > kMaxDim) return 0;
+  return align256(cider::attn_decode_ws_floats((int)H, T) * sizeof(float));
+}
+
+int cider_attn_decode(const void* q_f16, const void* kT_cache_f16, const void* v_cache_f16,
+                      const int64_t* n_valid, float scale, void* ws, size_t ws_bytes,
+                      void* out_f16, int64_t H, int64_t KV, int64_t D, int64_t T, void* stream) {
+  static const char* fn = "cider_attn_decode";
+  if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
+  if (H <= 0 || KV <= 0 || H > 4096 || H % KV != 0 ||
+      (H / KV != 1 && H / KV != 2 && H / KV != 4 && H / KV != 8))
+    return fail(CIDER_E_INVALID, "%s: H/KV must be 1, 2, 4 or 8 (H=%lld KV=%lld)", fn,
+                (long long)H, (long long)KV);
+  if (T <= 0 || T > kMaxDim || T % 8 != 0)
+    return fail(CIDER_E_INVALID, "%s: cache capacity T=%lld must be a positive multiple of 8",
+                fn, (long long)T);
+  CIDER_TRY(need(fn, q_f16, "q", true));
+  CIDER_TRY(need(fn, kT_cache_f16, "kT_cache", true));
+  CIDER_TRY(need(fn, v_cache_f16, "v_cache", true));
+  CIDER_TRY(need(fn, n_valid, "n_valid", true));
+  CIDER_TRY(need(fn, out_f16, "out", true));
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, cider_attn_decode_workspace_bytes(H, T)));
+  if (!aligned16(q_f16) || !aligned16(kT_cache_f16) || !aligned16(v_cache_f16))
+    return fail(CIDER_E_INVALID, "%s: q and the caches must be 16-byte aligned", fn);
+  return hip_status(
+      cider::launch_attn_decode(reinterpret_cast<const uint16_t*>(q_f16),
+                                reinterpret_cast<const uint16_t*>(kT_cache_f16),
+                                reinterpret_cast<const uint16_t*>(v_cache_f16), n_valid, scale,
+                                reinterpret_cast<float*>(ws), reinterpret_cast<uint16_t*>(out_f16),
+                                (int)H, (int)KV, T, (hipStream_t)stream),
+      fn);
+}
+
 }  // extern "C"

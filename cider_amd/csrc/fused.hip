@@ -1,0 +1,368 @@
+// Producer kernels of the W8A8 linear: the ops that hand a linear its input,
+// with the per-token quantization of cider/kernels/w8a8_quantize.metal:33-86
+// fused into their last pass, so the fp16 activation never makes a round trip
+// through HBM before the GEMM reads its int8 copy.
+//
+//   rmsnorm_quant   h = x (+ add, rounded to fp16 and written back)
+//                   r = 1 / sqrt(sum_k h^2 / K + eps)          (fp32)
+//                   y = h(f32(w) * f32(h(h * r)))              (fp16 out, optional)
+//                   q, sa = quantize_per_token(y)              (optional)
+//                   The RMSNorm order is the Hugging Face / mlx-lm one that the
+//                   reference's models use before every linear: normalise in
+//                   fp32, round to fp16, then scale by the fp16 weight.
+//   silu_mul_quant  y = h(f32(h(silu(g))) * f32(u)) over a row [g | u] of the
+//                   fused gate+up output (cider/fused_hybrid.py:209), then q, sa
+//                   silu(g) = g / (1 + exp(-g)) in fp32.
+//   qk_norm_rope    per token and head of a fused q/k/v projection: RMSNorm of
+//                   q and k over head_dim (own weights), rotate-half RoPE
+//                   (q*cos + rot(q)*sin, each product and the sum rounded to
+//                   fp16), q to a [L, H, D] buffer, k and v straight into the
+//                   KV cache (K transposed [KV, D, T], V [KV, T, D]).
+//
+// The quantization of y is exactly the library's quantize_per_token applied to
+// the fp16 y this kernel produces (same helpers), so q and sa are bit-identical
+// to the unfused pair of calls on that y.  The RMSNorm and SiLU steps are the
+// model's, not the reference library's; their fp32 sums run in a fixed order
+// (each lane in element order, then an xor butterfly).
+//
+// MI355X design: one 64-lane wave per row, 4 rows per workgroup.  A row of up
+// to 64 * 32 * 8 = 16384 elements stays in registers (NV 16-byte vectors per
+// lane) from the read through the reductions to the quantized store, so x is
+// read from HBM once and only q (1 byte/element) and sa go back; longer rows
+// stream from L2 a second and third time.  Reductions are wave-local
+// (shuffles, no LDS, no barrier).
+#include "common.hpp"
+#include "kernels.hpp"
+#include "quant_common.hpp"
+
+namespace cider {
+
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ uint16_t lo16(int32_t w) { return (uint16_t)((uint32_t)w & 0xffffu); }
+__device__ __forceinline__ uint16_t hi16(int32_t w) { return (uint16_t)((uint32_t)w >> 16); }
+__device__ __forceinline__ int32_t pack2(uint16_t a, uint16_t b) {
+  return (int32_t)((uint32_t)a | ((uint32_t)b << 16));
+}
+
+// h(a + b) elementwise on 8 fp16 values
+__device__ __forceinline__ i32x4 add8(i32x4 a, i32x4 b) {
+  i32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    r[j] = pack2(f2h(h2f(lo16(a[j])) + h2f(lo16(b[j]))), f2h(h2f(hi16(a[j])) + h2f(hi16(b[j]))));
+  return r;
+}
+
+__device__ __forceinline__ float sumsq8(i32x4 v, float s) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = h2f(lo16(v[j])), b = h2f(hi16(v[j]));
+    s = s + a * a;
+    s = s + b * b;
+  }
+  return s;
+}
+
+// RMSNorm output of one element: h(f32(w) * f32(h(x * r)))
+__device__ __forceinline__ uint16_t norm1(uint16_t x, uint16_t w, float r) {
+  return f2h(h2f(w) * h2f(f2h(h2f(x) * r)));
+}
+
+__device__ __forceinline__ i32x4 norm8(i32x4 v, i32x4 w, float r) {
+  i32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = pack2(norm1(lo16(v[j]), lo16(w[j]), r), norm1(hi16(v[j]), hi16(w[j]), r));
+  return o;
+}
+
+__device__ __forceinline__ uint16_t swiglu1(uint16_t g, uint16_t u) {
+  const float gf = h2f(g);
+  const uint16_t a = f2h(gf / (1.0f + expf(-gf)));
+  return f2h(h2f(a) * h2f(u));
+}
+
+__device__ __forceinline__ i32x4 swiglu8(i32x4 g, i32x4 u) {
+  i32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    o[j] = pack2(swiglu1(lo16(g[j]), lo16(u[j])), swiglu1(hi16(g[j]), hi16(u[j])));
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (+ residual add) (+ per-token quantize)
+// ---------------------------------------------------------------------------
+template <int NV, bool ADD, bool WY, bool WQ>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(
+    const uint16_t* x, const uint16_t* __restrict__ add, uint16_t* hsum,
+    const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ y,
+    int8_t* __restrict__ q, float* __restrict__ sa, int M, int K) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // uniform per wave
+  const int nvec = K >> 3;
+  const uint16_t* xr = x + row * K;
+  // h of vector e; with ADD the first pass writes it to hsum (which may alias x)
+  auto first_h = [&](int e) -> i32x4 {
+    i32x4 h = ld16(xr + 8 * e);
+    if constexpr (ADD) {
+      h = add8(h, ld16(add + row * K + 8 * e));
+      *reinterpret_cast<i32x4*>(hsum + row * K + 8 * e) = h;
+    }
+    return h;
+  };
+  const uint16_t* hr = ADD ? hsum + row * K : xr;
+
+  float ss = 0.0f, amax = 0.0f;
+  if constexpr (NV > 0) {
+    i32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + i * kWave;
+      v[i] = e < nvec ? first_h(e) : i32x4{0, 0, 0, 0};
+      ss = sumsq8(v[i], ss);
+    }
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + i * kWave;
+      if (e < nvec) {
+        v[i] = norm8(v[i], ld16(w + 8 * e), r);
+        if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * K + 8 * e) = v[i];
+        amax = absmax8(v[i], amax);
+      }
+    }
+    if constexpr (WQ) {
+      amax = wave_max(amax);
+      const float s = row_scale(amax);
+      const float inv = 1.0f / s;
+      if (lane == 0) sa[row] = s;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = lane + i * kWave;
+        if (e < nvec) *reinterpret_cast<i32x2*>(q + row * K + 8 * e) = quant8(v[i], inv);
+      }
+    }
+  } else {
+    for (int e = lane; e < nvec; e += kWave) ss = sumsq8(first_h(e), ss);
+    ss = wave_sum(ss);
+    const float r = 1.0f / sqrtf(ss / (float)K + eps);
+    for (int e = lane; e < nvec; e += kWave) {
+      const i32x4 v = norm8(ld16(hr + 8 * e), ld16(w + 8 * e), r);
+      if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * K + 8 * e) = v;
+      amax = absmax8(v, amax);
+    }
+    if constexpr (WQ) {
+      amax = wave_max(amax);
+      const float s = row_scale(amax);
+      const float inv = 1.0f / s;
+      if (lane == 0) sa[row] = s;
+      for (int e = lane; e < nvec; e += kWave)
+        *reinterpret_cast<i32x2*>(q + row * K + 8 * e) =
+            quant8(norm8(ld16(hr + 8 * e), ld16(w + 8 * e), r), inv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU (+ per-token quantize)
+// ---------------------------------------------------------------------------
+template <int NV, bool WY, bool WQ>
+__global__ __launch_bounds__(256) void silu_mul_kernel(
+    const uint16_t* __restrict__ gu, uint16_t* __restrict__ y, int8_t* __restrict__ q,
+    float* __restrict__ sa, int M, int I) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int nvec = I >> 3;
+  const uint16_t* g = gu + row * 2 * I;
+  const uint16_t* u = g + I;
+  float amax = 0.0f;
+  if constexpr (NV > 0) {
+    i32x4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + i * kWave;
+      if (e < nvec) {
+        v[i] = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
+        if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v[i];
+        amax = absmax8(v[i], amax);
+      }
+    }
+    if constexpr (WQ) {
+      amax = wave_max(amax);
+      const float s = row_scale(amax);
+      const float inv = 1.0f / s;
+      if (lane == 0) sa[row] = s;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = lane + i * kWave;
+        if (e < nvec) *reinterpret_cast<i32x2*>(q + row * I + 8 * e) = quant8(v[i], inv);
+      }
+    }
+  } else {
+    for (int e = lane; e < nvec; e += kWave) {
+      const i32x4 v = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
+      if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v;
+      amax = absmax8(v, amax);
+    }
+    if constexpr (WQ) {
+      amax = wave_max(amax);
+      const float s = row_scale(amax);
+      const float inv = 1.0f / s;
+      if (lane == 0) sa[row] = s;
+      for (int e = lane; e < nvec; e += kWave)
+        *reinterpret_cast<i32x2*>(q + row * I + 8 * e) =
+            quant8(swiglu8(ld16(g + 8 * e), ld16(u + 8 * e)), inv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// per-head q/k RMSNorm + RoPE + KV-cache write (head_dim 128)
+// ---------------------------------------------------------------------------
+// One wave per (token, head) of the fused projection row [q heads | k heads |
+// v heads]; lane l holds elements l and l + 64, which is exactly the pair the
+// rotate-half RoPE mixes.
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(
+    const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
+    const uint16_t* __restrict__ kw, float eps, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, int64_t P, const int64_t* __restrict__ rope_row,
+    const int64_t* __restrict__ slot, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kT,
+    uint16_t* __restrict__ vc, int L, int H, int KV, int64_t T) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63;
+  const int heads = H + 2 * KV;
+  const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = gw / heads;
+  const int hh = (int)(gw % heads);
+  if (t >= L) return;
+  const uint16_t* src = qkv + (t * heads + hh) * D;
+  const uint16_t x0 = src[lane], x1 = src[lane + 64];
+  if (hh >= H + KV) {  // v: copy into the cache
+    const int64_t p = slot[t];
+    if (p < 0 || p >= T) return;
+    uint16_t* dst = vc + ((int64_t)(hh - H - KV) * T + p) * D;
+    dst[lane] = x0;
+    dst[lane + 64] = x1;
+    return;
+  }
+  const int64_t rr = rope_row[t];
+  if (rr < 0 || rr >= P) return;
+  const float a = h2f(x0), b = h2f(x1);
+  float ss = a * a;
+  ss = ss + b * b;
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)D + eps);
+  const uint16_t* wn = hh < H ? qw : kw;
+  const float n0 = h2f(norm1(x0, wn[lane], r)), n1 = h2f(norm1(x1, wn[lane + 64], r));
+  const uint16_t* cr = cos_t + rr * D;
+  const uint16_t* sr = sin_t + rr * D;
+  // out = x * cos + rotate_half(x) * sin, rotate_half(x) = [-x[64:], x[:64]]
+  const uint16_t o0 = f2h(h2f(f2h(n0 * h2f(cr[lane]))) + h2f(f2h(-(n1 * h2f(sr[lane])))));
+  const uint16_t o1 =
+      f2h(h2f(f2h(n1 * h2f(cr[lane + 64]))) + h2f(f2h(n0 * h2f(sr[lane + 64]))));
+  if (hh < H) {
+    uint16_t* dst = q_out + (t * H + hh) * D;
+    dst[lane] = o0;
+    dst[lane + 64] = o1;
+  } else {
+    const int64_t p = slot[t];
+    if (p < 0 || p >= T) return;
+    uint16_t* dst = kT + (int64_t)(hh - H) * D * T + p;
+    dst[(int64_t)lane * T] = o0;
+    dst[(int64_t)(lane + 64) * T] = o1;
+  }
+}
+
+template <template <int> class F, typename... A>
+hipError_t by_nv(int nvec, A... args) {
+  const int per_lane = (nvec + kWave - 1) / kWave;
+  if (per_lane <= 1) return F<1>::run(args...);
+  if (per_lane <= 2) return F<2>::run(args...);
+  if (per_lane <= 4) return F<4>::run(args...);
+  if (per_lane <= 8) return F<8>::run(args...);
+  if (per_lane <= 16) return F<16>::run(args...);
+  if (per_lane <= 32) return F<32>::run(args...);
+  return F<0>::run(args...);
+}
+
+template <int NV>
+struct RmsRun {
+  static hipError_t run(const uint16_t* x, const uint16_t* add, uint16_t* hsum,
+                        const uint16_t* w, float eps, uint16_t* y, int8_t* q, float* sa,
+                        int M, int K, hipStream_t s) {
+    const dim3 grid((M + 3) / 4), block(256);
+    const int sel = (add ? 4 : 0) | (y ? 2 : 0) | (q ? 1 : 0);
+#define CIDER_RMS(A, Y, Q)                                                            \
+  case (A ? 4 : 0) | (Y ? 2 : 0) | (Q ? 1 : 0):                                       \
+    rmsnorm_kernel<NV, A, Y, Q><<<grid, block, 0, s>>>(x, add, hsum, w, eps, y, q, sa, \
+                                                       M, K);                         \
+    break;
+    switch (sel) {
+      CIDER_RMS(false, false, true)
+      CIDER_RMS(false, true, false)
+      CIDER_RMS(false, true, true)
+      CIDER_RMS(true, false, true)
+      CIDER_RMS(true, true, false)
+      CIDER_RMS(true, true, true)
+      default:
+        return hipErrorInvalidValue;
+    }
+#undef CIDER_RMS
+    return hipGetLastError();
+  }
+};
+
+template <int NV>
+struct SwiRun {
+  static hipError_t run(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
+                        hipStream_t s) {
+    const dim3 grid((M + 3) / 4), block(256);
+    if (y && q)
+      silu_mul_kernel<NV, true, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+    else if (y)
+      silu_mul_kernel<NV, true, false><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+    else if (q)
+      silu_mul_kernel<NV, false, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
+};
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* add, uint16_t* hsum,
+                          const uint16_t* w, float eps, uint16_t* y, int8_t* q, float* sa, int M,
+                          int K, hipStream_t s) {
+  return by_nv<RmsRun>(K >> 3, x, add, hsum, w, eps, y, q, sa, M, K, s);
+}
+
+hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
+                           hipStream_t s) {
+  return by_nv<SwiRun>(I >> 3, gu, y, q, sa, M, I, s);
+}
+
+hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,
+                               float eps, const uint16_t* cos_t, const uint16_t* sin_t, int64_t P,
+                               const int64_t* rope_row, const int64_t* slot, uint16_t* q_out,
+                               uint16_t* kT, uint16_t* vc, int L, int H, int KV, int64_t T,
+                               hipStream_t s) {
+  const int64_t waves = (int64_t)L * (H + 2 * KV);
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  qk_norm_rope_kernel<<<grid, block, 0, s>>>(qkv, qw, kw, eps, cos_t, sin_t, P, rope_row, slot,
+                                             q_out, kT, vc, L, H, KV, T);
+  return hipGetLastError();
+}
+
+}  // namespace cider

@@ -34,6 +34,26 @@ hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,
                      hipStream_t s);
 
+// Producer kernels (fused.hip): RMSNorm (+ residual add) and SwiGLU, each
+// optionally ending in the per-token quantization; per-head q/k RMSNorm +
+// RoPE + KV-cache write.
+hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* add, uint16_t* hsum,
+                          const uint16_t* w, float eps, uint16_t* y, int8_t* q, float* sa, int M,
+                          int K, hipStream_t s);
+hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
+                           hipStream_t s);
+hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,
+                               float eps, const uint16_t* cos_t, const uint16_t* sin_t, int64_t P,
+                               const int64_t* rope_row, const int64_t* slot, uint16_t* q_out,
+                               uint16_t* kT, uint16_t* vc, int L, int H, int KV, int64_t T,
+                               hipStream_t s);
+
+// Single-query attention over a KV cache (attn_decode.hip).
+size_t attn_decode_ws_floats(int H, int64_t T);
+hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kT, const uint16_t* vc,
+                              const int64_t* n, float scale, float* ws, uint16_t* out, int H,
+                              int KV, int64_t T, hipStream_t s);
+
 hipError_t launch_w4_repack_ref(const uint8_t* src_kn, uint8_t* dst_nk, int N,
                                 int K, hipStream_t s);
 

@@ -106,6 +106,28 @@ class CiderLinear(torch.nn.Module):
             _lib.check(rc)
         return y
 
+    def forward_quantized(self, q: torch.Tensor, scale_a: torch.Tensor) -> torch.Tensor:
+        """Per-channel linear on activations already quantized per token
+        (q int8 [M, K], scale_a fp32 [M]), as a producer kernel with the
+        quantization fused in hands them over (``cider_amd.fused``).  Equal to
+        ``forward`` on the fp16 tensor that q and scale_a were quantized from
+        (for M >= 2, where ``forward`` quantizes too)."""
+        if self._mode != "per_channel":
+            raise ValueError("forward_quantized: per-channel layers only")
+        M, K = q.shape
+        if K != self._in_features or scale_a.numel() != M:
+            raise ValueError("forward_quantized: q / scale_a do not match the layer")
+        lib = _lib.load()
+        N = self._out_features
+        y = torch.empty((M, N), dtype=torch.float16, device=q.device)
+        rc = lib.cider_perchannel_gemm(
+            q.data_ptr(), scale_a.data_ptr(), self.w_int8.data_ptr(), self.scale_w.data_ptr(),
+            self.bias.data_ptr(), y.data_ptr(), M, N, K,
+            torch.cuda.current_stream(q.device).cuda_stream)
+        if rc != 0:
+            _lib.check(rc)
+        return y
+
     @staticmethod
     def from_float(layer: torch.nn.Module, target_group_size: Optional[int] = None,
                    device=None) -> "CiderLinear":

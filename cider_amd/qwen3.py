@@ -15,11 +15,16 @@ outputs; o_proj and down_proj stay single.  Prefill (M = prompt length) runs
 the quantize + int8 GEMM path; decode (M = 1) runs the fp16-activation MV,
 exactly as ``CiderLinear`` dispatches for the reference (``cider/nn.py:102-113``).
 
-Everything that is not a projection (embedding lookup, RMSNorm, RoPE,
-attention, SiLU, residual adds, the fp16 lm_head) is plain PyTorch on the GPU.
-Attention keeps K transposed in its cache ([kv_heads, head_dim, T]) and groups
-the 4 query heads of each KV head along rows, so both attention products are
-batched matmuls over contiguous, non-transposed operands.
+With ``fused=True`` (the default) the producers of each linear's input are
+HIP kernels of this library (``cider_amd.fused``): the residual add and
+RMSNorm before q/k/v and gate/up, and the SwiGLU before down_proj, end in the
+per-token quantization, so prefill hands (q, scale_a) straight to the int8
+GEMM; the per-head q/k RMSNorm and RoPE write k and v into the cache in the
+same kernel; decode attention is a single-query split-K kernel over the
+cache.  ``fused=False`` runs those steps as plain PyTorch ops instead (the
+A/B reference).  The embedding lookup, prefill attention (batched matmuls over
+the K-transposed cache, the 4 query heads of each KV head grouped along rows)
+and the fp16 lm_head are PyTorch on the GPU in both modes.
 
 Decode keeps the position, the next token and the KV cache on the device, so a
 whole decode step (embedding to argmax) can be captured once as a HIP graph and
@@ -36,6 +41,7 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
+from . import fused as FK
 from .nn import CiderLinear
 
 
@@ -169,13 +175,54 @@ class Qwen3Layer(torch.nn.Module):
         x = x + self.o(self._attend(q, kT_cache, v_cache, mask))
         return x + self._mlp(x)
 
+    # ---- fused producers (HIP kernels) -------------------------------------
+    # The residual stream is carried as (x, pending): the layer's true input is
+    # h(x + pending); the add happens inside the next RMSNorm kernel, which
+    # writes the sum back over x.
+
+    def _norm(self, x, pending, w, want_y, want_q):
+        return FK.rmsnorm_quantize(x, w, self.cfg.rms_eps, add=pending,
+                                   sum_out=x if pending is not None else None,
+                                   want_y=want_y, want_q=want_q)
+
+    def prefill_fused(self, x, pending, tables, rope_row, slot, kT_cache, v_cache, n, mask):
+        """x [L, hidden] (+ pending) at cache slots `slot`; attends over cache
+        positions 0..n-1 with `mask` [L, n].  Returns (x, pending)."""
+        c = self.cfg
+        a = self._norm(x, pending, self.input_norm, False, True)
+        qkv = self.qkv.forward_quantized(a.q, a.scale_a)
+        q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
+                            rope_row, slot, kT_cache, v_cache, c.num_heads, c.num_kv_heads)
+        attn = self._attend(q, kT_cache[:, :, :n], v_cache[:, :n, :], mask)
+        b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
+        gu = self.gate_up.forward_quantized(b.q, b.scale_a)
+        _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
+        return b.h, self.down.forward_quantized(qd, sd)
+
+    def decode_fused(self, x, pending, tables, pos, n_valid, kT_cache, v_cache, ws):
+        """One token x [1, hidden] (+ pending) at device position `pos`
+        ([1] int64), attending over n_valid = pos + 1 cache positions."""
+        c = self.cfg
+        a = self._norm(x, pending, self.input_norm, True, False)
+        qkv = self.qkv(a.y)
+        q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
+                            pos, pos, kT_cache, v_cache, c.num_heads, c.num_kv_heads)
+        attn = FK.attn_decode(q, kT_cache, v_cache, n_valid, 1.0 / math.sqrt(c.head_dim), ws=ws)
+        b = self._norm(a.h, self.o(attn.reshape(1, -1)), self.post_norm, True, False)
+        h, _, _ = FK.silu_mul_quantize(self.gate_up(b.y), want_y=True, want_q=False)
+        return b.h, self.down(h)
+
 
 class Qwen3(torch.nn.Module):
     """Random-init Qwen3-shaped causal LM over W8A8 per-channel linears."""
 
     def __init__(self, cfg: Qwen3Config = QWEN3_8B, max_len: int = 4096, seed: int = 0,
-                 device="cuda"):
+                 device="cuda", fused: bool = True):
         super().__init__()
+        if fused and cfg.head_dim != 128:
+            raise ValueError("Qwen3(fused=True): the q/k-norm, RoPE and attention kernels "
+                             "take head_dim 128")
+        self.fused = fused
         dev = torch.device(device)
         if dev.type != "cuda":
             raise RuntimeError("Qwen3: the W8A8 linears run on a ROCm GPU only")
@@ -183,6 +230,10 @@ class Qwen3(torch.nn.Module):
         gen.manual_seed(seed)
         self.cfg = cfg
         self.max_len = max_len
+        # cache capacity: a multiple of 8 positions (16-byte rows of the
+        # transposed K cache for the attention kernel)
+        cap = (max_len + 7) // 8 * 8
+        self.capacity = cap
         self.device = dev
         h = cfg.hidden_size
         self.embed = (torch.randn(cfg.vocab_size, h, device=dev, generator=gen) * 0.02).half()
@@ -191,14 +242,15 @@ class Qwen3(torch.nn.Module):
         self.final_norm = torch.ones(h, dtype=torch.float16, device=dev)
         self.lm_head = (torch.randn(cfg.vocab_size, h, device=dev, generator=gen)
                         * (1.0 / math.sqrt(h))).half()
-        self.cos, self.sin = rope_tables(cfg.head_dim, max_len, cfg.rope_theta, dev)
+        self.cos, self.sin = rope_tables(cfg.head_dim, cap, cfg.rope_theta, dev)
         kv, d = cfg.num_kv_heads, cfg.head_dim
         # zero-filled: decode attends over the whole cache, masked entries
         # must hold finite values
-        self.kT_cache = torch.zeros(cfg.num_layers, kv, d, max_len, dtype=torch.float16,
+        self.kT_cache = torch.zeros(cfg.num_layers, kv, d, cap, dtype=torch.float16,
                                     device=dev)
-        self.v_cache = torch.zeros(cfg.num_layers, kv, max_len, d, dtype=torch.float16,
+        self.v_cache = torch.zeros(cfg.num_layers, kv, cap, d, dtype=torch.float16,
                                    device=dev)
+        self._attn_ws = FK.attn_decode_workspace(cfg.num_heads, cap, dev) if fused else None
         self._graph = None
 
     # ---- prefill ----------------------------------------------------------
@@ -210,11 +262,22 @@ class Qwen3(torch.nn.Module):
         if L > self.max_len:
             raise ValueError(f"prompt of {L} tokens exceeds max_len={self.max_len}")
         x = self.embed.index_select(0, ids)
-        cos, sin = self.cos[:L, None, :], self.sin[:L, None, :]
         mask = torch.full((L, L), float("-inf"), device=self.device).triu_(1)
+        if self.fused:
+            pos = torch.arange(L, device=self.device)
+            pending = None
+            for i, layer in enumerate(self.layers):
+                x, pending = layer.prefill_fused(x, pending, (self.cos, self.sin), pos, pos,
+                                                 self.kT_cache[i], self.v_cache[i], L, mask)
+            return F.linear(self._final_norm(x, pending), self.lm_head)
+        cos, sin = self.cos[:L, None, :], self.sin[:L, None, :]
         for i, layer in enumerate(self.layers):
             x = layer.prefill(x, cos, sin, self.kT_cache[i], self.v_cache[i], mask)
         return F.linear(rms_norm(x, self.final_norm, self.cfg.rms_eps), self.lm_head)
+
+    def _final_norm(self, x, pending):
+        return FK.rmsnorm_quantize(x, self.final_norm, self.cfg.rms_eps, add=pending,
+                                   sum_out=x, want_y=True, want_q=False).y
 
     # ---- decode -----------------------------------------------------------
     @torch.no_grad()
@@ -222,9 +285,16 @@ class Qwen3(torch.nn.Module):
         """One token: tok [1] int64, pos [1] int64 (both on the device).
         Returns the logits [1, vocab]."""
         x = self.embed.index_select(0, tok)
+        if self.fused:
+            n_valid = pos + 1
+            pending = None
+            for i, layer in enumerate(self.layers):
+                x, pending = layer.decode_fused(x, pending, (self.cos, self.sin), pos, n_valid,
+                                                self.kT_cache[i], self.v_cache[i], self._attn_ws)
+            return F.linear(self._final_norm(x, pending), self.lm_head)
         cos = self.cos.index_select(0, pos)[:, None, :]
         sin = self.sin.index_select(0, pos)[:, None, :]
-        ar = torch.arange(self.max_len, device=self.device)
+        ar = torch.arange(self.capacity, device=self.device)
         mask = torch.where(ar <= pos, 0.0, float("-inf"))
         for i, layer in enumerate(self.layers):
             x = layer.decode(x, cos, sin, pos, self.kT_cache[i], self.v_cache[i], mask)

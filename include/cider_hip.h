@@ -133,6 +133,64 @@ int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
                                int64_t M, int64_t N, int64_t K, int group_size,
                                void* stream);
 
+/* ---- producers of the linear's input, and decode attention ------------
+ * The reference library has no such kernels: its models (Qwen3 through
+ * mlx-lm, cider/fused_hybrid.py:142-213) run RMSNorm, SwiGLU, RoPE and SDPA
+ * as MLX ops and hand the fp16 result to the linear, which quantizes it
+ * (cider/kernels/w8a8_quantize.metal:17-87). These entry points are those
+ * callers on the GPU, with the quantization fused into the producer. */
+
+/* RMSNorm of fp16 rows [M,K] with fp16 weight w [K]:
+ *   h = x, or h = h(x + add) written to sum (sum may alias x) when add != NULL
+ *   r = 1 / sqrt(sum_k f32(h)^2 / K + eps)
+ *   y = h(f32(w) * f32(h(h * r)))            -> y_f16 [M,K] if y_f16 != NULL
+ *   q, sa = quantize_per_token(y)            -> q [M,K], sa [M] if q != NULL
+ * q and sa are bit-identical to cider_quantize_per_token on that y. At least
+ * one of y / q; K % 8 == 0; fp16 arrays 16-byte aligned, q 8-byte aligned;
+ * y must not alias x or sum. */
+int cider_rmsnorm_quantize(const void* x_f16, const void* add_f16, void* sum_f16,
+                           const void* w_f16, float eps, void* y_f16, int8_t* q,
+                           float* sa, int64_t M, int64_t K, void* stream);
+
+/* SwiGLU of the fused gate+up output gu [M, 2I] (gate first, as
+ * cider/fused_hybrid.py:209 splits it):
+ *   y = h(f32(h(g / (1 + exp(-g)))) * f32(u))   -> y_f16 [M,I] if non-NULL
+ *   q, sa = quantize_per_token(y)               -> if q != NULL
+ * I % 8 == 0; alignment as cider_rmsnorm_quantize. */
+int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* sa,
+                            int64_t M, int64_t I, void* stream);
+
+/* Per-head RMSNorm of q and k (weights [D]) and rotate-half RoPE on the rows
+ * of a fused q/k/v projection qkv [L, (H + 2 KV) * D]:
+ *   q_out [L, H, D]          <- RoPE(RMSNorm(q))
+ *   kT_cache[j, :, slot[t]]  <- RoPE(RMSNorm(k_j))    (cache [KV, D, T])
+ *   v_cache[j, slot[t], :]   <- v_j                   (cache [KV, T, D])
+ * using rows rope_row[t] of the cos / sin tables [P, D] (fp16); RoPE is
+ * out = h(h(x*cos) + h(rot(x)*sin)), rot(x) = [-x[D/2:], x[:D/2]].
+ * rope_row and slot are int64 device arrays [L]; a token whose rope_row is
+ * outside [0, P) is skipped, and a slot outside [0, T) writes nothing.
+ * D must be 128. */
+int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16,
+                       const void* k_norm_w_f16, float eps, const void* cos_f16,
+                       const void* sin_f16, int64_t P, const int64_t* rope_row,
+                       const int64_t* slot, void* q_out_f16, void* kT_cache_f16,
+                       void* v_cache_f16, int64_t L, int64_t H, int64_t KV,
+                       int64_t D, int64_t T, void* stream);
+
+/* Bytes of workspace cider_attn_decode needs (fp32 per-chunk partials). */
+size_t cider_attn_decode_workspace_bytes(int64_t H, int64_t T);
+
+/* Single-query grouped-query attention over the caches written by
+ * cider_qk_norm_rope: for query head h of KV head j = h / (H / KV),
+ *   out[h] = sum_{t < n} softmax_t(scale * q[h] . K[j,:,t]) V[j,t,:]
+ * in fp32, rounded to fp16 [H, D]. n = min(*n_valid, T) is read on the
+ * device (int64), so a captured call serves a growing sequence. D == 128,
+ * H / KV in {1, 2, 4, 8}, T % 8 == 0; ws 256-byte aligned. */
+int cider_attn_decode(const void* q_f16, const void* kT_cache_f16,
+                      const void* v_cache_f16, const int64_t* n_valid, float scale,
+                      void* ws, size_t ws_bytes, void* out_f16, int64_t H,
+                      int64_t KV, int64_t D, int64_t T, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

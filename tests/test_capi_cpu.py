@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 11, syms
+    assert len(syms) == 16, syms
 
 
 def test_library_exports_every_header_symbol(lib):
@@ -92,6 +92,52 @@ def test_validation_errors_without_gpu(lib):
     assert lib.cider_perchannel_linear(n, n, n, n, n, n, 0, 0, 8, 16, n) == _lib.CIDER_OK
     assert lib.cider_int8_matmul_int32(n, n, n, 5, 0, 16, n) == _lib.CIDER_OK
     assert _err(lib) == ""
+
+
+def test_producer_and_attention_validation_without_gpu(lib):
+    from cider_amd import _lib
+    p = ctypes.c_void_p(0x1000)
+    n = None
+    E = _lib.CIDER_E_INVALID
+    # K must be a multiple of 8; something must be requested; add needs sum
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, 1e-6, p, n, n, 4, 12, n) == E
+    assert "multiple of 8" in _err(lib)
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, 1e-6, n, n, n, 4, 16, n) == E
+    assert "neither" in _err(lib)
+    assert lib.cider_rmsnorm_quantize(p, p, n, p, 1e-6, p, n, n, 4, 16, n) == E
+    assert "sum" in _err(lib)
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, -1.0, p, n, n, 4, 16, n) == E
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, 1e-6, n, p, n, 4, 16, n) == E
+    assert "sa is NULL" in _err(lib)
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, 1e-6, ctypes.c_void_p(0x1008), n, n,
+                                      4, 16, n) == E
+    assert "aligned" in _err(lib)
+    assert lib.cider_rmsnorm_quantize(p, n, n, p, 1e-6, p, n, n, 4, 16, n) == E
+    assert "alias" in _err(lib)
+    assert lib.cider_silu_mul_quantize(p, p, n, n, 4, 20, n) == E
+    assert lib.cider_silu_mul_quantize(p, n, n, n, 4, 16, n) == E
+    # head_dim 128 only; sizes; NULL tables
+    args = [p, p, p, 1e-6, p, p, 64, p, p, p, p, p, 3, 8, 2, 128, 64, n]
+    bad = list(args)
+    bad[15] = 64
+    assert lib.cider_qk_norm_rope(*bad) == E and "head_dim" in _err(lib)
+    bad = list(args)
+    bad[4] = n
+    assert lib.cider_qk_norm_rope(*bad) == E and "cos is NULL" in _err(lib)
+    bad = list(args)
+    bad[16] = 0
+    assert lib.cider_qk_norm_rope(*bad) == E
+    # attention: group ratio, capacity multiple of 8, workspace
+    wsb = lib.cider_attn_decode_workspace_bytes(32, 4096)
+    assert wsb == 32 * 32 * 130 * 4  # 32 chunks of 128 positions, 32 heads
+    assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 24, 8, 128, 4096, n) == E
+    assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 32, 8, 128, 4092, n) == E
+    assert lib.cider_attn_decode(p, p, p, p, 0.1, p, 16, p, 32, 8, 128, 4096, n) == E
+    assert "workspace" in _err(lib)
+    assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 32, 8, 64, 4096, n) == E
+    # empty problems succeed
+    assert lib.cider_rmsnorm_quantize(n, n, n, n, 1e-6, p, n, n, 0, 16, n) == _lib.CIDER_OK
+    assert lib.cider_qk_norm_rope(*(args[:12] + [0] + args[13:])) == _lib.CIDER_OK
 
 
 def test_check_maps_codes_to_exceptions(lib):

@@ -1,0 +1,272 @@
+"""GPU parity of the producer kernels (RMSNorm / SwiGLU with the per-token
+quantization fused in, per-head q/k norm + RoPE + cache write) and of the
+single-query decode attention.
+
+Bars:
+  * quantization: q and scale_a bit-identical to the oracle's
+    quantize_per_token (restating cider/kernels/w8a8_quantize.metal:33-86)
+    applied to the fp16 tensor the producer itself returns;
+  * residual add: bit-identical to fp16 addition;
+  * RMSNorm / SwiGLU / RoPE outputs: the same chain of fp16 roundings
+    evaluated in float64 on the CPU.  The kernel's fp32 sum of squares and exp
+    differ from float64 in the last bits, which can move the rounding of the
+    chain's first fp16 intermediate by one step: the output must equal the
+    chain's for that intermediate or a neighbour (RoPE: within the error bound
+    that step propagates to), and almost all elements must be identical;
+  * attention: float64 softmax attention on the CPU, within fp16 output
+    rounding plus fp32 accumulation error (rtol 4e-3, atol 2e-3).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from cider_amd import fused as F
+from oracle import cider_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _f16(a):
+    return np.asarray(a, dtype=np.float64).astype(np.float16).astype(np.float64)
+
+
+def _ulp16(v):
+    """fp16 ulp at |v| (normal range), as float64."""
+    a = np.maximum(np.abs(v), 2.0 ** -14)
+    return 2.0 ** (np.floor(np.log2(a)) - 10)
+
+
+def _rms_parts(h, w, eps):
+    """float64 RMSNorm chain: t = h(h * r) and the weight, y = h(w * t)."""
+    r = 1.0 / np.sqrt((h * h).sum(-1, keepdims=True) / h.shape[-1] + eps)
+    return _f16(h * r), w
+
+
+def _rms_ref(h, w, eps):
+    t, w = _rms_parts(h, w, eps)
+    return _f16(w * t)
+
+
+def _assert_chain(got, t, w, what, max_frac=0.02):
+    """got == h(w * t') with t' equal to t or one fp16 step either side: t is
+    the float64 chain's rounded intermediate (h(h * r) for RMSNorm, h(silu(g))
+    for SwiGLU); the kernel's fp32 sum of squares / exp may move that rounding
+    by one step, which w scales before the final rounding."""
+    t16 = t.astype(np.float16)
+    lo = np.nextafter(t16, np.float16(-np.inf)).astype(np.float64)
+    hi = np.nextafter(t16, np.float16(np.inf)).astype(np.float64)
+    got = got.astype(np.float64)
+    ok = (got == _f16(w * t)) | (got == _f16(w * lo)) | (got == _f16(w * hi))
+    assert np.all(ok), f"{what}: {int(np.sum(~ok))} elements off by more than one step of t"
+    frac = np.mean(got != _f16(w * t))
+    assert frac <= max_frac, f"{what}: {frac:.4f} of the elements differ"
+
+
+def _assert_rms(got, h, w, eps, what):
+    t, w = _rms_parts(h, w, eps)
+    _assert_chain(got, t, w, what)
+
+
+def _quant_check(y_t, q_t, sa_t, what):
+    y = y_t.cpu().numpy()
+    q_ref, sa_ref = O.quantize_per_token(y)
+    assert np.array_equal(q_t.cpu().numpy(), q_ref), f"{what}: q differs from the oracle"
+    assert np.array_equal(sa_t.cpu().numpy().view(np.uint32),
+                          np.asarray(sa_ref, dtype=np.float32).view(np.uint32)), \
+        f"{what}: scale_a differs from the oracle"
+
+
+RMS_SHAPES = [(1, 4096), (7, 2560), (300, 4096), (33, 12288), (5, 20480), (64, 8), (4, 264)]
+
+
+@pytest.mark.parametrize("M,K", RMS_SHAPES)
+@pytest.mark.parametrize("with_add", [False, True])
+def test_rmsnorm_quantize(M, K, with_add):
+    g = torch.Generator(device="cuda").manual_seed(M * 131 + K)
+    x = (torch.randn(M, K, device="cuda", generator=g) * 3).half()
+    w = (torch.rand(K, device="cuda", generator=g) * 2).half()
+    add = (torch.randn(M, K, device="cuda", generator=g)).half() if with_add else None
+    r = F.rmsnorm_quantize(x, w, 1e-6, add=add)
+    torch.cuda.synchronize()
+    h = x if add is None else x + add
+    if add is not None:
+        assert torch.equal(r.h, h), "residual sum is not the fp16 sum"
+    _assert_rms(r.y.cpu().numpy(), h.double().cpu().numpy(), w.double().cpu().numpy(), 1e-6,
+                f"rmsnorm y M={M} K={K}")
+    _quant_check(r.y, r.q, r.scale_a, f"rmsnorm q M={M} K={K}")
+    # q-only launch computes the same q
+    r2 = F.rmsnorm_quantize(x, w, 1e-6, add=add, want_y=False)
+    assert torch.equal(r2.q, r.q) and torch.equal(r2.scale_a, r.scale_a)
+
+
+def test_rmsnorm_in_place_residual_and_special_rows():
+    K = 1024
+    x = torch.randn(6, K, device="cuda").half()
+    x[1] = 0                       # zero row: y = 0, scale 1, q = 0
+    x[2] = 2.5                     # constant row: y = h(w * h(2.5 / sqrt(6.25 + eps)))
+    add = torch.zeros_like(x)
+    w = torch.ones(K, device="cuda", dtype=torch.float16)
+    x0 = x.clone()
+    r = F.rmsnorm_quantize(x, w, 1e-6, add=add, sum_out=x)   # h written over x
+    torch.cuda.synchronize()
+    assert torch.equal(x, x0) and r.h.data_ptr() == x.data_ptr()
+    assert torch.all(r.y[1] == 0) and torch.all(r.q[1] == 0) and r.scale_a[1].item() == 1.0
+    one = np.float16(2.5 / math.sqrt(6.25 + 1e-6))
+    assert torch.all(r.y[2].cpu() == torch.tensor(float(one)).half())
+    assert torch.all(r.q[2] == 127)
+
+
+SWI_SHAPES = [(1, 12288), (3, 6144), (129, 4096), (2, 24576), (16, 8)]
+
+
+@pytest.mark.parametrize("M,I", SWI_SHAPES)
+def test_silu_mul_quantize(M, I):
+    g = torch.Generator(device="cuda").manual_seed(M + I)
+    gu = (torch.randn(M, 2 * I, device="cuda", generator=g) * 3).half()
+    y, q, sa = F.silu_mul_quantize(gu)
+    torch.cuda.synchronize()
+    a = gu[:, :I].double().cpu().numpy()
+    u = gu[:, I:].double().cpu().numpy()
+    _assert_chain(y.cpu().numpy(), _f16(a / (1.0 + np.exp(-a))), u, f"swiglu M={M} I={I}")
+    _quant_check(y, q, sa, f"swiglu q M={M} I={I}")
+    _, q2, sa2 = F.silu_mul_quantize(gu, want_y=False)
+    assert torch.equal(q2, q) and torch.equal(sa2, sa)
+
+
+def _rope_tables(P, D=128, theta=1e6):
+    inv = 1.0 / (theta ** (np.arange(0, D, 2) / D))
+    f = np.outer(np.arange(P), inv)
+    emb = np.concatenate([f, f], -1)
+    return np.cos(emb).astype(np.float16), np.sin(emb).astype(np.float16)
+
+
+@pytest.mark.parametrize("L,H,KV", [(1, 32, 8), (37, 16, 8), (5, 4, 4)])
+def test_qk_norm_rope_and_cache(L, H, KV):
+    D, T, P = 128, 96, 200
+    g = torch.Generator(device="cuda").manual_seed(L * 7 + H)
+    qkv = (torch.randn(L, (H + 2 * KV) * D, device="cuda", generator=g) * 2).half()
+    qw = (torch.rand(D, device="cuda", generator=g) + 0.5).half()
+    kw = (torch.rand(D, device="cuda", generator=g) + 0.5).half()
+    cos_np, sin_np = _rope_tables(P)
+    cos, sin = torch.from_numpy(cos_np).cuda(), torch.from_numpy(sin_np).cuda()
+    rope_row = torch.randint(0, P, (L,), device="cuda", generator=g)
+    slot = torch.randperm(T, device="cuda", generator=g)[:L].contiguous()
+    kT = torch.zeros(KV, D, T, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
+    q = F.qk_norm_rope(qkv, qw, kw, 1e-6, cos, sin, rope_row, slot, kT, vc, H, KV)
+    torch.cuda.synchronize()
+
+    x = qkv.double().cpu().numpy().reshape(L, H + 2 * KV, D)
+    rr = rope_row.cpu().numpy()
+    c, s = cos_np.astype(np.float64)[rr][:, None, :], sin_np.astype(np.float64)[rr][:, None, :]
+
+    def ref(part, w):
+        """(expected out, error bound): the norm output n may be one step of
+        its intermediate off (scaled by w, then rounded), which the rotation
+        carries with |cos| and |sin| into two rounded products and a rounded
+        sum; bound = 2 fp16 steps of each product plus one of the result."""
+        n = _rms_ref(part, w.double().cpu().numpy(), 1e-6)
+        rot = np.concatenate([-n[..., D // 2:], n[..., :D // 2]], -1)
+        a, b = _f16(n * c), _f16(rot * s)
+        out = _f16(a + b)
+        return out, 2 * (_ulp16(a) + _ulp16(b)) + _ulp16(out)
+
+    def check(got, exp_bound, what):
+        exp, bound = exp_bound
+        diff = np.abs(got.astype(np.float64) - exp)
+        assert np.all(diff <= bound), f"{what}: {int(np.sum(diff > bound))} beyond the bound"
+        assert np.mean(diff > 0) <= 0.03, f"{what}: {np.mean(diff > 0):.4f} differ"
+
+    check(q.cpu().numpy(), ref(x[:, :H], qw), "q")
+    k_exp = ref(x[:, H:H + KV], kw)
+    sl = slot.cpu().numpy()
+    k_got = kT.cpu().numpy().astype(np.float64)[:, :, sl].transpose(2, 0, 1)   # [L, KV, D]
+    check(k_got, k_exp, "k cache")
+    v_got = vc.cpu().numpy()[:, sl, :].transpose(1, 0, 2)
+    assert np.array_equal(v_got, qkv.cpu().numpy().reshape(L, H + 2 * KV, D)[:, H + KV:])
+    untouched = np.setdiff1d(np.arange(T), sl)
+    assert np.all(kT.cpu().numpy()[:, :, untouched] == 0)
+    assert np.all(vc.cpu().numpy()[:, untouched, :] == 0)
+
+
+def test_qk_norm_rope_skips_out_of_range_slots():
+    H, KV, D, T = 4, 2, 128, 16
+    qkv = torch.randn(2, (H + 2 * KV) * D, device="cuda").half()
+    w = torch.ones(D, device="cuda", dtype=torch.float16)
+    cos_np, sin_np = _rope_tables(8)
+    cos, sin = torch.from_numpy(cos_np).cuda(), torch.from_numpy(sin_np).cuda()
+    kT = torch.zeros(KV, D, T, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
+    rope_row = torch.tensor([1, 2], device="cuda")
+    slot = torch.tensor([3, T], device="cuda")     # the second token has no slot
+    F.qk_norm_rope(qkv, w, w, 1e-6, cos, sin, rope_row, slot, kT, vc, H, KV)
+    torch.cuda.synchronize()
+    written = (kT != 0).any(dim=1).any(dim=0).cpu().numpy()
+    assert written[3] and written.sum() == 1
+    assert torch.equal(vc[:, 3], qkv[0].reshape(H + 2 * KV, D)[H + KV:])
+
+
+def _attn_ref(q, kT, vc, n, scale):
+    H, D = q.shape
+    KV = kT.shape[0]
+    G = H // KV
+    out = np.zeros((H, D))
+    for h in range(H):
+        j = h // G
+        s = scale * (q[h] @ kT[j][:, :n])
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ vc[j][:n]
+    return out
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+@pytest.mark.parametrize("n", [1, 127, 128, 129, 600, 640, 645])
+def test_attn_decode(G, n):
+    KV, D, T = 2, 128, 640
+    H = KV * G
+    g = torch.Generator(device="cuda").manual_seed(G * 1000 + n)
+    q = torch.randn(H, D, device="cuda", generator=g).half()
+    kT = torch.randn(KV, D, T, device="cuda", generator=g).half()
+    vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    # positions >= n hold garbage that must not leak into the result
+    nn = min(n, T)
+    kT[:, :, nn:] = float("nan")
+    vc[:, nn:, :] = float("nan")
+    nv = torch.tensor([n], device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    out = F.attn_decode(q, kT, vc, nv, scale)
+    torch.cuda.synchronize()
+    exp = _attn_ref(q.double().cpu().numpy(), kT.double().cpu().numpy()[:, :, :nn],
+                    vc.double().cpu().numpy()[:, :nn], nn, scale)
+    got = out.double().cpu().numpy().reshape(H, D)
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, exp, rtol=4e-3, atol=2e-3)
+
+
+def test_attn_decode_graph_replays_follow_device_length():
+    KV, G, D, T = 8, 4, 128, 512
+    H = KV * G
+    q = torch.randn(H, D, device="cuda").half()
+    kT = torch.randn(KV, D, T, device="cuda").half()
+    vc = torch.randn(KV, T, D, device="cuda").half()
+    nv = torch.tensor([1], device="cuda")
+    ws = F.attn_decode_workspace(H, T, "cuda")
+    out = torch.empty(H * D, dtype=torch.float16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        F.attn_decode(q, kT, vc, nv, 0.1, ws=ws, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        F.attn_decode(q, kT, vc, nv, 0.1, ws=ws, out=out)
+    for n in (3, 130, 257, 512, 40):
+        nv.fill_(n)
+        eager = F.attn_decode(q, kT, vc, nv, 0.1)
+        torch.cuda.synchronize()
+        gr.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"n={n}"

@@ -16,7 +16,7 @@ import torch
 from cider_amd import qwen3 as Q
 
 TINY = Q.Qwen3Config(hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4,
-                     num_kv_heads=2, head_dim=64, vocab_size=1000)
+                     num_kv_heads=2, head_dim=128, vocab_size=1000)
 
 
 def test_qwen3_8b_linear_work():
@@ -129,6 +129,25 @@ def test_tiny_decode_matches_prefill():
     # decode runs the fp16-activation MV, prefill the W8A8 GEMM: equal up to
     # activation quantization
     _close(last[0], full[64], 8e-2, "decode vs prefill")
+
+
+@pytest.mark.gpu
+def test_tiny_fused_matches_torch_producers():
+    """The fused HIP producers (RMSNorm + quantize, SwiGLU + quantize, q/k
+    norm + RoPE + cache write, decode attention) against the same model run
+    with PyTorch ops for those steps; equal up to RMSNorm / exp rounding that
+    can move an activation's int8 rounding."""
+    ids = torch.randint(0, TINY.vocab_size, (40,), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(10))
+    a = Q.Qwen3(TINY, max_len=128, seed=9, fused=True)
+    b = Q.Qwen3(TINY, max_len=128, seed=9, fused=False)
+    _close(a.prefill(ids), b.prefill(ids), 3e-2, "prefill fused vs torch")
+    assert torch.allclose(a.v_cache[:, :, :40].float(), b.v_cache[:, :, :40].float(),
+                          rtol=3e-2, atol=3e-2)
+    tok = ids[-1:].clone()
+    pos = torch.tensor([40], device="cuda")
+    _close(a.decode_step(tok, pos)[0], b.decode_step(tok, pos)[0], 3e-2,
+           "decode fused vs torch")
 
 
 @pytest.mark.gpu
