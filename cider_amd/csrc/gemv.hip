@@ -234,6 +234,153 @@ __global__ __launch_bounds__(256) void mv_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide-row variant for full blocks (K % 256 == 0, K <= kMaxF32K, aligned):
+// one physical lane per reference lane (32 lanes per row, two rows per wave),
+// so each block costs a lane one 8-byte weight load, and the grid has twice
+// the waves of the 16-lane layout (more weight bytes in flight on short-N
+// shapes).  x is staged in LDS as fp32, converted once per workgroup, which
+// leaves three VALU operations per weight element (byte -> f32, multiply,
+// add) in the loop.  Same reduction order as mv_kernel and the reference:
+// lane l's chain over blocks, then the xor butterfly 16, 8, 4, 2, 1.
+// ---------------------------------------------------------------------------
+constexpr int kMaxF32K = 16384;  // fp32 x in LDS up to 64 KB
+
+__device__ __forceinline__ float dot8f(uint32_t w0, uint32_t w1, const f32x4& xa,
+                                       const f32x4& xb) {
+  float d = (float)(int8_t)(w0 & 0xffu) * xa[0];
+  d = d + (float)(int8_t)((w0 >> 8) & 0xffu) * xa[1];
+  d = d + (float)(int8_t)((w0 >> 16) & 0xffu) * xa[2];
+  d = d + (float)(int8_t)(w0 >> 24) * xa[3];
+  d = d + (float)(int8_t)(w1 & 0xffu) * xb[0];
+  d = d + (float)(int8_t)((w1 >> 8) & 0xffu) * xb[1];
+  d = d + (float)(int8_t)((w1 >> 16) & 0xffu) * xb[2];
+  d = d + (float)(int8_t)(w1 >> 24) * xb[3];
+  return d;
+}
+
+template <bool PG, int U>
+__global__ __launch_bounds__(256) void mv_wide_kernel(
+    const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
+    const float* __restrict__ sw, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int N, int K, int gs) {
+  constexpr int kRows = 8;  // rows per workgroup: 2 per wave
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
+  float* xs = reinterpret_cast<float*>(dyn);
+  const int nb = K >> 8;
+  const int G = PG ? K / gs : 0;
+  float* sws = xs + K;  // per-group scales [G][kRows]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rl = lane & 31;                 // reference lane
+  const int row_in_wg = wave * 2 + (lane >> 5);
+  const int n0 = blockIdx.x * kRows;
+  const int n = n0 + row_in_wg;
+  const bool live = n < N;
+  const int8_t* wr = w + (int64_t)(live ? n : 0) * K + 8 * rl;
+
+  // branch-free: a block past the end re-reads the last one (never consumed)
+  auto load_w = [&](int b) -> i32x2 { return ld8(wr + (int64_t)min(b, nb - 1) * 256); };
+
+  // ---- stage x as fp32 (and the group scales); x reads first, then the
+  // first 2U weight blocks, then the conversions and LDS stores
+  constexpr int XR = 4;
+  const int nchunk = K >> 3;
+  i32x4 xr[XR];
+#pragma unroll
+  for (int q = 0; q < XR; ++q) xr[q] = ld16(x + 8 * min(tid + q * 256, nchunk - 1));
+  constexpr int SR = 4;
+  float sr[SR];
+  auto load_s = [&](int e) -> float {
+    const int g = e / kRows, r = e % kRows;
+    return (n0 + r < N) ? sw[(int64_t)g * N + n0 + r] : 0.0f;
+  };
+  if constexpr (PG) {
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * 256;
+      if (e < G * kRows) sr[q] = load_s(e);
+    }
+  }
+  i32x2 wa[U], wb[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) wa[u] = load_w(u);
+#pragma unroll
+  for (int u = 0; u < U; ++u) wb[u] = load_w(U + u);
+
+  auto store_x = [&](int e, i32x4 v) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      lo[2 * i] = h2f((uint16_t)((uint32_t)v[i] & 0xffffu));
+      lo[2 * i + 1] = h2f((uint16_t)((uint32_t)v[i] >> 16));
+      hi[2 * i] = h2f((uint16_t)((uint32_t)v[2 + i] & 0xffffu));
+      hi[2 * i + 1] = h2f((uint16_t)((uint32_t)v[2 + i] >> 16));
+    }
+    *reinterpret_cast<f32x4*>(xs + 8 * e) = lo;
+    *reinterpret_cast<f32x4*>(xs + 8 * e + 4) = hi;
+  };
+#pragma unroll
+  for (int q = 0; q < XR; ++q) {
+    const int e = tid + q * 256;
+    if (e < nchunk) store_x(e, xr[q]);
+  }
+  for (int e = tid + XR * 256; e < nchunk; e += 256) store_x(e, ld16(x + 8 * e));
+  if constexpr (PG) {
+#pragma unroll
+    for (int q = 0; q < SR; ++q) {
+      const int e = tid + q * 256;
+      if (e < G * kRows) sws[e] = sr[q];
+    }
+    for (int e = tid + SR * 256; e < G * kRows; e += 256) sws[e] = load_s(e);
+  }
+  __syncthreads();
+
+  float r = 0.0f;  // the chain of reference lane rl
+  auto consume = [&](int b0, const i32x2 (&wv)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (b0 + u >= nb) break;
+      const int k = (b0 + u) * 256 + 8 * rl;
+      const f32x4 xa = *reinterpret_cast<const f32x4*>(xs + k);
+      const f32x4 xb = *reinterpret_cast<const f32x4*>(xs + k + 4);
+      const float d = dot8f((uint32_t)wv[u][0], (uint32_t)wv[u][1], xa, xb);
+      if constexpr (PG) {
+        const float t = sws[(k / gs) * kRows + row_in_wg] * d;
+        r = r + t;
+      } else {
+        r = r + d;
+      }
+    }
+  };
+  for (int b = 0; b < nb; b += 2 * U) {
+    consume(b, wa);
+    if (b + U >= nb) break;
+    if (b + 2 * U < nb) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) wa[u] = load_w(b + 2 * U + u);
+    }
+    consume(b + U, wb);
+    if (b + 3 * U < nb) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) wb[u] = load_w(b + 3 * U + u);
+    }
+  }
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 32);
+  if (rl == 0 && live) {
+    float v;
+    if constexpr (PG) {
+      v = bias ? r + h2f(bias[n]) : r;
+    } else {
+      v = sw[n] * r;
+      if (bias) v = v + h2f(bias[n]);
+    }
+    y[n] = f2h(v);
+  }
+}
+
 namespace {
 
 constexpr int kMaxLdsK = 32768;  // x staged in LDS up to 64 KB
@@ -265,9 +412,39 @@ hipError_t pick_u(const uint16_t* x, const int8_t* w, const float* sw, const uin
 
 }  // namespace
 
+namespace {
+
+template <bool PG, int U>
+hipError_t run_wide(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
+                    uint16_t* y, int N, int K, int gs, size_t lds, hipStream_t s) {
+  mv_wide_kernel<PG, U><<<(N + 7) / 8, 256, lds, s>>>(x, w, sw, bias, y, N, K, gs);
+  return hipGetLastError();
+}
+
+template <bool PG>
+hipError_t pick_wide(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
+                     uint16_t* y, int N, int K, int gs, size_t lds, hipStream_t s) {
+  const int nb = K >> 8;
+  if (nb <= 8) return run_wide<PG, 4>(x, w, sw, bias, y, N, K, gs, lds, s);
+  if (nb <= 10) return run_wide<PG, 5>(x, w, sw, bias, y, N, K, gs, lds, s);
+  if (nb <= 12) return run_wide<PG, 6>(x, w, sw, bias, y, N, K, gs, lds, s);
+  if (nb <= 16) return run_wide<PG, 8>(x, w, sw, bias, y, N, K, gs, lds, s);
+  if (nb <= 24) return run_wide<PG, 12>(x, w, sw, bias, y, N, K, gs, lds, s);
+  return run_wide<PG, 16>(x, w, sw, bias, y, N, K, gs, lds, s);
+}
+
+}  // namespace
+
 hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,
                      hipStream_t s) {
+  if (K % 256 == 0 && K <= kMaxF32K && (((uintptr_t)w & 15) == 0) &&
+      (((uintptr_t)x & 15) == 0)) {
+    const int G = gs > 0 ? K / gs : 0;
+    const size_t lds = (size_t)K * sizeof(float) + (size_t)G * 8 * sizeof(float);
+    if (gs > 0) return pick_wide<true>(x, w, sw, bias, y, N, K, gs, lds, s);
+    return pick_wide<false>(x, w, sw, bias, y, N, K, gs, lds, s);
+  }
   // Rows per workgroup: 16 (4 waves) when N is large, down to 4 (one wave)
   // so that short-N shapes still launch >= 512 workgroups.
   int rows = 16;

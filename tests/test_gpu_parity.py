@@ -150,8 +150,12 @@ def test_perchannel_gemm_matches_linear():
     assert_bits_equal(H(y1), H(y2))
 
 
+# K % 256 == 0 up to 16384 runs the 32-lanes-per-row kernel (fp32 x in LDS;
+# one workgroup = 8 rows: N=8 exact, N=9 ragged); K=16640 the 16-lane kernel
+# with fp16 x; K=300 and K=8 the bounds-checked tail path.
 @pytest.mark.parametrize("N,K", [(40, 256), (130, 1024), (10240, 2560), (2560, 10240),
-                                 (100, 300), (7, 8)])
+                                 (100, 300), (7, 8), (8, 256), (9, 512), (100, 16384),
+                                 (33, 16640), (4096, 12288)])
 def test_perchannel_mv(N, K):
     x, w, sw, b = synth_pc(1, N, K, 500 + N + K)
     y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
@@ -221,6 +225,19 @@ def test_pergroup_linear(gs, M, N, K):
         assert_bits_equal(y, exp, f"pg gs{gs} {M}x{N}x{K}")
     else:
         assert_f16_close(y, exp, what=f"pg gs{gs} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+@pytest.mark.parametrize("N,K", [(9, 16384), (4096, 12288), (2560, 10240), (17, 256)])
+def test_pergroup_mv_shapes(gs, N, K):
+    if K % gs:
+        pytest.skip("K not a multiple of gs")
+    x = O.synth_activations(1, K, 60 + gs)
+    w = O.synth_weights_i8(N, K, 61 + N)
+    sw = O.synth_scales((K // gs, N), 62 + K)
+    b = (np.random.default_rng(63).standard_normal(N) * 0.1).astype(np.float16)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"pg mv gs{gs} {N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128])
