@@ -75,24 +75,35 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
   const int64_t c0 = (int64_t)c * kChunk;
   if (c0 >= n) return;  // uniform: nothing of this chunk is valid
 
+  // Issue every load of the chunk first (K for the scores, V for P.V: neither
+  // depends on the other), so the chunk costs one memory latency.  Positions
+  // past n (within T) are loaded and never used; 8-position groups wholly
+  // past n re-load group 0 of the chunk (always valid).
+  const int tq = tid & 15, dq = tid >> 4;  // scores: 8 positions x 8 dimensions
+  const int dv = tid & 15, ts = tid >> 4;  // P.V: 8 dimensions x 8 positions
+  const int64_t tk0 = c0 + 8 * tq, tv0 = c0 + 8 * ts;
+  i32x4 kv[8], vv[8];
+  {
+    const uint16_t* kp = kT + ((int64_t)j * kD + 8 * dq) * T + (tk0 < n ? tk0 : c0);
+#pragma unroll
+    for (int jd = 0; jd < 8; ++jd) kv[jd] = ld16(kp + (int64_t)jd * T);
+    const uint16_t* vp = vc + ((int64_t)j * T + (tv0 < n ? tv0 : c0)) * kD + 8 * dv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) vv[i] = ld16(vp + (int64_t)i * kD);
+  }
   for (int e = tid; e < G * kD; e += 256) qs[e / kD][e % kD] = h2f(q[(int64_t)y * G * kD + e]);
   __syncthreads();
 
   // ---- scores: thread (dq, tq) sums dimensions 8dq..8dq+7 for positions
   // c0 + 8tq .. +7
   {
-    const int tq = tid & 15, dq = tid >> 4;
-    const int64_t t0 = c0 + 8 * tq;
+    const int64_t t0 = tk0;
     float acc[G][8];
 #pragma unroll
     for (int r = 0; r < G; ++r)
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
     if (t0 < n) {
-      const uint16_t* kp = kT + ((int64_t)j * kD + 8 * dq) * T + t0;
-      i32x4 kv[8];
-#pragma unroll
-      for (int jd = 0; jd < 8; ++jd) kv[jd] = ld16(kp + (int64_t)jd * T);
 #pragma unroll
       for (int jd = 0; jd < 8; ++jd) {
         float kf[8];
@@ -141,18 +152,13 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
   // ---- P.V: thread (ts, dv) sums positions 8ts..8ts+7 for dimensions
   // 8dv..8dv+7
   {
-    const int dv = tid & 15, ts = tid >> 4;
     float acc[G][8];
 #pragma unroll
     for (int r = 0; r < G; ++r)
 #pragma unroll
       for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
-    const int64_t t0 = c0 + 8 * ts;
+    const int64_t t0 = tv0;
     if (t0 < n) {
-      const uint16_t* vp = vc + ((int64_t)j * T + t0) * kD + 8 * dv;
-      i32x4 vv[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) vv[i] = ld16(vp + (int64_t)i * kD);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         if (t0 + i >= n) break;  // invalid positions may hold anything
@@ -187,7 +193,10 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
   }
 }
 
-// One wave per query head: merges the chunks that hold valid positions.
+// One wave per query head merges the chunks that hold valid positions: lane c
+// reads chunk c's max and sum (64 chunks per pass), then every lane
+// accumulates its two output dimensions over the chunks with the weights
+// broadcast from the owning lane.
 template <int G>
 __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict__ ws,
                                                         const int64_t* __restrict__ n_ptr,
@@ -205,17 +214,45 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
     o[lane + 64] = 0;
     return;
   }
+  const float* base = ws + (int64_t)j * nchunk * G * (kD + 2);
+  constexpr int kStride = G * (kD + 2);
   float m = -INFINITY;
-  for (int c = 0; c < last; ++c)
-    m = fmaxf(m, ws[((int64_t)j * nchunk + c) * G * (kD + 2) + G * kD + r]);
+  for (int c = lane; c < last; c += 64) m = fmaxf(m, base[(int64_t)c * kStride + G * kD + r]);
+  m = wave_max_f(m);
   float l = 0.0f, a0 = 0.0f, a1 = 0.0f;
-  for (int c = 0; c < last; ++c) {
-    const float* p = ws + ((int64_t)j * nchunk + c) * G * (kD + 2);
-    const float f = expf(p[G * kD + r] - m);
-    l = l + f * p[G * kD + G + r];
-    a0 = a0 + f * p[r * kD + lane];
-    a1 = a1 + f * p[r * kD + lane + 64];
+  for (int c0 = 0; c0 < last; c0 += 64) {
+    const int c = c0 + lane;
+    float f = 0.0f;
+    if (c < last) {
+      const float* p = base + (int64_t)c * kStride;
+      f = expf(p[G * kD + r] - m);
+      l = l + f * p[G * kD + G + r];
+    }
+    const int cnt = last - c0 < 64 ? last - c0 : 64;
+    int i = 0;
+    for (; i + 4 <= cnt; i += 4) {  // four chunks' loads in flight
+      float fi[4], x0[4], x1[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float* p = base + (int64_t)(c0 + i + u) * kStride + r * kD;
+        fi[u] = __shfl(f, i + u);
+        x0[u] = p[lane];
+        x1[u] = p[lane + 64];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a0 = a0 + fi[u] * x0[u];
+        a1 = a1 + fi[u] * x1[u];
+      }
+    }
+    for (; i < cnt; ++i) {
+      const float* p = base + (int64_t)(c0 + i) * kStride + r * kD;
+      const float fi = __shfl(f, i);
+      a0 = a0 + fi * p[lane];
+      a1 = a1 + fi * p[lane + 64];
+    }
   }
+  l = wave_sum_f(l);
   o[lane] = f2h(a0 / l);
   o[lane + 64] = f2h(a1 / l);
 }

@@ -23,14 +23,17 @@
 // the fp16 y this kernel produces (same helpers), so q and sa are bit-identical
 // to the unfused pair of calls on that y.  The RMSNorm and SiLU steps are the
 // model's, not the reference library's; their fp32 sums run in a fixed order
-// (each lane in element order, then an xor butterfly).
+// (each lane in element order, then an xor butterfly over the wave, then the
+// waves in order when a workgroup shares a row).
 //
 // MI355X design: one 64-lane wave per row, 4 rows per workgroup.  A row of up
 // to 64 * 32 * 8 = 16384 elements stays in registers (NV 16-byte vectors per
 // lane) from the read through the reductions to the quantized store, so x is
 // read from HBM once and only q (1 byte/element) and sa go back; longer rows
 // stream from L2 a second and third time.  Reductions are wave-local
-// (shuffles, no LDS, no barrier).
+// (shuffles, no LDS, no barrier).  With at most 64 rows (decode) a row gets a
+// whole 256-thread workgroup instead (four waves, LDS for the cross-wave sum
+// and max), and SwiGLU without quantization is elementwise over the grid.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "quant_common.hpp"
@@ -228,6 +231,125 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Few rows (decode): one 256-thread workgroup per row, so a row's loads come
+// from four waves at once; the sums and maxima go through LDS in wave order.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_sum4(float v, float* red) {
+  const int wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // red may still be read from the previous reduction
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+__device__ __forceinline__ float block_max4(float v, float* red) {
+  const int wave = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+template <int NVB, bool ADD, bool WY, bool WQ>
+__global__ __launch_bounds__(256) void rmsnorm_row_kernel(
+    const uint16_t* x, const uint16_t* __restrict__ add, uint16_t* hsum,
+    const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ y,
+    int8_t* __restrict__ q, float* __restrict__ sa, int K) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int nvec = K >> 3;
+  const uint16_t* xr = x + row * K;
+  i32x4 v[NVB];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = tid + i * 256;
+    if (e < nvec) {
+      v[i] = ld16(xr + 8 * e);
+      if constexpr (ADD) {
+        v[i] = add8(v[i], ld16(add + row * K + 8 * e));
+        *reinterpret_cast<i32x4*>(hsum + row * K + 8 * e) = v[i];
+      }
+    } else {
+      v[i] = i32x4{0, 0, 0, 0};
+    }
+    ss = sumsq8(v[i], ss);
+  }
+  ss = block_sum4(ss, red);
+  const float r = 1.0f / sqrtf(ss / (float)K + eps);
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = tid + i * 256;
+    if (e < nvec) {
+      v[i] = norm8(v[i], ld16(w + 8 * e), r);
+      if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * K + 8 * e) = v[i];
+      amax = absmax8(v[i], amax);
+    }
+  }
+  if constexpr (WQ) {
+    amax = block_max4(amax, red);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (tid == 0) sa[row] = s;
+#pragma unroll
+    for (int i = 0; i < NVB; ++i) {
+      const int e = tid + i * 256;
+      if (e < nvec) *reinterpret_cast<i32x2*>(q + row * K + 8 * e) = quant8(v[i], inv);
+    }
+  }
+}
+
+template <int NVB, bool WY>
+__global__ __launch_bounds__(256) void silu_mul_row_kernel(
+    const uint16_t* __restrict__ gu, uint16_t* __restrict__ y, int8_t* __restrict__ q,
+    float* __restrict__ sa, int I) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int nvec = I >> 3;
+  const uint16_t* g = gu + row * 2 * I;
+  const uint16_t* u = g + I;
+  i32x4 v[NVB];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = tid + i * 256;
+    if (e < nvec) {
+      v[i] = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
+      if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v[i];
+      amax = absmax8(v[i], amax);
+    }
+  }
+  amax = block_max4(amax, red);
+  const float s = row_scale(amax);
+  const float inv = 1.0f / s;
+  if (tid == 0) sa[row] = s;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = tid + i * 256;
+    if (e < nvec) *reinterpret_cast<i32x2*>(q + row * I + 8 * e) = quant8(v[i], inv);
+  }
+}
+
+// SwiGLU without quantization: no row reduction, one 8-element vector per
+// thread over the whole [M, I] output.
+__global__ __launch_bounds__(256) void silu_mul_ew_kernel(const uint16_t* __restrict__ gu,
+                                                          uint16_t* __restrict__ y, int64_t M,
+                                                          int I) {
+  const int nvec = I >> 3;
+  const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (v >= M * nvec) return;
+  const int64_t row = v / nvec;
+  const int e = (int)(v % nvec);
+  const uint16_t* g = gu + row * 2 * I;
+  *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = swiglu8(ld16(g + 8 * e), ld16(g + I + 8 * e));
+}
+
+// ---------------------------------------------------------------------------
 // per-head q/k RMSNorm + RoPE + KV-cache write (head_dim 128)
 // ---------------------------------------------------------------------------
 // One wave per (token, head) of the fused projection row [q heads | k heads |
@@ -342,15 +464,73 @@ struct SwiRun {
 
 }  // namespace
 
+namespace {
+
+// rows at or below this count run one workgroup per row
+constexpr int kFewRows = 64;
+
+template <int NVB>
+hipError_t run_rms_row(const uint16_t* x, const uint16_t* add, uint16_t* hsum, const uint16_t* w,
+                       float eps, uint16_t* y, int8_t* q, float* sa, int M, int K, hipStream_t s) {
+  const int sel = (add ? 4 : 0) | (y ? 2 : 0) | (q ? 1 : 0);
+#define CIDER_RMSR(A, Y, Q)                                                              \
+  case (A ? 4 : 0) | (Y ? 2 : 0) | (Q ? 1 : 0):                                          \
+    rmsnorm_row_kernel<NVB, A, Y, Q><<<M, 256, 0, s>>>(x, add, hsum, w, eps, y, q, sa, K); \
+    break;
+  switch (sel) {
+    CIDER_RMSR(false, false, true)
+    CIDER_RMSR(false, true, false)
+    CIDER_RMSR(false, true, true)
+    CIDER_RMSR(true, false, true)
+    CIDER_RMSR(true, true, false)
+    CIDER_RMSR(true, true, true)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef CIDER_RMSR
+  return hipGetLastError();
+}
+
+template <int NVB>
+hipError_t run_swi_row(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
+                       hipStream_t s) {
+  if (y)
+    silu_mul_row_kernel<NVB, true><<<M, 256, 0, s>>>(gu, y, q, sa, I);
+  else
+    silu_mul_row_kernel<NVB, false><<<M, 256, 0, s>>>(gu, y, q, sa, I);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_rmsnorm(const uint16_t* x, const uint16_t* add, uint16_t* hsum,
                           const uint16_t* w, float eps, uint16_t* y, int8_t* q, float* sa, int M,
                           int K, hipStream_t s) {
-  return by_nv<RmsRun>(K >> 3, x, add, hsum, w, eps, y, q, sa, M, K, s);
+  const int nvec = K >> 3;
+  if (M <= kFewRows) {
+    if (nvec <= 256) return run_rms_row<1>(x, add, hsum, w, eps, y, q, sa, M, K, s);
+    if (nvec <= 512) return run_rms_row<2>(x, add, hsum, w, eps, y, q, sa, M, K, s);
+    if (nvec <= 1024) return run_rms_row<4>(x, add, hsum, w, eps, y, q, sa, M, K, s);
+    if (nvec <= 2048) return run_rms_row<8>(x, add, hsum, w, eps, y, q, sa, M, K, s);
+  }
+  return by_nv<RmsRun>(nvec, x, add, hsum, w, eps, y, q, sa, M, K, s);
 }
 
 hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
                            hipStream_t s) {
-  return by_nv<SwiRun>(I >> 3, gu, y, q, sa, M, I, s);
+  const int nvec = I >> 3;
+  if (!q) {
+    const int64_t total = (int64_t)M * nvec;
+    silu_mul_ew_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(gu, y, M, I);
+    return hipGetLastError();
+  }
+  if (M <= kFewRows) {
+    if (nvec <= 256) return run_swi_row<1>(gu, y, q, sa, M, I, s);
+    if (nvec <= 512) return run_swi_row<2>(gu, y, q, sa, M, I, s);
+    if (nvec <= 1024) return run_swi_row<4>(gu, y, q, sa, M, I, s);
+    if (nvec <= 2048) return run_swi_row<8>(gu, y, q, sa, M, I, s);
+  }
+  return by_nv<SwiRun>(nvec, gu, y, q, sa, M, I, s);
 }
 
 hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,
