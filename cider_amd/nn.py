@@ -133,7 +133,13 @@ class CiderLinear(torch.nn.Module):
                    device=None) -> "CiderLinear":
         """From a ``torch.nn.Linear`` (or any module with ``weight`` [N, K] and
         optional ``bias``): symmetric requant, per-channel unless
-        ``target_group_size`` is given (``cider/nn.py:173-192``)."""
+        ``target_group_size`` is given (``cider/nn.py:173-192``).  An
+        MLX-style affine-quantized layer (``weight`` words, ``scales``,
+        ``biases``, ``group_size``, ``bits``) is dequantized and requantized
+        as ``cider/nn.py:127-171`` does (``cider_amd.ingest.from_affine``)."""
+        if hasattr(layer, "scales") and hasattr(layer, "bits"):
+            from .ingest import from_affine
+            return from_affine(layer, target_group_size, device)
         if not hasattr(layer, "weight"):
             raise TypeError(f"Unsupported layer: {type(layer)}")
         weight = layer.weight.detach()
