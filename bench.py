@@ -51,6 +51,10 @@ def parse():
                     help="instead of the default line, print one JSON line for configs[3]: "
                          "Qwen3-8B-shaped W8A8 stack, 2048-token prefill + 128 greedy "
                          "decode steps (decode step captured as a HIP graph)")
+    ap.add_argument("--qwen3vl", action="store_true",
+                    help="instead of the default line, print one JSON line for configs[4]: "
+                         "Qwen3-VL-2B-shaped W8A8 text decoder, chunked prefill (512) of "
+                         "1334 / 2393 / 3455-token multimodal prompts, then graph decode")
     ap.add_argument("--torch-producers", action="store_true",
                     help="with --qwen3: run RMSNorm, SwiGLU, q/k norm + RoPE and decode "
                          "attention as PyTorch ops instead of the fused HIP kernels (A/B)")
@@ -102,6 +106,9 @@ def main():
         return
     if args.qwen3:
         bench_qwen3(torch, args, dev)
+        return
+    if args.qwen3vl:
+        bench_qwen3vl(torch, args, dev)
         return
     M, N, K = args.M, args.N, args.K
     x, w, sw, bias = synth_inputs(torch, M, N, K, args.seed, dev)
@@ -441,6 +448,72 @@ def bench_qwen3(torch, args, dev):
         "producers": ("pytorch ops" if args.torch_producers else
                       "fused HIP kernels (RMSNorm/SwiGLU + quantize, q/k norm + RoPE, "
                       "decode attention)"),
+        "build_s": round(build_s, 1),
+    }), flush=True)
+
+
+def bench_qwen3vl(torch, args, dev):
+    """random-init Qwen3-VL-2B-shaped text decoder
+    (cider_amd/qwen3vl.py), W8A8 per-channel projections, prompts of 1334 /
+    2393 / 3455 tokens with 2 / 3 / 4 synthetic 256-token image blocks at
+    3-axis M-RoPE positions, chunked prefill (chunk 512), then 64 greedy
+    decode steps per prompt, each one replay of the captured decode step."""
+    from cider_amd import qwen3vl as V
+    cfg = V.QWEN3_VL_2B
+    prompts = [(1334, 2), (2393, 3), (3455, 4)]
+    steps = 64
+    t0 = time.perf_counter()
+    m = V.Qwen3VL(cfg, max_len=max(p for p, _ in prompts) + steps + 1, seed=args.seed,
+                  device=dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    stream = torch.cuda.current_stream(dev)
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    rows = []
+    for i, (L, n_img) in enumerate(prompts):
+        segs = V.synth_segments(L, n_img, args.seed + i)
+        x, _ = m.embed_prompt(segs, seed=args.seed + i)
+        pos3 = V.rope_index(segs)
+        m.prefill_chunked(x, pos3)      # warm-up (also fills the cache)
+        torch.cuda.synchronize()
+        reps = 3
+        e[0].record(stream)
+        for _ in range(reps):
+            logits = m.prefill_chunked(x, pos3)
+        e[1].record(stream)
+        torch.cuda.synchronize()
+        pre_ms = e[0].elapsed_time(e[1]) / reps
+        first = torch.argmax(logits[-1].float()).reshape(1)
+        state = {"tok": first.clone(), "pos": torch.tensor([L], device=dev),
+                 "i": torch.zeros(1, dtype=torch.int64, device=dev),
+                 "out": torch.zeros(steps, dtype=torch.int64, device=dev)}
+        g, _ = m.capture_decode(state)
+        e[0].record(stream)
+        for _ in range(steps):
+            g.replay()
+        e[1].record(stream)
+        torch.cuda.synchronize()
+        dec_ms = e[0].elapsed_time(e[1]) / steps
+        rows.append({"prompt_tokens": L, "images": n_img,
+                     "prefill_ms": round(pre_ms, 3),
+                     "prefill_tokens_per_s": round(L / pre_ms * 1e3, 1),
+                     "decode_ms_per_token": round(dec_ms, 4),
+                     "decode_tokens_per_s": round(1e3 / dec_ms, 1),
+                     "tokens_distinct": int(state["out"].unique().numel())})
+    print(json.dumps({
+        "metric": "Qwen3-VL-2B-shaped W8A8 text decoder: chunked-prefill tokens/s and decode "
+                  "tokens/s at 1334 / 2393 / 3455-token multimodal prompts",
+        "value": rows[-1]["prefill_tokens_per_s"], "unit": "tokens/s (prefill, 3455 tokens)",
+        "higher_is_better": True, "n_gpus": 1, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "configs[4]: 28 layers, hidden 2048, intermediate 6144, 16 q / 8 kv "
+                               "heads of 128, vocab 151936 (tied fp16 lm_head), random init; "
+                               "text ids + 256-token fp16 N(0,0.02) image blocks at M-RoPE "
+                               "positions; chunk 512; 64 graph-replayed greedy decode steps",
+                   "seed": args.seed},
+        "prompts": rows,
+        "reference_m5pro_w8a8_pc": {"prefill_tokens_per_s": [3242, 2983, 2796],
+                                    "decode_tokens_per_s": [104, 100, 95],
+                                    "note": "different hardware and the full VLM service"},
         "build_s": round(build_s, 1),
     }), flush=True)
 

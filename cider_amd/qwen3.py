@@ -199,14 +199,17 @@ class Qwen3Layer(torch.nn.Module):
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
         return b.h, self.down.forward_quantized(qd, sd)
 
-    def decode_fused(self, x, pending, tables, pos, n_valid, kT_cache, v_cache, ws):
-        """One token x [1, hidden] (+ pending) at device position `pos`
-        ([1] int64), attending over n_valid = pos + 1 cache positions."""
+    def decode_fused(self, x, pending, tables, pos, n_valid, kT_cache, v_cache, ws,
+                     rope_pos=None):
+        """One token x [1, hidden] (+ pending) at device cache slot `pos`
+        ([1] int64; RoPE row `rope_pos`, default pos), attending over
+        n_valid = pos + 1 cache positions."""
         c = self.cfg
         a = self._norm(x, pending, self.input_norm, True, False)
         qkv = self.qkv(a.y)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
-                            pos, pos, kT_cache, v_cache, c.num_heads, c.num_kv_heads)
+                            pos if rope_pos is None else rope_pos, pos, kT_cache, v_cache,
+                            c.num_heads, c.num_kv_heads)
         attn = FK.attn_decode(q, kT_cache, v_cache, n_valid, 1.0 / math.sqrt(c.head_dim), ws=ws)
         b = self._norm(a.h, self.o(attn.reshape(1, -1)), self.post_norm, True, False)
         h, _, _ = FK.silu_mul_quantize(self.gate_up(b.y), want_y=True, want_q=False)
@@ -251,6 +254,10 @@ class Qwen3(torch.nn.Module):
         self.v_cache = torch.zeros(cfg.num_layers, kv, cap, d, dtype=torch.float16,
                                    device=dev)
         self._attn_ws = FK.attn_decode_workspace(cfg.num_heads, cap, dev) if fused else None
+        # RoPE row = cache slot + this offset in decode (device [1] int64; None
+        # = 0); multimodal prompts whose M-RoPE positions run behind their
+        # length set it after prefill
+        self._rope_delta = None
         self._graph = None
 
     # ---- prefill ----------------------------------------------------------
@@ -287,11 +294,15 @@ class Qwen3(torch.nn.Module):
         x = self.embed.index_select(0, tok)
         if self.fused:
             n_valid = pos + 1
+            rope_pos = None if self._rope_delta is None else pos + self._rope_delta
             pending = None
             for i, layer in enumerate(self.layers):
                 x, pending = layer.decode_fused(x, pending, (self.cos, self.sin), pos, n_valid,
-                                                self.kT_cache[i], self.v_cache[i], self._attn_ws)
+                                                self.kT_cache[i], self.v_cache[i], self._attn_ws,
+                                                rope_pos)
             return F.linear(self._final_norm(x, pending), self.lm_head)
+        if self._rope_delta is not None:
+            raise ValueError("decode_step: a RoPE position offset needs fused=True")
         cos = self.cos.index_select(0, pos)[:, None, :]
         sin = self.sin.index_select(0, pos)[:, None, :]
         ar = torch.arange(self.capacity, device=self.device)
