@@ -8,6 +8,8 @@
 // caller's workspace, and applies the reference's dispatch policy:
 //   W8 per-channel / per-group: M == 1 -> fp16 MV, otherwise quantize -> GEMM
 //   W4A8: always quantize -> GEMM (M == 1 included)
+// For decode-sized M (<= 4) "quantize -> GEMM" is one GEMV kernel that
+// quantizes while staging x (identical q and scale_a).
 // The GEMM launcher picks the tile shape from M (skinny for M <= 64); the
 // choice never changes results on the integer path.
 #include <stdarg.h>
@@ -84,6 +86,20 @@ int check_ws(const char* fn, const void* ws, size_t ws_bytes, size_t needed) {
   if (((uintptr_t)ws & 255) != 0)
     return fail(CIDER_E_INVALID, "%s: workspace must be 256-byte aligned", fn);
   return CIDER_OK;
+}
+
+// Decode-sized calls (M <= 4, K <= 16384, aligned) run one GEMV kernel that
+// quantizes x per token while staging it (same helpers as the quantize
+// kernel, so the same q and scale_a) instead of a quantize launch followed by
+// a GEMM launch.  Returns true and the launch status in *rc if it ran.
+bool try_fused_gemv(const char* fn, const void* x, const cider::GemmArgs& g, int wf, int epi,
+                    int gs, hipStream_t s, int* rc) {
+  cider::GemmArgs t = g;
+  t.x = reinterpret_cast<const int8_t*>(x);
+  if (!cider::gemv_q_supported(t, wf, true)) return false;
+  *rc = hip_status(cider::launch_gemv_qx(reinterpret_cast<const uint16_t*>(x), g, wf, epi, gs, s),
+                   fn);
+  return true;
 }
 
 // Quantizes x into the workspace; returns q and sa pointers.
@@ -183,6 +199,9 @@ int cider_perchannel_linear(const void* x_f16, const int8_t* w_nk, const float* 
                                        reinterpret_cast<uint16_t*>(y_f16), (int)N, (int)K, 0, s),
                       fn);
   CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int rc;
+  const cider::GemmArgs gf{nullptr, w_nk, nullptr, sw, bias, y_f16, (int)M, (int)N, (int)K};
+  if (try_fused_gemv(fn, x_f16, gf, cider::W_I8, cider::EPI_PC, 0, s, &rc)) return rc;
   int8_t* q;
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
@@ -214,6 +233,9 @@ int cider_pergroup_linear(const void* x_f16, const int8_t* w_nk, const float* sw
                                        group_size, s),
                       fn);
   CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int rc;
+  const cider::GemmArgs gf{nullptr, w_nk, nullptr, sw_gn, bias, y_f16, (int)M, (int)N, (int)K};
+  if (try_fused_gemv(fn, x_f16, gf, cider::W_I8, cider::EPI_PG, group_size, s, &rc)) return rc;
   int8_t* q;
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
@@ -249,6 +271,9 @@ int cider_w4a8_linear(const void* x_f16, const uint8_t* w4_nk, const float* sw, 
   CIDER_TRY(need(fn, y_f16, "y", true));
   const hipStream_t s = (hipStream_t)stream;
   CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int rc;
+  const cider::GemmArgs gf{nullptr, w4_nk, nullptr, sw, nullptr, y_f16, (int)M, (int)N, (int)K};
+  if (try_fused_gemv(fn, x_f16, gf, cider::W_I4, cider::EPI_PC, 0, s, &rc)) return rc;
   int8_t* q;
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
@@ -274,6 +299,11 @@ int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
   CIDER_TRY(need(fn, y_f16, "y", true));
   const hipStream_t s = (hipStream_t)stream;
   CIDER_TRY(check_ws(fn, ws, ws_bytes, quant_ws_bytes(M, K)));
+  int rc;
+  const cider::GemmArgs gf{nullptr, w4_nk, nullptr, scale_gn_f16,
+                           reinterpret_cast<const uint16_t*>(bias_f16), y_f16, (int)M, (int)N,
+                           (int)K};
+  if (try_fused_gemv(fn, x_f16, gf, cider::W_I4, cider::EPI_PG, group_size, s, &rc)) return rc;
   int8_t* q;
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));

@@ -369,6 +369,7 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                        int gs, hipStream_t s) {
+  if (gemv_q_supported(a, wf, false)) return launch_gemv_q(a, wf, epi, gs, s);
   if (a.M <= 64) return launch_skinny(a, wf, epi, sw_half, gs, s);
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&

@@ -29,6 +29,14 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
 hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                        int gs, hipStream_t s);
 
+// Decode-sized GEMV on quantized activations (1 <= M <= 4), gemv_q.hip.
+bool gemv_q_supported(const GemmArgs& a, int wf, bool fused);
+hipError_t launch_gemv_q(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s);
+// Same, on fp16 activations x [M, K] quantized per token inside the kernel
+// (a.x and a.sa are ignored).
+hipError_t launch_gemv_qx(const uint16_t* x, const GemmArgs& a, int wf, int epi, int gs,
+                          hipStream_t s);
+
 // M == 1 fp16-activation MV (per-channel when gs == 0, else per-group).
 hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,

@@ -8,7 +8,8 @@
 //
 // MI355X design: one 64-lane wavefront owns one row, so the absmax is a pure
 // cross-lane reduction (no LDS, no barrier); a workgroup of 4 waves handles 4
-// rows.  Rows of up to 64*8*32 = 16384 elements stay in registers between the
+// rows.  Up to 64 rows (decode-sized batches) get a 1024-thread workgroup per
+// row instead.  Rows of up to 64*8*32 = 16384 elements stay in registers between the
 // absmax and the quantize pass (each element is read from HBM once); longer
 // rows are re-read, which hits in L2.
 #include "common.hpp"
@@ -58,6 +59,44 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(
   }
 }
 
+// Few rows (M <= 64): one 1024-thread workgroup per row, so sixteen waves
+// share a row's loads and conversions (a single wave per row leaves the
+// row's VALU work serial: about 8 us at K = 12288); the absmax goes through
+// LDS in wave order.  Vectorized rows only; NV 16-byte vectors per thread.
+template <int NV>
+__global__ __launch_bounds__(1024) void quantize_row_kernel(
+    const uint16_t* __restrict__ x, int8_t* __restrict__ q,
+    float* __restrict__ sa, int K) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * K;
+  int8_t* qr = q + row * K;
+  const int nvec = K >> 3;
+  i32x4 v[NV];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + i * 1024;
+    v[i] = e < nvec ? ld16(xr + 8 * e) : i32x4{0, 0, 0, 0};
+    amax = absmax8(v[i], amax);
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) amax = fmaxf(amax, red[w]);
+  const float s = row_scale(amax);
+  const float inv = 1.0f / s;
+  if (tid == 0) sa[row] = s;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = tid + i * 1024;
+    if (e < nvec) *reinterpret_cast<i32x2*>(qr + 8 * e) = quant8(v[i], inv);
+  }
+}
+
 // Any K and alignment: element-wise, two passes.
 __global__ __launch_bounds__(256) void quantize_scalar_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q,
@@ -85,7 +124,21 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
     quantize_scalar_kernel<<<grid, block, 0, s>>>(x, q, sa, M, K);
     return hipGetLastError();
   }
-  const int per_lane = ((K >> 3) + kWave - 1) / kWave;
+  const int nvec = K >> 3;
+  if (M <= 64 && nvec > 64 && nvec <= 8 * 1024) {
+    // a row per 1024-thread workgroup (max(a, b) is exact, so the absmax does
+    // not depend on how the row is split)
+    if (nvec <= 1024)
+      quantize_row_kernel<1><<<M, 1024, 0, s>>>(x, q, sa, K);
+    else if (nvec <= 2048)
+      quantize_row_kernel<2><<<M, 1024, 0, s>>>(x, q, sa, K);
+    else if (nvec <= 4096)
+      quantize_row_kernel<4><<<M, 1024, 0, s>>>(x, q, sa, K);
+    else
+      quantize_row_kernel<8><<<M, 1024, 0, s>>>(x, q, sa, K);
+    return hipGetLastError();
+  }
+  const int per_lane = (nvec + kWave - 1) / kWave;
   if (per_lane <= 1)
     quantize_vec_kernel<1><<<grid, block, 0, s>>>(x, q, sa, M, K);
   else if (per_lane <= 2)

@@ -220,11 +220,8 @@ def test_pergroup_linear(gs, M, N, K):
     sw = O.synth_scales((K // gs, N), 42 + K)
     b = (np.random.default_rng(43).standard_normal(N) * 0.1).astype(np.float16)
     y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
-    exp = O.pergroup_linear(x, w, sw, gs, b)
-    if M > 64 or M == 1:
-        assert_bits_equal(y, exp, f"pg gs{gs} {M}x{N}x{K}")
-    else:
-        assert_f16_close(y, exp, what=f"pg gs{gs} {M}x{N}x{K}")
+    # every M keeps the reference's sequential group chain: bit-exact
+    assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"pg gs{gs} {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128, 256])
@@ -305,11 +302,7 @@ def test_w4a8_pergroup(gs, M, N, K):
     packed = O.pack_w4_lo_first(w4)
     sc = O.synth_scales((K // gs, N), 72 + K).astype(np.float16)
     y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
-    exp = O.w4a8_pergroup_linear(x, packed, sc, gs)
-    if M > 64:
-        assert_bits_equal(y, exp, f"w4g gs{gs} {M}x{N}x{K}")
-    else:
-        assert_f16_close(y, exp, what=f"w4g gs{gs} {M}x{N}x{K}")
+    assert_bits_equal(y, O.w4a8_pergroup_linear(x, packed, sc, gs), f"w4g gs{gs} {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128])
@@ -323,6 +316,71 @@ def test_w4a8_pergroup_full_size_rows(gs):
     rows = np.r_[0:16, M - 16:M]
     exp = O.w4a8_pergroup_linear(x[rows], packed, sc, gs)
     assert_bits_equal(y[rows], exp, f"w4g gs{gs} full-size rows")
+
+
+# Decode-sized GEMV on quantized activations (M <= 4, K <= 16384, K % 16 == 0
+# for int8 / % 32 for int4): one wave per weight row, v_dot4 products; N=17
+# leaves most waves of the last workgroup without a row.
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(17, 256), (300, 2560), (1024, 16384), (64, 12288)])
+def test_gemv_q_exact(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 100 + M + N)
+    if M > 1:  # M == 1 on W8 runs the fp16 MV
+        y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
+        assert_bits_equal(y, O.perchannel_linear(x, w, sw, b), f"gemv pc {M}x{N}x{K}")
+        for gs in (64, 128, 256):
+            swg = O.synth_scales((K // gs, N), 101 + gs)
+            yg = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
+            assert_bits_equal(yg, O.pergroup_linear(x, w, swg, gs, b), f"gemv pg{gs} {M}x{N}x{K}")
+    q = np.random.default_rng(102).integers(-128, 128, (M, K), dtype=np.int8)
+    assert np.array_equal(C.int8_matmul_int32(T(q), T(w)).cpu().numpy(),
+                          O.int8_matmul_int32(q, w)), f"gemv i32 {M}x{N}x{K}"
+    wf = np.random.default_rng(103).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    assert_bits_equal(H(C.w4a8_linear(T(x), T(packed), T(sw4))),
+                      O.w4a8_linear(x, packed, sw4), f"gemv w4 {M}x{N}x{K}")
+    w4 = np.random.default_rng(104).integers(-8, 8, (N, K), dtype=np.int8)
+    for gs in (64, 128):
+        sc = O.synth_scales((K // gs, N), 105 + gs).astype(np.float16)
+        pk = O.pack_w4_lo_first(w4)
+        assert_bits_equal(H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b))),
+                          O.w4a8_pergroup_linear(x, pk, sc, gs, b), f"gemv w4g{gs} {M}x{N}x{K}")
+
+
+# Skinny kernel (M <= 64) at shapes where N alone gives few workgroups, so the
+# K range is split over 8 or 16 waves per workgroup (int32 sums exact in any
+# order); per-group deals the groups to the waves round-robin and keeps the
+# sequential group chain, so it is bit-exact too (K = 12288 at gs = 64: 192
+# groups, a chain long enough for any other order to show).
+@pytest.mark.parametrize("M,N,K", [(16, 2560, 10240), (32, 1024, 8192), (3, 256, 16384),
+                                   (64, 512, 4096)])
+def test_skinny_wave_splits_exact(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 90 + M)
+    y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
+    assert_bits_equal(y, O.perchannel_linear(x, w, sw, b), f"skinny pc {M}x{N}x{K}")
+    q = np.random.default_rng(91).integers(-128, 128, (M, K), dtype=np.int8)
+    c = C.int8_matmul_int32(T(q), T(w)).cpu().numpy()
+    assert np.array_equal(c, O.int8_matmul_int32(q, w)), f"skinny i32 {M}x{N}x{K}"
+    wf = np.random.default_rng(92).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    y4 = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+    assert_bits_equal(y4, O.w4a8_linear(x, packed, sw4), f"skinny w4 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 12288), (16, 4096, 12288), (5, 2560, 10240)])
+def test_skinny_wave_splits_pergroup(gs, M, N, K):
+    x = O.synth_activations(M, K, 93 + M)
+    w4 = np.random.default_rng(94).integers(-8, 8, (N, K), dtype=np.int8)
+    sc = O.synth_scales((K // gs, N), 95).astype(np.float16)
+    y = H(C.w4a8_pergroup_linear(T(x), T(O.pack_w4_lo_first(w4)), T(sc), gs))
+    assert_bits_equal(y, O.w4a8_pergroup_linear(x, O.pack_w4_lo_first(w4), sc, gs),
+                      f"skinny w4g gs{gs} {M}x{N}x{K}")
+    if M > 1:
+        w = O.synth_weights_i8(N, K, 96)
+        sw = O.synth_scales((K // gs, N), 97)
+        y8 = H(C.pergroup_linear(T(x), T(w), T(sw), gs))
+        assert_bits_equal(y8, O.pergroup_linear(x, w, sw, gs), f"skinny pg gs{gs} {M}x{N}x{K}")
 
 
 # --------------------------------------------------------------------------
