@@ -230,7 +230,7 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
             "weight_copies": copies, "calls": iters, "us_per_call": round(avg * 1e3, 3),
             "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
             "peak_gbs": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "bound": "hbm", "kernel": "mv_kernel<per-channel>"}
+            "bound": "hbm", "kernel": "mv_wide_kernel<per-channel> (cider_amd/csrc/gemv.hip)"}
 
 
 def sweep(torch, args, dev):
