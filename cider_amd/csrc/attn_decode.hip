@@ -1,9 +1,9 @@
 // Single-query (decode) attention over a KV cache, grouped-query heads.
 //
 //   for query head h = j * G + r of KV head j (G = H / KV):
-//     s_t = scale * sum_d f32(q[h,d]) * f32(K[j,d,t])        t < n
+//     s_t = scale * sum_d f32(q[h,d]) * f32(K[j,t,d])        t < n
 //     o   = sum_t softmax(s)_t * f32(V[j,t,d])               -> fp16 [H, D]
-// with the K cache transposed ([KV, D, T]) and V row-major ([KV, T, D]); n,
+// with both caches [KV, T, D] (position-major, 256 bytes per position); n,
 // the number of valid positions, is read from device memory so a captured
 // decode step replays unchanged while the sequence grows.  All arithmetic is
 // fp32 (the reference's models call MLX's fused SDPA here, whose
@@ -16,9 +16,9 @@
 //     scores, its max m_c, sum l_c and unnormalised output o_c (fp32) and
 //     writes them to a workspace; a second kernel merges the chunks with the
 //     usual max-rescaling.  Each K / V byte is read once for all G heads.
-//   * scores: a thread owns 8 consecutive positions (one 16-byte load per
-//     head dimension from the transposed K) and 8 of the 128 dimensions;
-//     the 16 dimension slices are summed through LDS.
+//   * scores: a thread owns 8 consecutive positions and 8 of the 128
+//     dimensions (one 16-byte K load per position); the 16 dimension slices
+//     are summed through LDS.
 //   * P.V: a thread owns 8 dimensions (one 16-byte V load per position) and
 //     8 positions; the 16 position slices are summed through LDS.
 //   * the grid covers the cache capacity T; chunks at or past n exit at once
@@ -61,7 +61,7 @@ __device__ __forceinline__ void unpack8(i32x4 v, float (&f)[8]) {
 // o_c[G][kD], m_c[G], l_c[G]
 template <int G, int R>
 __global__ __launch_bounds__(256) void attn_chunk_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kT,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int64_t* __restrict__ n_ptr, float scale,
     float* __restrict__ ws, int64_t T, int nchunk) {
   __shared__ float qs[G][kD];
@@ -84,9 +84,9 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
   const int64_t tk0 = c0 + 8 * tq, tv0 = c0 + 8 * ts;
   i32x4 kv[8], vv[8];
   {
-    const uint16_t* kp = kT + ((int64_t)j * kD + 8 * dq) * T + (tk0 < n ? tk0 : c0);
+    const uint16_t* kp = kc + ((int64_t)j * T + (tk0 < n ? tk0 : c0)) * kD + 8 * dq;
 #pragma unroll
-    for (int jd = 0; jd < 8; ++jd) kv[jd] = ld16(kp + (int64_t)jd * T);
+    for (int i = 0; i < 8; ++i) kv[i] = ld16(kp + (int64_t)i * kD);
     const uint16_t* vp = vc + ((int64_t)j * T + (tv0 < n ? tv0 : c0)) * kD + 8 * dv;
 #pragma unroll
     for (int i = 0; i < 8; ++i) vv[i] = ld16(vp + (int64_t)i * kD);
@@ -105,14 +105,13 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
       for (int i = 0; i < 8; ++i) acc[r][i] = 0.0f;
     if (t0 < n) {
 #pragma unroll
-      for (int jd = 0; jd < 8; ++jd) {
-        float kf[8];
-        unpack8(kv[jd], kf);
+      for (int i = 0; i < 8; ++i) {
+        float kf[8];  // dimensions 8dq .. 8dq + 7 of position t0 + i
+        unpack8(kv[i], kf);
 #pragma unroll
         for (int r = 0; r < G; ++r) {
-          const float qd = qs[r][8 * dq + jd];
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[r][i] = acc[r][i] + qd * kf[i];
+          for (int jd = 0; jd < 8; ++jd) acc[r][i] = acc[r][i] + qs[r][8 * dq + jd] * kf[jd];
         }
       }
     }
@@ -258,10 +257,10 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(const float* __restrict_
 }
 
 template <int G, int R>
-hipError_t run_attn(const uint16_t* q, const uint16_t* kT, const uint16_t* vc, const int64_t* n,
+hipError_t run_attn(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const int64_t* n,
                     float scale, float* ws, uint16_t* out, int KV, int64_t T, hipStream_t s) {
   const int nchunk = (int)((T + kChunk - 1) / kChunk);
-  attn_chunk_kernel<G, R><<<dim3(nchunk, KV * R), 256, 0, s>>>(q, kT, vc, n, scale, ws, T,
+  attn_chunk_kernel<G, R><<<dim3(nchunk, KV * R), 256, 0, s>>>(q, kc, vc, n, scale, ws, T,
                                                                 nchunk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -276,14 +275,14 @@ size_t attn_decode_ws_floats(int H, int64_t T) {
   return (size_t)(nchunk * H * (kD + 2));
 }
 
-hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kT, const uint16_t* vc,
+hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                               const int64_t* n, float scale, float* ws, uint16_t* out, int H,
                               int KV, int64_t T, hipStream_t s) {
   switch (H / KV) {
-    case 1: return run_attn<1, 1>(q, kT, vc, n, scale, ws, out, KV, T, s);
-    case 2: return run_attn<2, 1>(q, kT, vc, n, scale, ws, out, KV, T, s);
-    case 4: return run_attn<4, 1>(q, kT, vc, n, scale, ws, out, KV, T, s);
-    case 8: return run_attn<4, 2>(q, kT, vc, n, scale, ws, out, KV, T, s);
+    case 1: return run_attn<1, 1>(q, kc, vc, n, scale, ws, out, KV, T, s);
+    case 2: return run_attn<2, 1>(q, kc, vc, n, scale, ws, out, KV, T, s);
+    case 4: return run_attn<4, 1>(q, kc, vc, n, scale, ws, out, KV, T, s);
+    case 8: return run_attn<4, 2>(q, kc, vc, n, scale, ws, out, KV, T, s);
     default: return hipErrorInvalidValue;
   }
 }

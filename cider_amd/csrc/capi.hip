@@ -377,7 +377,7 @@ int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* s
 int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16, const void* k_norm_w_f16,
                        float eps, const void* cos_f16, const void* sin_f16, int64_t P,
                        const int64_t* rope_row, const int64_t* slot, void* q_out_f16,
-                       void* kT_cache_f16, void* v_cache_f16, int64_t L, int64_t H, int64_t KV,
+                       void* k_cache_f16, void* v_cache_f16, int64_t L, int64_t H, int64_t KV,
                        int64_t D, int64_t T, void* stream) {
   static const char* fn = "cider_qk_norm_rope";
   if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
@@ -395,7 +395,7 @@ int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16, const void
   CIDER_TRY(need(fn, rope_row, "rope_row", true));
   CIDER_TRY(need(fn, slot, "slot", true));
   CIDER_TRY(need(fn, q_out_f16, "q_out", true));
-  CIDER_TRY(need(fn, kT_cache_f16, "kT_cache", true));
+  CIDER_TRY(need(fn, k_cache_f16, "k_cache", true));
   CIDER_TRY(need(fn, v_cache_f16, "v_cache", true));
   return hip_status(
       cider::launch_qk_norm_rope(
@@ -404,7 +404,7 @@ int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16, const void
           reinterpret_cast<const uint16_t*>(k_norm_w_f16), eps,
           reinterpret_cast<const uint16_t*>(cos_f16), reinterpret_cast<const uint16_t*>(sin_f16),
           P, rope_row, slot, reinterpret_cast<uint16_t*>(q_out_f16),
-          reinterpret_cast<uint16_t*>(kT_cache_f16), reinterpret_cast<uint16_t*>(v_cache_f16),
+          reinterpret_cast<uint16_t*>(k_cache_f16), reinterpret_cast<uint16_t*>(v_cache_f16),
           (int)L, (int)H, (int)KV, T, (hipStream_t)stream),
       fn);
 }
@@ -414,7 +414,7 @@ size_t cider_attn_decode_workspace_bytes(int64_t H, int64_t T) {
   return align256(cider::attn_decode_ws_floats((int)H, T) * sizeof(float));
 }
 
-int cider_attn_decode(const void* q_f16, const void* kT_cache_f16, const void* v_cache_f16,
+int cider_attn_decode(const void* q_f16, const void* k_cache_f16, const void* v_cache_f16,
                       const int64_t* n_valid, float scale, void* ws, size_t ws_bytes,
                       void* out_f16, int64_t H, int64_t KV, int64_t D, int64_t T, void* stream) {
   static const char* fn = "cider_attn_decode";
@@ -427,16 +427,16 @@ int cider_attn_decode(const void* q_f16, const void* kT_cache_f16, const void* v
     return fail(CIDER_E_INVALID, "%s: cache capacity T=%lld must be a positive multiple of 8",
                 fn, (long long)T);
   CIDER_TRY(need(fn, q_f16, "q", true));
-  CIDER_TRY(need(fn, kT_cache_f16, "kT_cache", true));
+  CIDER_TRY(need(fn, k_cache_f16, "k_cache", true));
   CIDER_TRY(need(fn, v_cache_f16, "v_cache", true));
   CIDER_TRY(need(fn, n_valid, "n_valid", true));
   CIDER_TRY(need(fn, out_f16, "out", true));
   CIDER_TRY(check_ws(fn, ws, ws_bytes, cider_attn_decode_workspace_bytes(H, T)));
-  if (!aligned16(q_f16) || !aligned16(kT_cache_f16) || !aligned16(v_cache_f16))
+  if (!aligned16(q_f16) || !aligned16(k_cache_f16) || !aligned16(v_cache_f16))
     return fail(CIDER_E_INVALID, "%s: q and the caches must be 16-byte aligned", fn);
   return hip_status(
       cider::launch_attn_decode(reinterpret_cast<const uint16_t*>(q_f16),
-                                reinterpret_cast<const uint16_t*>(kT_cache_f16),
+                                reinterpret_cast<const uint16_t*>(k_cache_f16),
                                 reinterpret_cast<const uint16_t*>(v_cache_f16), n_valid, scale,
                                 reinterpret_cast<float*>(ws), reinterpret_cast<uint16_t*>(out_f16),
                                 (int)H, (int)KV, T, (hipStream_t)stream),

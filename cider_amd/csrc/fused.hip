@@ -17,7 +17,7 @@
 //                   q and k over head_dim (own weights), rotate-half RoPE
 //                   (q*cos + rot(q)*sin, each product and the sum rounded to
 //                   fp16), q to a [L, H, D] buffer, k and v straight into the
-//                   KV cache (K transposed [KV, D, T], V [KV, T, D]).
+//                   KV caches (both [KV, T, D]).
 //
 // The quantization of y is exactly the library's quantize_per_token applied to
 // the fp16 y this kernel produces (same helpers), so q and sa are bit-identical
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, float eps, const uint16_t* __restrict__ cos_t,
     const uint16_t* __restrict__ sin_t, int64_t P, const int64_t* __restrict__ rope_row,
-    const int64_t* __restrict__ slot, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kT,
+    const int64_t* __restrict__ slot, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int L, int H, int KV, int64_t T) {
   constexpr int D = 128;
   const int lane = threadIdx.x & 63;
@@ -400,9 +400,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
   } else {
     const int64_t p = slot[t];
     if (p < 0 || p >= T) return;
-    uint16_t* dst = kT + (int64_t)(hh - H) * D * T + p;
-    dst[(int64_t)lane * T] = o0;
-    dst[(int64_t)(lane + 64) * T] = o1;
+    uint16_t* dst = kc + ((int64_t)(hh - H) * T + p) * D;
+    dst[lane] = o0;
+    dst[lane + 64] = o1;
   }
 }
 
@@ -536,12 +536,12 @@ hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa
 hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,
                                float eps, const uint16_t* cos_t, const uint16_t* sin_t, int64_t P,
                                const int64_t* rope_row, const int64_t* slot, uint16_t* q_out,
-                               uint16_t* kT, uint16_t* vc, int L, int H, int KV, int64_t T,
+                               uint16_t* kc, uint16_t* vc, int L, int H, int KV, int64_t T,
                                hipStream_t s) {
   const int64_t waves = (int64_t)L * (H + 2 * KV);
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
   qk_norm_rope_kernel<<<grid, block, 0, s>>>(qkv, qw, kw, eps, cos_t, sin_t, P, rope_row, slot,
-                                             q_out, kT, vc, L, H, KV, T);
+                                             q_out, kc, vc, L, H, KV, T);
   return hipGetLastError();
 }
 

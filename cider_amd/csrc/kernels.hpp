@@ -53,12 +53,12 @@ hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa
 hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,
                                float eps, const uint16_t* cos_t, const uint16_t* sin_t, int64_t P,
                                const int64_t* rope_row, const int64_t* slot, uint16_t* q_out,
-                               uint16_t* kT, uint16_t* vc, int L, int H, int KV, int64_t T,
+                               uint16_t* kc, uint16_t* vc, int L, int H, int KV, int64_t T,
                                hipStream_t s);
 
 // Single-query attention over a KV cache (attn_decode.hip).
 size_t attn_decode_ws_floats(int H, int64_t T);
-hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kT, const uint16_t* vc,
+hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                               const int64_t* n, float scale, float* ws, uint16_t* out, int H,
                               int KV, int64_t T, hipStream_t s);
 

@@ -95,28 +95,28 @@ def silu_mul_quantize(gate_up: torch.Tensor, want_y: bool = True, want_q: bool =
 
 def qk_norm_rope(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor,
                  eps: float, cos: torch.Tensor, sin: torch.Tensor, rope_row: torch.Tensor,
-                 slot: torch.Tensor, kT_cache: torch.Tensor, v_cache: torch.Tensor,
+                 slot: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                  num_heads: int, num_kv_heads: int, q_out: Optional[torch.Tensor] = None,
                  stream=None) -> torch.Tensor:
     """Per-head q/k RMSNorm + rotate-half RoPE over a fused projection
-    qkv [L, (H + 2 KV) * 128]; k and v go into the caches (kT_cache [KV, 128,
-    T], v_cache [KV, T, 128]) at positions ``slot`` (int64 [L]); cos / sin are
+    qkv [L, (H + 2 KV) * 128]; k and v go into the caches (k_cache and
+    v_cache, both [KV, T, 128]) at positions ``slot`` (int64 [L]); cos / sin are
     fp16 tables [P, 128] read at rows ``rope_row`` (int64 [L]).  Returns q
     [L, H, 128]."""
     fn = "qk_norm_rope"
-    dev = _require_gpu(fn, qkv, q_norm_w, k_norm_w, cos, sin, rope_row, slot, kT_cache, v_cache)
+    dev = _require_gpu(fn, qkv, q_norm_w, k_norm_w, cos, sin, rope_row, slot, k_cache, v_cache)
     D = 128
     H, KV = int(num_heads), int(num_kv_heads)
     if qkv.dim() != 2 or qkv.shape[1] != (H + 2 * KV) * D:
         raise ValueError(f"{fn}: qkv must be [L, {(H + 2 * KV) * D}]")
     for name, t in (("qkv", qkv), ("q_norm_w", q_norm_w), ("k_norm_w", k_norm_w), ("cos", cos),
-                    ("sin", sin), ("kT_cache", kT_cache), ("v_cache", v_cache)):
+                    ("sin", sin), ("k_cache", k_cache), ("v_cache", v_cache)):
         _f16(fn, name, t)
     if cos.shape != sin.shape or cos.dim() != 2 or cos.shape[1] != D:
         raise ValueError(f"{fn}: cos and sin must be [P, {D}]")
-    if kT_cache.dim() != 3 or kT_cache.shape[:2] != (KV, D):
-        raise ValueError(f"{fn}: kT_cache must be [{KV}, {D}, T]")
-    T = kT_cache.shape[2]
+    if k_cache.dim() != 3 or k_cache.shape[0] != KV or k_cache.shape[2] != D:
+        raise ValueError(f"{fn}: k_cache must be [{KV}, T, {D}]")
+    T = k_cache.shape[1]
     if tuple(v_cache.shape) != (KV, T, D):
         raise ValueError(f"{fn}: v_cache must be [{KV}, {T}, {D}]")
     L = qkv.shape[0]
@@ -129,7 +129,7 @@ def qk_norm_rope(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tens
             q_out = torch.empty((L, H, D), dtype=torch.float16, device=dev)
         _lib.check(lib.cider_qk_norm_rope(
             _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), float(eps), _ptr(cos), _ptr(sin),
-            cos.shape[0], _ptr(rope_row), _ptr(slot), _ptr(q_out), _ptr(kT_cache),
+            cos.shape[0], _ptr(rope_row), _ptr(slot), _ptr(q_out), _ptr(k_cache),
             _ptr(v_cache), L, H, KV, D, T, _stream_ptr(dev, stream)))
     return q_out
 
@@ -139,20 +139,22 @@ def attn_decode_workspace(num_heads: int, capacity: int, device) -> torch.Tensor
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
-def attn_decode(q: torch.Tensor, kT_cache: torch.Tensor, v_cache: torch.Tensor,
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 n_valid: torch.Tensor, scale: float, ws: Optional[torch.Tensor] = None,
                 out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """Single-query grouped-query attention: q [H, 128] (or [1, H, 128])
-    against the first n = n_valid[0] positions of kT_cache [KV, 128, T] and
-    v_cache [KV, T, 128].  Returns fp16 [H * 128]."""
+    against the first n = n_valid[0] positions of k_cache and v_cache (both
+    [KV, T, 128]).  Returns fp16 [H * 128]."""
     fn = "attn_decode"
-    dev = _require_gpu(fn, q, kT_cache, v_cache, n_valid, ws, out)
+    dev = _require_gpu(fn, q, k_cache, v_cache, n_valid, ws, out)
     D = 128
     _f16(fn, "q", q)
     H = q.numel() // D
     if q.numel() != H * D:
         raise ValueError(f"{fn}: q must hold H x {D} values")
-    KV, d, T = kT_cache.shape
+    KV, T, d = k_cache.shape
+    if tuple(v_cache.shape) != (KV, T, d):
+        raise ValueError(f"{fn}: v_cache must match k_cache [KV, T, {d}]")
     if n_valid.dtype != torch.int64 or n_valid.numel() < 1:
         raise ValueError(f"{fn}: n_valid must be an int64 tensor")
     lib = _lib.load()
@@ -161,7 +163,7 @@ def attn_decode(q: torch.Tensor, kT_cache: torch.Tensor, v_cache: torch.Tensor,
             ws = attn_decode_workspace(H, T, dev)
         if out is None:
             out = torch.empty(H * D, dtype=torch.float16, device=dev)
-        _lib.check(lib.cider_attn_decode(_ptr(q), _ptr(kT_cache), _ptr(v_cache), _ptr(n_valid),
+        _lib.check(lib.cider_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(n_valid),
                                          float(scale), _ptr(ws), ws.numel(), _ptr(out), H, KV, d,
                                          T, _stream_ptr(dev, stream)))
     return out

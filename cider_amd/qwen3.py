@@ -21,10 +21,13 @@ RMSNorm before q/k/v and gate/up, and the SwiGLU before down_proj, end in the
 per-token quantization, so prefill hands (q, scale_a) straight to the int8
 GEMM; the per-head q/k RMSNorm and RoPE write k and v into the cache in the
 same kernel; decode attention is a single-query split-K kernel over the
-cache.  ``fused=False`` runs those steps as plain PyTorch ops instead (the
-A/B reference).  The embedding lookup, prefill attention (batched matmuls over
-the K-transposed cache, the 4 query heads of each KV head grouped along rows)
-and the fp16 lm_head are PyTorch on the GPU in both modes.
+cache; prefill attention is PyTorch's fused causal SDPA over the cache
+(grouped query heads, lower-right causal alignment for a chunk that follows
+earlier cache slots).  ``fused=False`` runs those steps as plain PyTorch ops
+instead (the A/B reference; its attention is batched matmuls with the 4 query
+heads of each KV head grouped along rows).  The embedding lookup and the fp16
+lm_head are PyTorch on the GPU in both modes.  Both caches are [KV, T, 128]
+(position-major).
 
 Decode keeps the position, the next token and the KV cache on the device, so a
 whole decode step (embedding to argmax) can be captured once as a HIP graph and
@@ -40,6 +43,8 @@ from typing import Optional
 
 import torch
 import torch.nn.functional as F
+
+from torch.nn.attention.bias import causal_lower_right
 
 from . import fused as FK
 from .nn import CiderLinear
@@ -136,14 +141,16 @@ class Qwen3Layer(torch.nn.Module):
                                 c.rms_eps), cos, sin)
         return q, k, v.reshape(L, c.num_kv_heads, c.head_dim)
 
-    def _attend(self, q: torch.Tensor, kT: torch.Tensor, v: torch.Tensor,
+    def _attend(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 mask: torch.Tensor) -> torch.Tensor:
-        """q [L, heads, d]; kT [kv, d, T]; v [kv, T, d]; mask broadcastable to
-        [kv, group, L, T] (0 or -inf).  Returns [L, heads * d]."""
+        """Attention as batched matmuls (the PyTorch-producer reference path):
+        q [L, heads, d]; k, v [kv, T, d]; mask broadcastable to [kv, group, L,
+        T] (0 or -inf).  Returns [L, heads * d]."""
         c = self.cfg
         L = q.shape[0]
         g = c.num_heads // c.num_kv_heads
-        T = kT.shape[-1]
+        T = k.shape[1]
+        kT = k.transpose(1, 2).contiguous()  # [kv, d, T]: no transposed bmm operand
         # q head j * g + r belongs to KV head j
         qg = (q * (1.0 / math.sqrt(c.head_dim))).reshape(L, c.num_kv_heads, g, c.head_dim)
         qg = qg.permute(1, 2, 0, 3).reshape(c.num_kv_heads, g * L, c.head_dim)
@@ -157,23 +164,37 @@ class Qwen3Layer(torch.nn.Module):
         gu = self.gate_up(rms_norm(x, self.post_norm, self.cfg.rms_eps))
         return self.down(F.silu(gu[:, :i]) * gu[:, i:])
 
-    def prefill(self, x, cos, sin, kT_cache, v_cache, mask):
-        """x [L, hidden] at positions 0..L-1; fills cache[:, :, :L]."""
+    def prefill(self, x, cos, sin, k_cache, v_cache, mask):
+        """x [L, hidden] at positions 0..L-1; fills cache[:, :L]."""
         L = x.shape[0]
         q, k, v = self._qkv(x, cos, sin)
-        kT_cache[:, :, :L].copy_(k.permute(1, 2, 0))
+        k_cache[:, :L, :].copy_(k.permute(1, 0, 2))
         v_cache[:, :L, :].copy_(v.permute(1, 0, 2))
-        x = x + self.o(self._attend(q, kT_cache[:, :, :L], v_cache[:, :L, :], mask))
+        x = x + self.o(self._attend(q, k_cache[:, :L, :], v_cache[:, :L, :], mask))
         return x + self._mlp(x)
 
-    def decode(self, x, cos, sin, pos, kT_cache, v_cache, mask):
+    def decode(self, x, cos, sin, pos, k_cache, v_cache, mask):
         """x [1, hidden] at device position `pos` ([1] int64); attends over the
         whole cache with `mask` (-inf past pos)."""
         q, k, v = self._qkv(x, cos, sin)
-        kT_cache.index_copy_(2, pos, k.permute(1, 2, 0))
+        k_cache.index_copy_(1, pos, k.permute(1, 0, 2))
         v_cache.index_copy_(1, pos, v.permute(1, 0, 2))
-        x = x + self.o(self._attend(q, kT_cache, v_cache, mask))
+        x = x + self.o(self._attend(q, k_cache, v_cache, mask))
         return x + self._mlp(x)
+
+    def _attend_sdpa(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """Causal attention of the chunk q [c, heads, d] (cache slots n - c ..
+        n - 1) over k, v [kv, n, d] with PyTorch's fused SDPA (grouped heads,
+        lower-right causal alignment when the chunk follows earlier slots)."""
+        c, n = q.shape[0], k.shape[1]
+        qq = q.permute(1, 0, 2).unsqueeze(0)
+        kk, vv = k.unsqueeze(0), v.unsqueeze(0)
+        if c == n:
+            o = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, enable_gqa=True)
+        else:
+            o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=causal_lower_right(c, n),
+                                               enable_gqa=True)
+        return o[0].permute(1, 0, 2).reshape(c, self.cfg.num_heads * self.cfg.head_dim)
 
     # ---- fused producers (HIP kernels) -------------------------------------
     # The residual stream is carried as (x, pending): the layer's true input is
@@ -185,21 +206,21 @@ class Qwen3Layer(torch.nn.Module):
                                    sum_out=x if pending is not None else None,
                                    want_y=want_y, want_q=want_q)
 
-    def prefill_fused(self, x, pending, tables, rope_row, slot, kT_cache, v_cache, n, mask):
-        """x [L, hidden] (+ pending) at cache slots `slot`; attends over cache
-        positions 0..n-1 with `mask` [L, n].  Returns (x, pending)."""
+    def prefill_fused(self, x, pending, tables, rope_row, slot, k_cache, v_cache, n):
+        """x [L, hidden] (+ pending) at cache slots n - L .. n - 1 (`slot`);
+        attends causally over cache slots 0..n-1.  Returns (x, pending)."""
         c = self.cfg
         a = self._norm(x, pending, self.input_norm, False, True)
         qkv = self.qkv.forward_quantized(a.q, a.scale_a)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
-                            rope_row, slot, kT_cache, v_cache, c.num_heads, c.num_kv_heads)
-        attn = self._attend(q, kT_cache[:, :, :n], v_cache[:, :n, :], mask)
+                            rope_row, slot, k_cache, v_cache, c.num_heads, c.num_kv_heads)
+        attn = self._attend_sdpa(q, k_cache[:, :n, :], v_cache[:, :n, :])
         b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
         gu = self.gate_up.forward_quantized(b.q, b.scale_a)
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
         return b.h, self.down.forward_quantized(qd, sd)
 
-    def decode_fused(self, x, pending, tables, pos, n_valid, kT_cache, v_cache, ws,
+    def decode_fused(self, x, pending, tables, pos, n_valid, k_cache, v_cache, ws,
                      rope_pos=None):
         """One token x [1, hidden] (+ pending) at device cache slot `pos`
         ([1] int64; RoPE row `rope_pos`, default pos), attending over
@@ -208,9 +229,9 @@ class Qwen3Layer(torch.nn.Module):
         a = self._norm(x, pending, self.input_norm, True, False)
         qkv = self.qkv(a.y)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
-                            pos if rope_pos is None else rope_pos, pos, kT_cache, v_cache,
+                            pos if rope_pos is None else rope_pos, pos, k_cache, v_cache,
                             c.num_heads, c.num_kv_heads)
-        attn = FK.attn_decode(q, kT_cache, v_cache, n_valid, 1.0 / math.sqrt(c.head_dim), ws=ws)
+        attn = FK.attn_decode(q, k_cache, v_cache, n_valid, 1.0 / math.sqrt(c.head_dim), ws=ws)
         b = self._norm(a.h, self.o(attn.reshape(1, -1)), self.post_norm, True, False)
         h, _, _ = FK.silu_mul_quantize(self.gate_up(b.y), want_y=True, want_q=False)
         return b.h, self.down(h)
@@ -249,8 +270,8 @@ class Qwen3(torch.nn.Module):
         kv, d = cfg.num_kv_heads, cfg.head_dim
         # zero-filled: decode attends over the whole cache, masked entries
         # must hold finite values
-        self.kT_cache = torch.zeros(cfg.num_layers, kv, d, cap, dtype=torch.float16,
-                                    device=dev)
+        self.k_cache = torch.zeros(cfg.num_layers, kv, cap, d, dtype=torch.float16,
+                                   device=dev)
         self.v_cache = torch.zeros(cfg.num_layers, kv, cap, d, dtype=torch.float16,
                                    device=dev)
         self._attn_ws = FK.attn_decode_workspace(cfg.num_heads, cap, dev) if fused else None
@@ -269,17 +290,17 @@ class Qwen3(torch.nn.Module):
         if L > self.max_len:
             raise ValueError(f"prompt of {L} tokens exceeds max_len={self.max_len}")
         x = self.embed.index_select(0, ids)
-        mask = torch.full((L, L), float("-inf"), device=self.device).triu_(1)
         if self.fused:
             pos = torch.arange(L, device=self.device)
             pending = None
             for i, layer in enumerate(self.layers):
                 x, pending = layer.prefill_fused(x, pending, (self.cos, self.sin), pos, pos,
-                                                 self.kT_cache[i], self.v_cache[i], L, mask)
+                                                 self.k_cache[i], self.v_cache[i], L)
             return F.linear(self._final_norm(x, pending), self.lm_head)
         cos, sin = self.cos[:L, None, :], self.sin[:L, None, :]
+        mask = torch.full((L, L), float("-inf"), device=self.device).triu_(1)
         for i, layer in enumerate(self.layers):
-            x = layer.prefill(x, cos, sin, self.kT_cache[i], self.v_cache[i], mask)
+            x = layer.prefill(x, cos, sin, self.k_cache[i], self.v_cache[i], mask)
         return F.linear(rms_norm(x, self.final_norm, self.cfg.rms_eps), self.lm_head)
 
     def _final_norm(self, x, pending):
@@ -298,7 +319,7 @@ class Qwen3(torch.nn.Module):
             pending = None
             for i, layer in enumerate(self.layers):
                 x, pending = layer.decode_fused(x, pending, (self.cos, self.sin), pos, n_valid,
-                                                self.kT_cache[i], self.v_cache[i], self._attn_ws,
+                                                self.k_cache[i], self.v_cache[i], self._attn_ws,
                                                 rope_pos)
             return F.linear(self._final_norm(x, pending), self.lm_head)
         if self._rope_delta is not None:
@@ -308,7 +329,7 @@ class Qwen3(torch.nn.Module):
         ar = torch.arange(self.capacity, device=self.device)
         mask = torch.where(ar <= pos, 0.0, float("-inf"))
         for i, layer in enumerate(self.layers):
-            x = layer.decode(x, cos, sin, pos, self.kT_cache[i], self.v_cache[i], mask)
+            x = layer.decode(x, cos, sin, pos, self.k_cache[i], self.v_cache[i], mask)
         return F.linear(rms_norm(x, self.final_norm, self.cfg.rms_eps), self.lm_head)
 
     def _greedy_step(self, state: dict):

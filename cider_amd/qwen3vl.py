@@ -161,14 +161,12 @@ class Qwen3VL(Qwen3):
             e = min(L, s + chunk)
             c = e - s
             xc = x[s:e].clone()
-            # query i (slot s + i) sees slots 0 .. s + i
-            mask = torch.full((c, e), float("-inf"), device=self.device).triu_(s + 1)
             rows = torch.arange(c, device=self.device)
             pc = None
             for i, layer in enumerate(self.layers):
+                # query i (slot s + i) sees slots 0 .. s + i
                 xc, pc = layer.prefill_fused(xc, pc, (cos[s:e], sin[s:e]), rows,
-                                             slots[s:e], self.kT_cache[i], self.v_cache[i], e,
-                                             mask)
+                                             slots[s:e], self.k_cache[i], self.v_cache[i], e)
             out = (xc, pc)
         xl, pl = out
         logits = F.linear(self._final_norm(xl[-1:].clone(), pl[-1:].clone()), self.lm_head)

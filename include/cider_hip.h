@@ -163,7 +163,7 @@ int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* s
 /* Per-head RMSNorm of q and k (weights [D]) and rotate-half RoPE on the rows
  * of a fused q/k/v projection qkv [L, (H + 2 KV) * D]:
  *   q_out [L, H, D]          <- RoPE(RMSNorm(q))
- *   kT_cache[j, :, slot[t]]  <- RoPE(RMSNorm(k_j))    (cache [KV, D, T])
+ *   k_cache[j, slot[t], :]   <- RoPE(RMSNorm(k_j))    (cache [KV, T, D])
  *   v_cache[j, slot[t], :]   <- v_j                   (cache [KV, T, D])
  * using rows rope_row[t] of the cos / sin tables [P, D] (fp16); RoPE is
  * out = h(h(x*cos) + h(rot(x)*sin)), rot(x) = [-x[D/2:], x[:D/2]].
@@ -173,7 +173,7 @@ int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* s
 int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16,
                        const void* k_norm_w_f16, float eps, const void* cos_f16,
                        const void* sin_f16, int64_t P, const int64_t* rope_row,
-                       const int64_t* slot, void* q_out_f16, void* kT_cache_f16,
+                       const int64_t* slot, void* q_out_f16, void* k_cache_f16,
                        void* v_cache_f16, int64_t L, int64_t H, int64_t KV,
                        int64_t D, int64_t T, void* stream);
 
@@ -182,11 +182,11 @@ size_t cider_attn_decode_workspace_bytes(int64_t H, int64_t T);
 
 /* Single-query grouped-query attention over the caches written by
  * cider_qk_norm_rope: for query head h of KV head j = h / (H / KV),
- *   out[h] = sum_{t < n} softmax_t(scale * q[h] . K[j,:,t]) V[j,t,:]
+ *   out[h] = sum_{t < n} softmax_t(scale * q[h] . K[j,t,:]) V[j,t,:]
  * in fp32, rounded to fp16 [H, D]. n = min(*n_valid, T) is read on the
  * device (int64), so a captured call serves a growing sequence. D == 128,
  * H / KV in {1, 2, 4, 8}, T % 8 == 0; ws 256-byte aligned. */
-int cider_attn_decode(const void* q_f16, const void* kT_cache_f16,
+int cider_attn_decode(const void* q_f16, const void* k_cache_f16,
                       const void* v_cache_f16, const int64_t* n_valid, float scale,
                       void* ws, size_t ws_bytes, void* out_f16, int64_t H,
                       int64_t KV, int64_t D, int64_t T, void* stream);

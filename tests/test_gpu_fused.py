@@ -154,9 +154,9 @@ def test_qk_norm_rope_and_cache(L, H, KV):
     cos, sin = torch.from_numpy(cos_np).cuda(), torch.from_numpy(sin_np).cuda()
     rope_row = torch.randint(0, P, (L,), device="cuda", generator=g)
     slot = torch.randperm(T, device="cuda", generator=g)[:L].contiguous()
-    kT = torch.zeros(KV, D, T, dtype=torch.float16, device="cuda")
+    kc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
     vc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
-    q = F.qk_norm_rope(qkv, qw, kw, 1e-6, cos, sin, rope_row, slot, kT, vc, H, KV)
+    q = F.qk_norm_rope(qkv, qw, kw, 1e-6, cos, sin, rope_row, slot, kc, vc, H, KV)
     torch.cuda.synchronize()
 
     x = qkv.double().cpu().numpy().reshape(L, H + 2 * KV, D)
@@ -183,12 +183,12 @@ def test_qk_norm_rope_and_cache(L, H, KV):
     check(q.cpu().numpy(), ref(x[:, :H], qw), "q")
     k_exp = ref(x[:, H:H + KV], kw)
     sl = slot.cpu().numpy()
-    k_got = kT.cpu().numpy().astype(np.float64)[:, :, sl].transpose(2, 0, 1)   # [L, KV, D]
+    k_got = kc.cpu().numpy().astype(np.float64)[:, sl, :].transpose(1, 0, 2)   # [L, KV, D]
     check(k_got, k_exp, "k cache")
     v_got = vc.cpu().numpy()[:, sl, :].transpose(1, 0, 2)
     assert np.array_equal(v_got, qkv.cpu().numpy().reshape(L, H + 2 * KV, D)[:, H + KV:])
     untouched = np.setdiff1d(np.arange(T), sl)
-    assert np.all(kT.cpu().numpy()[:, :, untouched] == 0)
+    assert np.all(kc.cpu().numpy()[:, untouched, :] == 0)
     assert np.all(vc.cpu().numpy()[:, untouched, :] == 0)
 
 
@@ -198,25 +198,25 @@ def test_qk_norm_rope_skips_out_of_range_slots():
     w = torch.ones(D, device="cuda", dtype=torch.float16)
     cos_np, sin_np = _rope_tables(8)
     cos, sin = torch.from_numpy(cos_np).cuda(), torch.from_numpy(sin_np).cuda()
-    kT = torch.zeros(KV, D, T, dtype=torch.float16, device="cuda")
+    kc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
     vc = torch.zeros(KV, T, D, dtype=torch.float16, device="cuda")
     rope_row = torch.tensor([1, 2], device="cuda")
     slot = torch.tensor([3, T], device="cuda")     # the second token has no slot
-    F.qk_norm_rope(qkv, w, w, 1e-6, cos, sin, rope_row, slot, kT, vc, H, KV)
+    F.qk_norm_rope(qkv, w, w, 1e-6, cos, sin, rope_row, slot, kc, vc, H, KV)
     torch.cuda.synchronize()
-    written = (kT != 0).any(dim=1).any(dim=0).cpu().numpy()
+    written = (kc != 0).any(dim=2).any(dim=0).cpu().numpy()
     assert written[3] and written.sum() == 1
     assert torch.equal(vc[:, 3], qkv[0].reshape(H + 2 * KV, D)[H + KV:])
 
 
-def _attn_ref(q, kT, vc, n, scale):
+def _attn_ref(q, kc, vc, n, scale):
     H, D = q.shape
-    KV = kT.shape[0]
+    KV = kc.shape[0]
     G = H // KV
     out = np.zeros((H, D))
     for h in range(H):
         j = h // G
-        s = scale * (q[h] @ kT[j][:, :n])
+        s = scale * (kc[j][:n] @ q[h])
         p = np.exp(s - s.max())
         out[h] = (p / p.sum()) @ vc[j][:n]
     return out
@@ -229,17 +229,17 @@ def test_attn_decode(G, n):
     H = KV * G
     g = torch.Generator(device="cuda").manual_seed(G * 1000 + n)
     q = torch.randn(H, D, device="cuda", generator=g).half()
-    kT = torch.randn(KV, D, T, device="cuda", generator=g).half()
+    kc = torch.randn(KV, T, D, device="cuda", generator=g).half()
     vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
     # positions >= n hold garbage that must not leak into the result
     nn = min(n, T)
-    kT[:, :, nn:] = float("nan")
+    kc[:, nn:, :] = float("nan")
     vc[:, nn:, :] = float("nan")
     nv = torch.tensor([n], device="cuda")
     scale = 1.0 / math.sqrt(D)
-    out = F.attn_decode(q, kT, vc, nv, scale)
+    out = F.attn_decode(q, kc, vc, nv, scale)
     torch.cuda.synchronize()
-    exp = _attn_ref(q.double().cpu().numpy(), kT.double().cpu().numpy()[:, :, :nn],
+    exp = _attn_ref(q.double().cpu().numpy(), kc.double().cpu().numpy()[:, :nn],
                     vc.double().cpu().numpy()[:, :nn], nn, scale)
     got = out.double().cpu().numpy().reshape(H, D)
     assert np.all(np.isfinite(got))
@@ -250,7 +250,7 @@ def test_attn_decode_graph_replays_follow_device_length():
     KV, G, D, T = 8, 4, 128, 512
     H = KV * G
     q = torch.randn(H, D, device="cuda").half()
-    kT = torch.randn(KV, D, T, device="cuda").half()
+    kc = torch.randn(KV, T, D, device="cuda").half()
     vc = torch.randn(KV, T, D, device="cuda").half()
     nv = torch.tensor([1], device="cuda")
     ws = F.attn_decode_workspace(H, T, "cuda")
@@ -258,14 +258,14 @@ def test_attn_decode_graph_replays_follow_device_length():
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        F.attn_decode(q, kT, vc, nv, 0.1, ws=ws, out=out)
+        F.attn_decode(q, kc, vc, nv, 0.1, ws=ws, out=out)
     torch.cuda.current_stream().wait_stream(s)
     gr = torch.cuda.CUDAGraph()
     with torch.cuda.graph(gr):
-        F.attn_decode(q, kT, vc, nv, 0.1, ws=ws, out=out)
+        F.attn_decode(q, kc, vc, nv, 0.1, ws=ws, out=out)
     for n in (3, 130, 257, 512, 40):
         nv.fill_(n)
-        eager = F.attn_decode(q, kT, vc, nv, 0.1)
+        eager = F.attn_decode(q, kc, vc, nv, 0.1)
         torch.cuda.synchronize()
         gr.replay()
         torch.cuda.synchronize()

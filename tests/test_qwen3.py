@@ -134,19 +134,21 @@ def test_tiny_decode_matches_prefill():
 @pytest.mark.gpu
 def test_tiny_fused_matches_torch_producers():
     """The fused HIP producers (RMSNorm + quantize, SwiGLU + quantize, q/k
-    norm + RoPE + cache write, decode attention) against the same model run
-    with PyTorch ops for those steps; equal up to RMSNorm / exp rounding that
-    can move an activation's int8 rounding."""
+    norm + RoPE + cache write, decode attention; prefill attention by fused
+    SDPA) against the same model run with PyTorch ops for those steps (its
+    attention rounds the scores to fp16).  The two differ by RMSNorm / exp
+    roundings that move single activations' int8 rounding and by that score
+    rounding: a few percent at the extreme logit, cosine far above 0.999."""
     ids = torch.randint(0, TINY.vocab_size, (40,), device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(10))
     a = Q.Qwen3(TINY, max_len=128, seed=9, fused=True)
     b = Q.Qwen3(TINY, max_len=128, seed=9, fused=False)
-    _close(a.prefill(ids), b.prefill(ids), 3e-2, "prefill fused vs torch")
-    assert torch.allclose(a.v_cache[:, :, :40].float(), b.v_cache[:, :, :40].float(),
-                          rtol=3e-2, atol=3e-2)
+    _close(a.prefill(ids), b.prefill(ids), 5e-2, "prefill fused vs torch")
+    _close(a.v_cache[:, :, :40], b.v_cache[:, :, :40], 5e-2, "v cache fused vs torch")
+    _close(a.k_cache[:, :, :40], b.k_cache[:, :, :40], 5e-2, "k cache fused vs torch")
     tok = ids[-1:].clone()
     pos = torch.tensor([40], device="cuda")
-    _close(a.decode_step(tok, pos)[0], b.decode_step(tok, pos)[0], 3e-2,
+    _close(a.decode_step(tok, pos)[0], b.decode_step(tok, pos)[0], 5e-2,
            "decode fused vs torch")
 
 
@@ -176,7 +178,7 @@ def test_tiny_graph_replays_match_eager():
         assert torch.equal(sa["tok"], sb["tok"]), f"step {t}"
         assert torch.equal(sa["pos"], sb["pos"])
     assert torch.equal(sa["out"], sb["out"])
-    assert torch.equal(a.kT_cache, b.kT_cache) and torch.equal(a.v_cache, b.v_cache)
+    assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.v_cache, b.v_cache)
 
 
 @pytest.mark.gpu

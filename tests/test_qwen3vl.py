@@ -121,10 +121,15 @@ def test_chunked_prefill_matches_one_shot_and_fp32():
     pos3 = V.rope_index(SEGS)
     L = x.shape[0]
     one = m.prefill_chunked(x, pos3, chunk=L)
-    kT1 = m.kT_cache[:, :, :, :L].clone()
+    k1 = m.k_cache[:, :, :L].clone()
     chunked = m.prefill_chunked(x, pos3, chunk=16)
-    _close(chunked, one, 2e-2, "chunked vs one-shot")
-    assert torch.allclose(m.kT_cache[:, :, :, :L].float(), kT1.float(), atol=2e-2, rtol=2e-2)
+    # one-shot runs SDPA's causal kernel, the chunks its lower-right-masked
+    # one: attention outputs equal up to fp16 rounding, which moves single
+    # activations' int8 rounding in the linears after it
+    _close(chunked, one, 5e-2, "chunked vs one-shot")
+    # layer 0 sees the same inputs in both runs: its cache is identical
+    assert torch.equal(m.k_cache[0, :, :L], k1[0])
+    _close(m.k_cache[:, :, :L], k1, 5e-2, "k cache chunked vs one-shot")
     cos, sin = V.mrope_cos_sin(pos3.cuda(), TINY.head_dim, TINY.rope_theta)
     ref = _ref_forward(m, x, cos, sin)[-1:]
     _close(chunked, ref, 8e-2, "chunked vs fp32 model")
