@@ -355,33 +355,45 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     float sam[TM];
 #pragma unroll
     for (int b = 0; b < TM; ++b) sam[b] = ssa[wm * WM + b * 32 + frow];
+    // the bias test is uniform: taken once, outside the conversion loops (a
+    // per-element select would cost two VALU ops per accumulator)
+    auto convert = [&](auto biasc) {
+      constexpr bool BIAS = decltype(biasc)::value != 0;
 #pragma unroll
-    for (int a = 0; a < TN; ++a) {
+      for (int a = 0; a < TN; ++a) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = wn * WN + a * 32 + 8 * g + 4 * h;  // column in tile
-        const f32x4 swv = *reinterpret_cast<const f32x4*>(ssw + nl);
-        const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
-        const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
-                             h2f((uint16_t)((uint32_t)bb[0] >> 16)),
-                             h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
-                             h2f((uint16_t)((uint32_t)bb[1] >> 16))};
-#pragma unroll
-        for (int b = 0; b < TM; ++b) {
-          const int ml = wm * WM + b * 32 + frow;  // row in tile
-          uint16_t o[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v = (float)acc[a][b][4 * g + r] * sam[b];
-            v = v * swv[r];
-            if (p.bias) v = v + bv[r];
-            o[r] = f2h(v);
+        for (int g = 0; g < 4; ++g) {
+          const int nl = wn * WN + a * 32 + 8 * g + 4 * h;  // column in tile
+          const f32x4 swv = *reinterpret_cast<const f32x4*>(ssw + nl);
+          float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          if constexpr (BIAS) {
+            const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+            bv[0] = h2f((uint16_t)((uint32_t)bb[0] & 0xffffu));
+            bv[1] = h2f((uint16_t)((uint32_t)bb[0] >> 16));
+            bv[2] = h2f((uint16_t)((uint32_t)bb[1] & 0xffffu));
+            bv[3] = h2f((uint16_t)((uint32_t)bb[1] >> 16));
           }
-          *reinterpret_cast<i32x2*>(smem + ml * C::OUT_LD + nl * 2) =
-              i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+#pragma unroll
+          for (int b = 0; b < TM; ++b) {
+            const int ml = wm * WM + b * 32 + frow;  // row in tile
+            uint16_t o[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float v = (float)acc[a][b][4 * g + r] * sam[b];
+              v = v * swv[r];
+              if constexpr (BIAS) v = v + bv[r];
+              o[r] = f2h(v);
+            }
+            *reinterpret_cast<i32x2*>(smem + ml * C::OUT_LD + nl * 2) = i32x2{
+                (int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+          }
         }
       }
-    }
+    };
+    if (p.bias)
+      convert(icst<1>{});
+    else
+      convert(icst<0>{});
     __syncthreads();
     // whole rows: BN / 8 lanes x 16 bytes per row, 512 / BN rows per store
     constexpr int LPR = BN / 8, RPS = 64 / LPR;
