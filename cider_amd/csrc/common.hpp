@@ -23,7 +23,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// fp32 -> fp16 of an already rounded binary32 value.  The empty asm makes f
+// opaque: without it the backend may fold  f2h(a * b)  (or  f2h(a * b + c))
+// into one v_fma_mixlo_f16, which rounds the exact product straight to fp16
+// (one rounding) instead of to binary32 and then to fp16 (two roundings), and
+// differs from the specified order at fp16 midpoints.
 __device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 

@@ -242,11 +242,14 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
             else
               read_w(rs, JN, q - TM, raw);
           }
+        // unpack of block a: in the last TN slots, and never before the slot
+        // that reads its new chunk (TM + a, clamped; a slot issues its reads
+        // before its unpacks).  At 64 x 128 (NMF = TN = 2) both land in slot 1.
 #pragma unroll
         for (int a = 0; a < TN; ++a) {
           constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
-          if ((first_slot + a < NMF ? first_slot + a : NMF - 1) == idx)
-            unpack_half(a, JN % 2, wn_);
+          const int want = first_slot + a > TM + a || !new_pair ? first_slot + a : TM + a;
+          if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a, JN % 2, wn_);
         }
       }
       if constexpr (dma) {

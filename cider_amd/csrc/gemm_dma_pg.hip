@@ -300,11 +300,14 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
             else
               read_w(rs, JN, q - PG_TM, raw);
           }
+        // unpack of block a2: in the last PG_TN slots, never before the slot
+        // that reads its new chunk (PG_TM + a2, clamped)
 #pragma unroll
         for (int a2 = 0; a2 < PG_TN; ++a2) {
           constexpr int first_slot = new_pair ? (NMF > PG_TN ? NMF - PG_TN : 0) : 0;
-          if ((first_slot + a2 < NMF ? first_slot + a2 : NMF - 1) == idx)
-            unpack_half(a2, JN % 2, wn_);
+          const int want =
+              first_slot + a2 > PG_TM + a2 || !new_pair ? first_slot + a2 : PG_TM + a2;
+          if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
         }
       }
       if constexpr (rd && SVDB) {
