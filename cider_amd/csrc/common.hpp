@@ -33,6 +33,18 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 -> fp16 (RNE), a in the low half, b in the high half: one
+// v_cvt_pk_f16_f32 of the already rounded binary32 values.  gfx950 converts
+// the two-wide vector whole, so no multiply folds into it and no empty asm is
+// needed (the asm of f2h orders the conversion against LDS traffic, which
+// costs the GEMM epilogues their overlap).
+__device__ __forceinline__ uint32_t f2h2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
+
 // 16x16x64 int8 MFMA: C[i][j] += sum_k A[i][k] * B[k][j].
 // Operand layout (64 lanes, 16 bytes each): lane l holds row i = l % 16 of A
 // (column j = l % 16 of B) and one 16-byte slice of K selected by l / 16; the

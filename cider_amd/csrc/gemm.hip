@@ -315,27 +315,25 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_kernel(const GemmArgs p) {
             if (n + r < N) yp[r] = acc[a][b][r];
         }
       } else {
-        uint16_t o[4];
+        float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float v;
           if constexpr (EPI == EPI_PC) {
-            v = (float)acc[a][b][r] * sam[b];
-            v = v * swv[r];
+            v[r] = (float)acc[a][b][r] * sam[b];
+            v[r] = v[r] * swv[r];
           } else {
-            v = facc[a][b][r] * sam[b];
+            v[r] = facc[a][b][r] * sam[b];
           }
-          if (p.bias) v = v + bv[r];
-          o[r] = f2h(v);
+          if (p.bias) v[r] = v[r] + bv[r];
         }
+        const uint32_t o01 = f2h2(v[0], v[1]), o23 = f2h2(v[2], v[3]);
         uint16_t* yp = reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n;
         if (vec_n) {
-          *reinterpret_cast<i32x2*>(yp) =
-              i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+          *reinterpret_cast<i32x2*>(yp) = i32x2{(int)o01, (int)o23};
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            if (n + r < N) yp[r] = o[r];
+            if (n + r < N) yp[r] = (uint16_t)((r < 2 ? o01 : o23) >> (16 * (r & 1)));
         }
       }
     }

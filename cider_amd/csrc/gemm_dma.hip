@@ -379,16 +379,16 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 #pragma unroll
           for (int b = 0; b < TM; ++b) {
             const int ml = wm * WM + b * 32 + frow;  // row in tile
-            uint16_t o[4];
+            float o[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               float v = (float)acc[a][b][4 * g + r] * sam[b];
               v = v * swv[r];
               if constexpr (BIAS) v = v + bv[r];
-              o[r] = f2h(v);
+              o[r] = v;
             }
-            *reinterpret_cast<i32x2*>(smem + ml * C::OUT_LD + nl * 2) = i32x2{
-                (int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+            *reinterpret_cast<i32x2*>(smem + ml * C::OUT_LD + nl * 2) =
+                i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
           }
         }
       }

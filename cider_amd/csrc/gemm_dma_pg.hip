@@ -462,15 +462,15 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
       for (int b = 0; b < PG_TM; ++b) {
         const int ml = wm * PG_WM + b * 32 + frow;
         const float sam = ssa[ml];
-        uint16_t o[4];
+        float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float v = facc[a][b][4 * q + r] * sam;
           if (p.bias) v = v + bv[r];
-          o[r] = f2h(v);
+          o[r] = v;
         }
         *reinterpret_cast<i32x2*>(smem + ml * PG_OUT_LD + nl * 2) =
-            i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+            i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
       }
     }
   }

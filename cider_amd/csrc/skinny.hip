@@ -166,24 +166,23 @@ __global__ __launch_bounds__(KW * 64) void skinny_kernel(const GemmArgs p) {
       }
     } else {
       const float sam = p.sa[m];
-      uint16_t o[4];
+      float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int n = ncol + r;
         const float swn = n < N ? reinterpret_cast<const float*>(p.sw)[n] : 0.0f;
-        float v = (float)acc[b][r] * sam;
-        v = v * swn;
-        if (p.bias) v = v + (n < N ? h2f(p.bias[n]) : 0.0f);
-        o[r] = f2h(v);
+        v[r] = (float)acc[b][r] * sam;
+        v[r] = v[r] * swn;
+        if (p.bias) v[r] = v[r] + (n < N ? h2f(p.bias[n]) : 0.0f);
       }
+      const uint32_t o01 = f2h2(v[0], v[1]), o23 = f2h2(v[2], v[3]);
       uint16_t* yp = reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + ncol;
       if (VEC) {
-        *reinterpret_cast<i32x2*>(yp) =
-            i32x2{(int)(o[0] | ((uint32_t)o[1] << 16)), (int)(o[2] | ((uint32_t)o[3] << 16))};
+        *reinterpret_cast<i32x2*>(yp) = i32x2{(int)o01, (int)o23};
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (ncol + r < N) yp[r] = o[r];
+          if (ncol + r < N) yp[r] = (uint16_t)((r < 2 ? o01 : o23) >> (16 * (r & 1)));
       }
     }
   }
