@@ -15,16 +15,19 @@
 //
 // MI355X design
 //   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
-//     (n), BM, BN in {64, 128, 256}, chosen per shape so the grid covers the
-//     256 CUs; at 256 x 256 each wave owns a 128 x 128 sub-tile = 4 x 4 blocks
-//     of 32 x 32 (16 int32 accumulators per lane per block, 256 AGPRs).
-//     Weights are the MFMA A operand, activations the B operand.  128 x 128
-//     per wave is the smallest wave tile whose fragment reads (32 KB per wave
-//     per 128-byte stage, half of LDS bandwidth at full MFMA rate) leave room
-//     for the DMA fill.
+//     (n) from {128 x 256, 128 x 128, 128 x 64, 64 x 128, 64 x 64}, picked
+//     per shape by measured rate and the number of rounds the grid needs on
+//     the 256 CUs.  At 128 x 256 (the large-M tile) each wave owns a 64 x 128
+//     sub-tile = 2 x 4 blocks of 32 x 32 (16 int32 accumulators per lane per
+//     block, 128 AGPRs).  Weights are the MFMA A operand, activations the B
+//     operand.  With int8 weights 256 x 256 (4 x 4 blocks per wave) is not
+//     picked: its 64 KB stages leave room for only two ring slots, too few
+//     to spread the loads (below), and 128 x 256 measured faster at every
+//     large shape.  With int4 weights (48 KB stages, three slots) 256 x 256
+//     is the fastest tile per MAC and is picked where its rounds fit.
 //   * K advances BK bytes per stage (128; 64 is kept for tuning); stage s
 //     lives in ring slot s % NS, NS = as many stages as fit the 160 KB LDS
-//     (2 at 256 x 256 x 128, up to 8 for small tiles).  Each wave moves its
+//     (3 at 128 x 256 x 128, up to 8 for small tiles).  Each wave moves its
 //     share of a stage with global_load_lds_dwordx4 (one instruction = 1 KB,
 //     written contiguously to LDS at M0): no VGPR staging, no ds_write.  The
 //     loads are issued from inline asm, so the compiler does not wait for
@@ -34,10 +37,14 @@
 //   * A stage is BK / 32 k sub-steps of TN x TM MFMAs.  Each sub-step is one
 //     fixed instruction order (sched_barrier): MFMAs, with the next
 //     sub-step's fragment reads issued one per MFMA in the order they will be
-//     consumed, and after the barrier this wave's DMA loads of stage kt + NS
-//     spread one per MFMA.  Left to itself, the compiler regroups the reads
-//     next to the MFMAs that consume them and exposes LDS latency at every
-//     sub-step (measured 137 -> 124 us at M=4096, N=10240, K=2560).
+//     consumed, and this wave's share of DMA loads spread over the MFMAs.
+//     Left to itself, the compiler regroups the reads next to the MFMAs that
+//     consume them and exposes LDS latency at every sub-step.
+//   * With three or more ring slots, a stage's DMA loads are spread over
+//     SUBS sub-steps (the last of stage kt and the first ones of stage kt+1)
+//     instead of one: the CU's vector-memory path accepts one 1 KB load per
+//     ~23 cycles, and a whole stage's loads inside one sub-step stalled the
+//     issuing waves for ~440 of its 512 MFMA cycles (measured at 256 x 256).
 //   * The one barrier per stage sits before its last sub-step: it publishes
 //     stage kt + 1 and frees the slot of stage kt, which then receives stage
 //     kt + NS.
@@ -52,7 +59,7 @@
 //     then the workgroup stores whole 2*BN-byte rows with 16-byte lanes, so
 //     HBM sees full 128-byte lines instead of 32-byte row fragments.
 //   * int4 weights: a k-stage of a weight row is 64 bytes of nibbles (the ring
-//     then holds 3 stages at 256 x 256).  One ds_read_b128 per W block brings
+//     then holds 4 stages at 128 x 256).  One ds_read_b128 per W block brings
 //     the 32 nibbles of a pair of sub-steps; each sub-step's 16 are unpacked
 //     to int8 in registers (sign extension by xor/sub, byte permute) one
 //     sub-step ahead of their MFMAs.  The k mapping of a pair puts lane half h
@@ -201,10 +208,20 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0;
 
+  // DMA loads of one stage are issued in DS parts: part 0 in the last
+  // sub-step of stage kt (after the barrier that frees its slot), parts
+  // 1 .. DS-1 in the first sub-steps of stage kt+1.  A stage's loads at once
+  // (PS per wave inside one sub-step) outrun what the CU's vector-memory path
+  // accepts (one 1 KB load per ~23 cycles) and stall the issuing waves.  Every
+  // part is out before the next barrier, so the counts waited for are as if
+  // the stage were issued at once.  Exception, measured: int4 weights at
+  // 256 x 256 (three slots) ran 25-40% slower split than whole.
+  constexpr int DS = (NS >= 3 && !(W4 && BM == 256)) ? SUBS : 1;
+
   // One k sub-step in a fixed instruction order (sched_barrier): the TN*TM
   // MFMAs on fragments (wc, xc); between them the operands of the next
-  // sub-step JN (from slot rs) when rd, and this wave's DMA loads of stage dst
-  // into slot dsl when dma.  int8: the next fragments are read one per MFMA
+  // sub-step JN (from slot rs) when rd, and part dmac - 1 of this wave's DMA
+  // loads of stage dst into slot dsl when dmac > 0.  int8: the next fragments are read one per MFMA
   // in the order they will be consumed (W0, X0 .. X(TM-1), W1 ..), each at
   // least TN*TM - TN - TM MFMAs before its use.  int4: the X fragments are
   // read first; when JN starts a new pair the raw W chunks are read next and
@@ -214,7 +231,9 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   auto step = [&](auto JNc, auto rdc, auto dmac, const i32x4 (&wc)[TN], const i32x4 (&xc)[TM],
                   int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst, int dsl) {
     constexpr int JN = decltype(JNc)::value;
-    constexpr bool rd = decltype(rdc)::value != 0, dma = decltype(dmac)::value != 0;
+    constexpr bool rd = decltype(rdc)::value != 0;
+    constexpr int part = decltype(dmac)::value - 1;  // -1: no DMA
+    constexpr int d0 = part < 0 ? 0 : part * PS / DS, d1 = part < 0 ? 0 : (part + 1) * PS / DS;
     constexpr int NMF = TN * TM, NR = TN + TM;
 #pragma unroll
     for (int idx = 0; idx < NMF; ++idx) {
@@ -252,10 +271,10 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
           if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a, JN % 2, wn_);
         }
       }
-      if constexpr (dma) {
+      if constexpr (part >= 0 && d1 > d0) {  // a part is empty when PS < DS
 #pragma unroll
-        for (int d = 0; d < PS; ++d)
-          if (d * NMF / PS == idx) dma_one(dst, dsl, d);
+        for (int d = d0; d < d1; ++d)
+          if ((d - d0) * NMF / (d1 - d0) == idx) dma_one(dst, dsl, d);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -287,14 +306,18 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 
   // Stage kt: sub-steps 0 .. SUBS-1.  The barrier before the last sub-step
   // publishes stage kt+1 (NS-2 younger stages still in flight) and frees the
-  // slot of stage kt, which receives stage kt+NS during that sub-step.
-  auto stage_body = [&](int kt, auto lastc) {
+  // slot of stage kt, which receives stage kt+NS from that sub-step on.  The
+  // first DS-1 sub-steps issue the rest of the loads the previous stage began
+  // (none in the first stage: the prologue loaded whole stages).
+  auto stage_body = [&](int kt, auto lastc, auto firstc) {
     constexpr bool LAST = decltype(lastc)::value != 0;
+    constexpr bool FIRST = decltype(firstc)::value != 0;
     const int sl = kt % NS;
+    const int pdst = min(kt - 1 + NS, nk - 1), psl = (kt + NS - 1) % NS;
 #define DMA_SUB(J)                                                                          \
   if constexpr ((J) < SUBS - 1) {                                                           \
-    step(icst<(J) + 1>{}, icst<1>{}, icst<0>{}, wf[(J) & 1], xf[(J) & 1], sl,               \
-         wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0);                                       \
+    step(icst<(J) + 1>{}, icst<1>{}, icst<(!FIRST && (J) + 1 < DS) ? (J) + 2 : 0>{},         \
+         wf[(J) & 1], xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], pdst, psl);     \
   } else if constexpr (!LAST) {                                                             \
     wait_vmcnt<(NS - 2) * PS>();                                                            \
     __syncthreads();                                                                        \
@@ -311,7 +334,8 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     }
 #undef DMA_SUB
   };
-  for (int kt = 0; kt < nk - 1; ++kt) stage_body(kt, icst<0>{});
+  if (nk > 1) stage_body(0, icst<0>{}, icst<1>{});
+  for (int kt = 1; kt < nk - 1; ++kt) stage_body(kt, icst<0>{}, icst<0>{});
   // Last stage.  The per-channel epilogue's scales are requested here, so
   // their latency hides behind the last MFMAs; indices are clamped, so the
   // loads are unconditional.
@@ -322,7 +346,10 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     sa_t = p.sa[min(m0 + tid % BM, M - 1)];
     if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
   }
-  stage_body(nk - 1, icst<1>{});
+  if (nk > 1)
+    stage_body(nk - 1, icst<1>{}, icst<0>{});
+  else
+    stage_body(0, icst<1>{}, icst<1>{});
   wait_vmcnt<0>();  // the reloads past the end land before LDS is reused
 
   // ---- epilogue: lane holds, per 32x32 block and group g, 4 consecutive n
@@ -421,27 +448,6 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   dma_tile<BM, BN, BK, EPI, WF>(p, m0, n0, smem);
 }
 
-// Two tile sizes in one grid, so that the last round of workgroups is not
-// half empty: workgroups [0, nbig) take 256 x 256 tiles of columns
-// [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
-// many tiles of half the work.  Workgroups start in index order, so the small
-// tiles form the last round; each region has its own XCD remap.
-template <int EPI, int WF>
-__global__ __launch_bounds__(256, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
-                                                                int nsplit) {
-  constexpr int S1 = DmaCfg<256, 256, 128, WF>::SMEM, S2 = DmaCfg<128, 256, 128, WF>::SMEM;
-  __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
-  const int b = blockIdx.x;
-  int m0, n0;
-  if (b < nbig) {
-    tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
-    dma_tile<256, 256, 128, EPI, WF>(p, m0, n0, smem);
-  } else {
-    tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
-    dma_tile<128, 256, 128, EPI, WF>(p, m0, n0, smem);
-  }
-}
-
 namespace {
 
 template <int BM, int BN, int BK, int EPI, int WF = W_I8>
@@ -453,47 +459,43 @@ hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
 
 template <int EPI, int WF>
 hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
+  // Estimated time = rounds of `cus` workgroups x tile area / tile rate.  The
+  // rates are throughputs measured on MI355X relative to a 256 x 256 tile (=
+  // 1) over M = 128 .. 16384 and (N, K) from (10240, 2560) to (4096, 12288),
+  // with back-to-back launches.  int8 weights: 128 x 256 streams as fast per
+  // MAC as 256 x 256 (whose two-slot ring cannot spread its loads) with half
+  // the fixed cost per tile and finer rounds, so 256 x 256 is not a
+  // candidate.  int4 weights: 256 x 256 has three slots and is the fastest
+  // tile per MAC.  Ties go to the larger tile.
+  struct Cand { int bm, bn; double rate; };
+  static const Cand c8[] = {{128, 256, 1.05}, {128, 128, 0.87}, {128, 64, 0.51},
+                            {64, 128, 0.50},  {64, 64, 0.40}};
+  static const Cand c4[] = {{256, 256, 1.0},  {128, 256, 0.94}, {128, 128, 0.72},
+                            {128, 64, 0.44},  {64, 128, 0.43},  {64, 64, 0.35}};
+  const Cand* cands = WF == W_I4 ? c4 : c8;
+  const int nc = WF == W_I4 ? 6 : 5;
   const int cus = num_cus();
-  // 256 x 256 tiles whose last round is at most half full and made of whole
-  // tile columns: cover those columns with 128 x 256 tiles instead, so the
-  // last round runs on (up to) every CU with half-length tiles.
-  {
-    const int tm = (a.M + 255) / 256, tn = (a.N + 255) / 256;
-    const int64_t T = (int64_t)tm * tn;
-    const int R = (int)(T % cus);
-    if (T > cus && R > 0 && 2 * R <= cus && R % tm == 0) {
-      const int tail_cols = R / tm;
-      const int nsplit = (tn - tail_cols) * 256;
-      const int nbig = (int)(T - R);
-      const int nsmall = ((a.M + 127) / 128) * tail_cols;
-      gemm_dma_mixed_kernel<EPI, WF><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
-      return hipGetLastError();
-    }
-  }
-  // Otherwise one tile size: estimated time = rounds of `cus` workgroups x
-  // tile area / tile efficiency (MFMA work per LDS byte falls with the
-  // tile); ties go to the larger tile.
-  struct Cand { int bm, bn; double eff; };
-  static const Cand cands[] = {{256, 256, 1.0}, {128, 256, 0.8}, {128, 128, 0.6},
-                               {64, 128, 0.45}, {64, 64, 0.3}};
   int best = 0;
   double best_cost = 1e300;
-  for (int i = 0; i < 5; ++i) {
+  for (int i = 0; i < nc; ++i) {
     const int64_t tiles =
         (int64_t)((a.M + cands[i].bm - 1) / cands[i].bm) * ((a.N + cands[i].bn - 1) / cands[i].bn);
-    const double cost = (double)((tiles + cus - 1) / cus) * cands[i].bm * cands[i].bn / cands[i].eff;
+    const double cost =
+        (double)((tiles + cus - 1) / cus) * cands[i].bm * cands[i].bn / cands[i].rate;
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = i;
     }
   }
-  switch (best) {
-    case 0: return run_dma<256, 256, 128, EPI, WF>(a, s);
-    case 1: return run_dma<128, 256, 128, EPI, WF>(a, s);
-    case 2: return run_dma<128, 128, 128, EPI, WF>(a, s);
-    case 3: return run_dma<64, 128, 128, EPI, WF>(a, s);
-    default: return run_dma<64, 64, 128, EPI, WF>(a, s);
+  const int bm = cands[best].bm, bn = cands[best].bn;
+  if constexpr (WF == W_I4) {
+    if (bm == 256) return run_dma<256, 256, 128, EPI, WF>(a, s);
   }
+  if (bm == 128 && bn == 256) return run_dma<128, 256, 128, EPI, WF>(a, s);
+  if (bm == 128 && bn == 128) return run_dma<128, 128, 128, EPI, WF>(a, s);
+  if (bm == 128) return run_dma<128, 64, 128, EPI, WF>(a, s);
+  if (bn == 128) return run_dma<64, 128, 128, EPI, WF>(a, s);
+  return run_dma<64, 64, 128, EPI, WF>(a, s);
 }
 
 }  // namespace

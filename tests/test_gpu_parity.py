@@ -97,9 +97,13 @@ def test_int8_matmul_reference_shapes(bitexact_shapes):
         assert sha(c) == rec["sha_c"], (rec["M"], rec["K"], rec["N"])
 
 
+# M > 64, K % 128 == 0, N % 8 == 0: the LDS-DMA kernel at each int32 tile the
+# dispatcher picks (64x64: 256x256 and 300x520; 128x256: 2048x10240; 128x128:
+# 1024x4096; 128x64: 128x10240; 64x128: 192x10240).
 @pytest.mark.parametrize("M,N,K", [(65, 64, 64), (256, 256, 128), (300, 520, 384),
                                    (1000, 130, 1000), (2, 3, 1), (70, 90, 17),
-                                   (2048, 10240, 128)])
+                                   (2048, 10240, 128), (1024, 4096, 256), (128, 10240, 128),
+                                   (192, 10240, 128)])
 def test_int8_matmul_more_shapes(M, N, K):
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
@@ -124,11 +128,9 @@ def test_int8_matmul_extremes():
 
 # Shapes cover every GEMM variant: skinny (M <= 64), the register-staged tiled
 # kernel (K % 128 != 0 or N % 8 != 0) and the LDS-DMA kernel at each tile the
-# dispatcher picks: 64x128 (M=128, N=10240), 64x64 (M=300/257), 128x128
-# (M=2048, N=2048),
-# 128x256 (M=1024, N=10240), 256x256 (the full-size tests below), and the
-# mixed 256x256 + 128x256 grid (M=2048, N=10240; M=1000, N=16640 with a
-# partial last tile row).
+# dispatcher picks: 128x64 (M=128, N=10240), 64x64 (M=300/257), 128x128
+# (M=1024, N=10240; M=2048, N=2048), 128x256 (M=600/2048, and M=1000,
+# N=16640 with a partial last tile row); 64x128 in the midpoint test below.
 @pytest.mark.parametrize("M,N,K", [(2, 16, 64), (7, 33, 130), (16, 1000, 2560), (33, 257, 513),
                                    (64, 128, 256), (65, 200, 320), (128, 10240, 2560),
                                    (300, 1000, 1024), (257, 512, 4096), (100, 70, 100),
@@ -156,10 +158,12 @@ def test_perchannel_gemm_matches_linear():
 # where the binary32 product lands exactly on an fp16 midpoint.  Random int8
 # operands with random binary32 scales put a few hundred such elements in each
 # case (the test asserts that they are there); the shapes select, in order,
-# the 64 x 128 and 64 x 64 LDS-DMA tiles, the mixed 256 / 128 tiling, the
-# register-staged kernel (K % 128 != 0), the skinny kernel and the GEMV.
+# the 128 x 64, 64 x 64 (twice) and 64 x 128 LDS-DMA tiles, the 128 x 256
+# tile, the register-staged kernel (K % 128 != 0), the skinny kernel and the
+# GEMV.
 @pytest.mark.parametrize("M,N,K,rows", [
     (128, 10240, 2560, None), (128, 2560, 10240, None), (1000, 1000, 1024, None),
+    (192, 10240, 2560, None),
     (4096, 10240, 2560, np.r_[0:64, 4032:4096]), (300, 1000, 1000, None),
     (48, 4096, 4096, None), (3, 10240, 2560, None)])
 def test_perchannel_gemm_double_rounding_midpoints(M, N, K, rows):
@@ -314,13 +318,15 @@ def test_w4_repack_matches_unpack():
 
 
 # M > 64, K % 128 == 0, N % 8 == 0 runs the LDS-DMA kernel with int4 weights
-# (512x640 and 256x1024 on 64x64 tiles, 192x6144 on 64x128, 300x136 with an
-# odd stage count, 2048x10240 on the mixed grid); N % 8 != 0 the
+# (512x640, 256x1024 and 300x136 -- an odd stage count -- on 64x64 tiles,
+# 192x6144 on 128x64, 192x10240 on 64x128, 2048x2048 on 128x128, 2048x10240 on
+# 128x256; 256x256 in the full-size test below); N % 8 != 0 the
 # register-staged kernel; M <= 64 the skinny kernel.
 @pytest.mark.parametrize("M,N,K", [(1, 32, 64), (9, 70, 160), (1, 12288, 4096),
                                    (16, 4096, 12288), (64, 300, 1024), (100, 300, 1024),
                                    (512, 640, 2048), (7, 33, 98), (256, 1024, 512),
-                                   (300, 136, 384), (2048, 10240, 256), (192, 6144, 1024)])
+                                   (300, 136, 384), (2048, 10240, 256), (192, 6144, 1024),
+                                   (192, 10240, 2560), (2048, 2048, 1024)])
 def test_w4a8_linear_ref_layout(M, N, K):
     x = O.synth_activations(M, K, 60 + M)
     wf = np.random.default_rng(61 + N).standard_normal((K, N)).astype(np.float32)
