@@ -544,8 +544,9 @@ def bench_qwen3vl(torch, args, dev):
     }), flush=True)
 
 
-# (bm, bn, rate) per weight format, as pick_tile in cider_amd/csrc/gemm_dma.hip
-_TILES_I8 = [(128, 256, 1.05), (128, 128, 0.87), (128, 64, 0.51), (64, 128, 0.50), (64, 64, 0.40)]
+# (bm, bn, rate) for int8 weights, as pick_tile in cider_amd/csrc/gemm_dma.hip
+_TILES_I8 = [(256, 256, 1.0), (128, 256, 0.87), (128, 128, 0.75), (128, 64, 0.517),
+             (64, 128, 0.508), (64, 64, 0.40)]
 
 
 def gemm_kernel_name(M, N, K, dev):
@@ -557,7 +558,9 @@ def gemm_kernel_name(M, N, K, dev):
         best, best_cost = None, None
         for bm, bn, rate in _TILES_I8:
             tiles = -(-M // bm) * -(-N // bn)
-            cost = -(-tiles // cus) * bm * bn / rate
+            full, rest = divmod(tiles, cus)
+            rounds = full + (0.6 + 0.4 * rest / cus if rest else 0.0)
+            cost = rounds * bm * bn / rate
             if best_cost is None or cost < best_cost * 0.999:
                 best, best_cost = (bm, bn), cost
         return "gemm_dma_kernel<%d, %d, 128, PC, I8> (%dx%d tiles)" % (best + best)

@@ -15,21 +15,22 @@
 //
 // MI355X design
 //   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
-//     (n) from {128 x 256, 128 x 128, 128 x 64, 64 x 128, 64 x 64}, picked
-//     per shape by measured rate and the number of rounds the grid needs on
-//     the 256 CUs.  At 128 x 256 (the large-M tile) each wave owns a 64 x 128
-//     sub-tile = 2 x 4 blocks of 32 x 32 (16 int32 accumulators per lane per
-//     block, 128 AGPRs).  Weights are the MFMA A operand, activations the B
-//     operand.  With int8 weights 256 x 256 (4 x 4 blocks per wave) is not
-//     picked: its 64 KB stages leave room for only two ring slots, too few
-//     to spread the loads (below), and 128 x 256 measured faster at every
-//     large shape.  With int4 weights (48 KB stages, three slots) 256 x 256
-//     is the fastest tile per MAC and is picked where its rounds fit.
+//     (n) from {256 x 256, 128 x 256, 128 x 128, 128 x 64, 64 x 128, 64 x 64},
+//     picked per shape by measured rate and the rounds the grid needs on the
+//     256 CUs.  At 256 x 256 (the large-M tile) each wave owns a 128 x 128
+//     sub-tile = 4 x 4 blocks of 32 x 32 (16 int32 accumulators per lane per
+//     block, 256 AGPRs): the fewest fragment reads per MAC, which the LDS
+//     bandwidth (~128 B/clk per CU) rewards; 128 x 256 (waves of 64 x 128)
+//     wins where its rounds fit the grid better.  Weights are the MFMA A
+//     operand, activations the B operand.  At 256 x 256 there is no register
+//     to spare: a spill reload is a vector-memory load, and waiting for it
+//     waits for every DMA load in flight (one spilled build ran 15 % slower).
 //   * K advances BK bytes per stage (128; 64 is kept for tuning); stage s
 //     lives in ring slot s % NS, NS = as many stages as fit the 160 KB LDS
-//     (3 at 128 x 256 x 128, up to 8 for small tiles).  Each wave moves its
-//     share of a stage with global_load_lds_dwordx4 (one instruction = 1 KB,
-//     written contiguously to LDS at M0): no VGPR staging, no ds_write.  The
+//     (2 at 256 x 256 x 128, 3 at 128 x 256, up to 8 for small tiles).  Each
+//     wave moves its share of a stage with global_load_lds_dwordx4 (one
+//     instruction = 1 KB, written contiguously to LDS at M0): no VGPR
+//     staging, no ds_write.  The
 //     loads are issued from inline asm, so the compiler does not wait for
 //     them; every issue moves the same number of loads (a stage past the end
 //     reloads the last stage into a slot nobody reads), so the wait before
@@ -45,6 +46,8 @@
 //     instead of one: the CU's vector-memory path accepts one 1 KB load per
 //     ~23 cycles, and a whole stage's loads inside one sub-step stalled the
 //     issuing waves for ~440 of its 512 MFMA cycles (measured at 256 x 256).
+//     Two slots (int8 256 x 256) leave the loads no later sub-step to go to;
+//     int4 weights at 256 x 256 (three slots) measured slower split.
 //   * The one barrier per stage sits before its last sub-step: it publishes
 //     stage kt + 1 and frees the slot of stage kt, which then receives stage
 //     kt + NS.
@@ -59,7 +62,7 @@
 //     then the workgroup stores whole 2*BN-byte rows with 16-byte lanes, so
 //     HBM sees full 128-byte lines instead of 32-byte row fragments.
 //   * int4 weights: a k-stage of a weight row is 64 bytes of nibbles (the ring
-//     then holds 4 stages at 128 x 256).  One ds_read_b128 per W block brings
+//     then holds 3 stages at 256 x 256).  One ds_read_b128 per W block brings
 //     the 32 nibbles of a pair of sub-steps; each sub-step's 16 are unpacked
 //     to int8 in registers (sign extension by xor/sub, byte permute) one
 //     sub-step ahead of their MFMAs.  The k mapping of a pair puts lane half h
@@ -282,15 +285,20 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 
   const int nk = K / BK;
   i32x4 wf[2][TN], xf[2][TM];
-  // Prologue: stages 0 .. NS-1 into slots 0 .. NS-1.  Every issue moves PS
+  // Prologue: stages 0 .. NS-2 into slots 0 .. NS-2, and part 0 of stage
+  // NS-1 into slot NS-1; stage 0's first sub-steps issue its other parts as
+  // every stage does for the stage before, so the first stage needs no code
+  // of its own (a copy of the loop body costs registers, and a spill reload
+  // would wait for every DMA load in flight).  Every issue moves the same
   // loads per wave; a stage past the end reloads stage nk-1 into a slot that
   // is never read, so the loads in flight at each wait are always the same
   // count.
+  constexpr int P0 = PS / DS;  // loads in part 0 of a stage
 #pragma unroll
   for (int st = 0; st < NS; ++st)
 #pragma unroll
-    for (int d = 0; d < PS; ++d) dma_one(min(st, nk - 1), st, d);
-  wait_vmcnt<(NS - 1) * PS>();  // stage 0 landed (loads complete in order)
+    for (int d = 0; d < (st < NS - 1 ? PS : P0); ++d) dma_one(min(st, nk - 1), st, d);
+  wait_vmcnt<(NS - 2) * PS + P0>();  // stage 0 landed (loads complete in order)
   __syncthreads();
 #pragma unroll
   for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
@@ -308,15 +316,14 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   // publishes stage kt+1 (NS-2 younger stages still in flight) and frees the
   // slot of stage kt, which receives stage kt+NS from that sub-step on.  The
   // first DS-1 sub-steps issue the rest of the loads the previous stage began
-  // (none in the first stage: the prologue loaded whole stages).
-  auto stage_body = [&](int kt, auto lastc, auto firstc) {
+  // (in the first stage, the rest of the prologue's stage NS-1).
+  auto stage_body = [&](int kt, auto lastc) {
     constexpr bool LAST = decltype(lastc)::value != 0;
-    constexpr bool FIRST = decltype(firstc)::value != 0;
     const int sl = kt % NS;
     const int pdst = min(kt - 1 + NS, nk - 1), psl = (kt + NS - 1) % NS;
 #define DMA_SUB(J)                                                                          \
   if constexpr ((J) < SUBS - 1) {                                                           \
-    step(icst<(J) + 1>{}, icst<1>{}, icst<(!FIRST && (J) + 1 < DS) ? (J) + 2 : 0>{},         \
+    step(icst<(J) + 1>{}, icst<1>{}, icst<((J) + 1 < DS) ? (J) + 2 : 0>{},                   \
          wf[(J) & 1], xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], pdst, psl);     \
   } else if constexpr (!LAST) {                                                             \
     wait_vmcnt<(NS - 2) * PS>();                                                            \
@@ -334,8 +341,7 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     }
 #undef DMA_SUB
   };
-  if (nk > 1) stage_body(0, icst<0>{}, icst<1>{});
-  for (int kt = 1; kt < nk - 1; ++kt) stage_body(kt, icst<0>{}, icst<0>{});
+  for (int kt = 0; kt < nk - 1; ++kt) stage_body(kt, icst<0>{});
   // Last stage.  The per-channel epilogue's scales are requested here, so
   // their latency hides behind the last MFMAs; indices are clamped, so the
   // loads are unconditional.
@@ -346,10 +352,7 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     sa_t = p.sa[min(m0 + tid % BM, M - 1)];
     if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
   }
-  if (nk > 1)
-    stage_body(nk - 1, icst<1>{}, icst<0>{});
-  else
-    stage_body(0, icst<1>{}, icst<1>{});
+  stage_body(nk - 1, icst<1>{});
   wait_vmcnt<0>();  // the reloads past the end land before LDS is reused
 
   // ---- epilogue: lane holds, per 32x32 block and group g, 4 consecutive n
@@ -459,38 +462,33 @@ hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
 
 template <int EPI, int WF>
 hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
-  // Estimated time = rounds of `cus` workgroups x tile area / tile rate.  The
-  // rates are throughputs measured on MI355X relative to a 256 x 256 tile (=
-  // 1) over M = 128 .. 16384 and (N, K) from (10240, 2560) to (4096, 12288),
-  // with back-to-back launches.  int8 weights: 128 x 256 streams as fast per
-  // MAC as 256 x 256 (whose two-slot ring cannot spread its loads) with half
-  // the fixed cost per tile and finer rounds, so 256 x 256 is not a
-  // candidate.  int4 weights: 256 x 256 has three slots and is the fastest
-  // tile per MAC.  Ties go to the larger tile.
+  // Estimated time = rounds x tile area / tile rate.  Rates are throughputs
+  // measured on MI355X relative to a 256 x 256 tile (= 1), with back-to-back
+  // launches, over M = 128 .. 8192 and (N, K) from (10240, 2560) to
+  // (4096, 12288).  A last round only partly full runs with less contention:
+  // it counts 0.6 + 0.4 x its occupancy.  Ties go to the larger tile.
   struct Cand { int bm, bn; double rate; };
-  static const Cand c8[] = {{128, 256, 1.05}, {128, 128, 0.87}, {128, 64, 0.51},
-                            {64, 128, 0.50},  {64, 64, 0.40}};
-  static const Cand c4[] = {{256, 256, 1.0},  {128, 256, 0.94}, {128, 128, 0.72},
-                            {128, 64, 0.44},  {64, 128, 0.43},  {64, 64, 0.35}};
+  static const Cand c8[] = {{256, 256, 1.0},   {128, 256, 0.87}, {128, 128, 0.75},
+                            {128, 64, 0.517},  {64, 128, 0.508}, {64, 64, 0.40}};
+  static const Cand c4[] = {{256, 256, 1.0},   {128, 256, 0.77}, {128, 128, 0.60},
+                            {128, 64, 0.41},   {64, 128, 0.40},  {64, 64, 0.32}};
   const Cand* cands = WF == W_I4 ? c4 : c8;
-  const int nc = WF == W_I4 ? 6 : 5;
   const int cus = num_cus();
   int best = 0;
   double best_cost = 1e300;
-  for (int i = 0; i < nc; ++i) {
+  for (int i = 0; i < 6; ++i) {
     const int64_t tiles =
         (int64_t)((a.M + cands[i].bm - 1) / cands[i].bm) * ((a.N + cands[i].bn - 1) / cands[i].bn);
-    const double cost =
-        (double)((tiles + cus - 1) / cus) * cands[i].bm * cands[i].bn / cands[i].rate;
+    const int64_t full = tiles / cus, rest = tiles % cus;
+    const double rounds = (double)full + (rest ? 0.6 + 0.4 * (double)rest / cus : 0.0);
+    const double cost = rounds * cands[i].bm * cands[i].bn / cands[i].rate;
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = i;
     }
   }
   const int bm = cands[best].bm, bn = cands[best].bn;
-  if constexpr (WF == W_I4) {
-    if (bm == 256) return run_dma<256, 256, 128, EPI, WF>(a, s);
-  }
+  if (bm == 256) return run_dma<256, 256, 128, EPI, WF>(a, s);
   if (bm == 128 && bn == 256) return run_dma<128, 256, 128, EPI, WF>(a, s);
   if (bm == 128 && bn == 128) return run_dma<128, 128, 128, EPI, WF>(a, s);
   if (bm == 128) return run_dma<128, 64, 128, EPI, WF>(a, s);
