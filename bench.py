@@ -563,6 +563,13 @@ def gemm_kernel_name(M, N, K, dev):
             cost = rounds * bm * bn / rate
             if best_cost is None or cost < best_cost * 0.999:
                 best, best_cost = (bm, bn), cost
+        tm, tn = -(-M // 256), -(-N // 256)
+        T = tm * tn
+        R = T % cus
+        if T > cus and 0 < R and 2 * R <= cus and R % tm == 0:
+            tail = (0.6 + 0.4 * 2 * R / cus) * 128 * 256 / 0.87
+            if (T // cus) * 256 * 256 + tail < best_cost * 0.999:
+                return "gemm_dma_mixed_kernel<PC, I8> (256x256 tiles + 128x256 last round)"
         return "gemm_dma_kernel<%d, %d, 128, PC, I8> (%dx%d tiles)" % (best + best)
     return "gemm_kernel<PC>"
 

@@ -451,6 +451,27 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
   dma_tile<BM, BN, BK, EPI, WF>(p, m0, n0, smem);
 }
 
+// Two tile sizes in one grid, so that the last round of workgroups is not
+// half empty: workgroups [0, nbig) take 256 x 256 tiles of columns
+// [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
+// many tiles of half the work.  Workgroups start in index order, so the small
+// tiles form the last round; each region has its own XCD remap.
+template <int EPI, int WF>
+__global__ __launch_bounds__(256, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
+                                                                int nsplit) {
+  constexpr int S1 = DmaCfg<256, 256, 128, WF>::SMEM, S2 = DmaCfg<128, 256, 128, WF>::SMEM;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
+  const int b = blockIdx.x;
+  int m0, n0;
+  if (b < nbig) {
+    tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
+    dma_tile<256, 256, 128, EPI, WF>(p, m0, n0, smem);
+  } else {
+    tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
+    dma_tile<128, 256, 128, EPI, WF>(p, m0, n0, smem);
+  }
+}
+
 namespace {
 
 template <int BM, int BN, int BK, int EPI, int WF = W_I8>
@@ -485,6 +506,26 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = i;
+    }
+  }
+  // Mixed grid: when the 256 x 256 tiles leave a last round at most half
+  // full, made of whole tile columns, those columns can run as twice as many
+  // 128 x 256 tiles of half the length, so the last round is full and half
+  // as long.
+  {
+    const int tm = (a.M + 255) / 256, tn = (a.N + 255) / 256;
+    const int64_t T = (int64_t)tm * tn;
+    const int R = (int)(T % cus);
+    if (T > cus && R > 0 && 2 * R <= cus && R % tm == 0) {
+      const double tail = (0.6 + 0.4 * 2.0 * R / cus) * 128 * 256 / cands[1].rate;
+      if ((double)(T / cus) * 256 * 256 / cands[0].rate + tail < best_cost * 0.999) {
+        const int tail_cols = R / tm;
+        const int nsplit = (tn - tail_cols) * 256;
+        const int nbig = (int)(T - R);
+        const int nsmall = ((a.M + 127) / 128) * tail_cols;
+        gemm_dma_mixed_kernel<EPI, WF><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
+        return hipGetLastError();
+      }
     }
   }
   const int bm = cands[best].bm, bn = cands[best].bn;

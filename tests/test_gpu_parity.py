@@ -98,12 +98,13 @@ def test_int8_matmul_reference_shapes(bitexact_shapes):
 
 
 # M > 64, K % 128 == 0, N % 8 == 0: the LDS-DMA kernel at each int32 tile the
-# dispatcher picks (64x64: 256x256 and 300x520; 128x256: 2048x10240; 128x128:
-# 1024x4096; 128x64: 128x10240; 64x128: 192x10240; 256x256: 4096x8192).
+# dispatcher picks (64x64: 256x256 and 300x520; the mixed 256x256 + 128x256
+# grid: 2048x10240; 128x256: 2048x4096; 128x128: 1024x4096; 128x64: 128x10240;
+# 64x128: 192x10240; 256x256: 4096x8192).
 @pytest.mark.parametrize("M,N,K", [(65, 64, 64), (256, 256, 128), (300, 520, 384),
                                    (1000, 130, 1000), (2, 3, 1), (70, 90, 17),
                                    (2048, 10240, 128), (1024, 4096, 256), (128, 10240, 128),
-                                   (192, 10240, 128), (4096, 8192, 256)])
+                                   (192, 10240, 128), (4096, 8192, 256), (2048, 4096, 256)])
 def test_int8_matmul_more_shapes(M, N, K):
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
@@ -129,9 +130,9 @@ def test_int8_matmul_extremes():
 # Shapes cover every GEMM variant: skinny (M <= 64), the register-staged tiled
 # kernel (K % 128 != 0 or N % 8 != 0) and the LDS-DMA kernel at each tile the
 # dispatcher picks: 128x64 (M=128, N=10240), 64x64 (M=300/257), 128x128
-# (M=2048, N=2048), 128x256 (M=600/2048, and M=1000, N=16640 with a partial
-# last tile row), 256x256 (M=1024, N=10240, and the full-size tests below);
-# 64x128 in the midpoint test below.
+# (M=2048, N=2048), 128x256 (M=600), 256x256 (M=1024, N=10240), and the mixed
+# 256x256 + 128x256 grid (M=2048, N=10240; M=1000, N=16640 with a partial last
+# tile row; the full-size tests below); 64x128 in the midpoint test below.
 @pytest.mark.parametrize("M,N,K", [(2, 16, 64), (7, 33, 130), (16, 1000, 2560), (33, 257, 513),
                                    (64, 128, 256), (65, 200, 320), (128, 10240, 2560),
                                    (300, 1000, 1024), (257, 512, 4096), (100, 70, 100),
@@ -159,8 +160,8 @@ def test_perchannel_gemm_matches_linear():
 # where the binary32 product lands exactly on an fp16 midpoint.  Random int8
 # operands with random binary32 scales put a few hundred such elements in each
 # case (the test asserts that they are there); the shapes select, in order,
-# the 128 x 64, 64 x 64 (twice), 64 x 128 and 256 x 256 LDS-DMA tiles, the
-# register-staged kernel (K % 128 != 0), the skinny kernel and the GEMV.
+# the 128 x 64, 64 x 64 (twice) and 64 x 128 LDS-DMA tiles, the mixed grid,
+# the register-staged kernel (K % 128 != 0), the skinny kernel and the GEMV.
 @pytest.mark.parametrize("M,N,K,rows", [
     (128, 10240, 2560, None), (128, 2560, 10240, None), (1000, 1000, 1024, None),
     (192, 10240, 2560, None),
@@ -320,8 +321,9 @@ def test_w4_repack_matches_unpack():
 # M > 64, K % 128 == 0, N % 8 == 0 runs the LDS-DMA kernel with int4 weights
 # (512x640, 256x1024 and 300x136 -- an odd stage count -- on 64x64 tiles,
 # 192x6144 and 192x10240 on 64x128, 2048x2048 on 128x128, 2048x4096 on
-# 128x256, 2048x10240 on 256x256; 128x64 in the midpoint test below); N % 8 != 0
-# the register-staged kernel; M <= 64 the skinny kernel.
+# 128x256, 2048x10240 on the mixed grid; 256x256 in the full-size test and
+# 128x64 in the midpoint test below); N % 8 != 0 the register-staged kernel;
+# M <= 64 the skinny kernel.
 @pytest.mark.parametrize("M,N,K", [(1, 32, 64), (9, 70, 160), (1, 12288, 4096),
                                    (16, 4096, 12288), (64, 300, 1024), (100, 300, 1024),
                                    (512, 640, 2048), (7, 33, 98), (256, 1024, 512),
