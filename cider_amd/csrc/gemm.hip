@@ -368,16 +368,29 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                        int gs, hipStream_t s) {
   if (gemv_q_supported(a, wf, false)) return launch_gemv_q(a, wf, epi, gs, s);
-  if (a.M <= 64) return launch_skinny(a, wf, epi, sw_half, gs, s);
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
                    (a.sw == nullptr || aligned16(a.sw));
-  if (epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 && a.N % 8 == 0)
-    return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)
+  const bool dma = epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 &&
+                   a.N % 8 == 0;
+  const bool dma_pg = epi == EPI_PG && (gs == 64 || gs == 128) && vec && a.K % 128 == 0 &&
+                      a.N % 8 == 0;
+  if (a.M <= 64) {
+    // The LDS-DMA kernel's 64 x 64 tiles load whole weight rows (one 16-byte
+    // lane after another) and beat the skinny kernel, whose MFMA operand loads
+    // touch 16 rows x 32-64 B, once they fill half the CUs or past M = 48
+    // (N=12288 K=4096 M=16: 12.9 vs 18.7 us; N=4096 K=12288 M=16, 64 tiles:
+    // 24.1 vs 17.1 us).
+    // Per-group stays on the skinny kernel: at 64-row tiles the exact group
+    // flush outweighs the tile's MFMAs (M=16 N=12288 K=4096 int4: 22.1 vs
+    // 19.9 us).
+    if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
+    return launch_skinny(a, wf, epi, sw_half, gs, s);
+  }
+  if (dma) return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)
   // per-group gs 64 / 128 on the LDS-DMA per-group kernel (gs 256 and other
   // shapes on the register-staged kernel)
-  if (epi == EPI_PG && (gs == 64 || gs == 128) && vec && a.K % 128 == 0 && a.N % 8 == 0)
-    return launch_gemm_dma_pg(a, gs, sw_half, wf, s);  // gemm_dma_pg.hip
+  if (dma_pg) return launch_gemm_dma_pg(a, gs, sw_half, wf, s);  // gemm_dma_pg.hip
   if (epi == EPI_I32) return run_tiled<256, 256, W_I8, EPI_I32, false, 0>(a, vec, s);
   if (epi == EPI_PC) {
     if (wf == W_I4) return run_tiled<256, 256, W_I4, EPI_PC, false, 0>(a, vec, s);

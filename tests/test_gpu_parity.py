@@ -411,7 +411,7 @@ def test_gemv_q_exact(M, N, K):
 # sequential group chain, so it is bit-exact too (K = 12288 at gs = 64: 192
 # groups, a chain long enough for any other order to show).
 @pytest.mark.parametrize("M,N,K", [(16, 2560, 10240), (32, 1024, 8192), (3, 256, 16384),
-                                   (64, 512, 4096)])
+                                   (48, 512, 4096)])
 def test_skinny_wave_splits_exact(M, N, K):
     x, w, sw, b = synth_pc(M, N, K, 90 + M)
     y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
@@ -423,6 +423,38 @@ def test_skinny_wave_splits_exact(M, N, K):
     packed, sw4 = O.pack_weight_int4(wf)
     y4 = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
     assert_bits_equal(y4, O.w4a8_linear(x, packed, sw4), f"skinny w4 {M}x{N}x{K}")
+
+
+# 5 <= M <= 64 with at least 128 column tiles of 64 (or M > 48) runs the
+# LDS-DMA kernel's 64 x 64 tiles (per-channel, int32, int4 weights) instead of
+# the skinny kernel: rows past M are loaded from the last valid row and never
+# stored.  Per-group stays on the skinny kernel at these shapes, checked too.
+@pytest.mark.parametrize("M,N,K", [(16, 10240, 2560), (5, 12288, 512), (33, 8192, 1024),
+                                   (64, 512, 4096), (49, 96, 256)])
+def test_small_m_dma_tiles(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 98 + M)
+    y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
+    assert_bits_equal(y, O.perchannel_linear(x, w, sw, b), f"small-M dma pc {M}x{N}x{K}")
+    q = np.random.default_rng(99).integers(-128, 128, (M, K), dtype=np.int8)
+    c = C.int8_matmul_int32(T(q), T(w)).cpu().numpy()
+    assert np.array_equal(c, O.int8_matmul_int32(q, w)), f"small-M dma i32 {M}x{N}x{K}"
+    wf = np.random.default_rng(100).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    y4 = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+    assert_bits_equal(y4, O.w4a8_linear(x, packed, sw4), f"small-M dma w4 {M}x{N}x{K}")
+    # per-group at the same shapes (skinny kernel, sequential group chain)
+    for gs in (64, 128):
+        if K % gs:
+            continue
+        swg = O.synth_scales((K // gs, N), 101 + gs)
+        yg = H(C.pergroup_linear(T(x), T(w), T(swg), gs))
+        assert_bits_equal(yg, O.pergroup_linear(x, w, swg, gs), f"small-M dma pg{gs} {M}x{N}x{K}")
+        w4 = np.random.default_rng(102).integers(-8, 8, (N, K), dtype=np.int8)
+        pk = O.pack_w4_lo_first(w4)
+        sc = O.synth_scales((K // gs, N), 103).astype(np.float16)
+        yw = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs))
+        assert_bits_equal(yw, O.w4a8_pergroup_linear(x, pk, sc, gs),
+                          f"small-M dma w4g{gs} {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128])
