@@ -356,6 +356,79 @@ int cider_rmsnorm_quantize(const void* x_f16, const void* add_f16, void* sum_f16
       fn);
 }
 
+namespace {
+
+// byte ranges [a, a + na) and [b, b + nb) overlap (either pointer NULL: no)
+bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  if (a == nullptr || b == nullptr) return false;
+  const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+  return pa < pb + nb && pb < pa + na;
+}
+
+int check_producer_mv(const char* fn, const void* x, const int8_t* w, const float* scale_w,
+                      const void* y, int64_t N, int64_t K) {
+  CIDER_TRY(check_dims(fn, 1, N, K));
+  if (N < 1 || K < 1) return fail(CIDER_E_INVALID, "%s: N and K must be >= 1", fn);
+  CIDER_TRY(need(fn, x, "x", true));
+  CIDER_TRY(need(fn, w, "w", true));
+  CIDER_TRY(need(fn, scale_w, "scale_w", true));
+  CIDER_TRY(need(fn, y, "y", true));
+  if (!cider::mv_producer_supported(x, w, (int)K))
+    return fail(CIDER_E_UNSUPPORTED,
+                "%s: needs K %% 256 == 0, K <= 16384 and 16-byte aligned x and w (K=%lld)", fn,
+                (long long)K);
+  if (((uintptr_t)y & 1) != 0) return fail(CIDER_E_INVALID, "%s: y must be 2-byte aligned", fn);
+  return CIDER_OK;
+}
+
+}  // namespace
+
+int cider_rmsnorm_mv(const void* x_f16, const void* add_f16, void* sum_f16, const void* norm_w_f16,
+                     float eps, const int8_t* w, const float* scale_w, const void* bias_f16,
+                     void* y_f16, int64_t N, int64_t K, void* stream) {
+  static const char* fn = "cider_rmsnorm_mv";
+  CIDER_TRY(check_producer_mv(fn, x_f16, w, scale_w, y_f16, N, K));
+  if (!(eps >= 0.0f)) return fail(CIDER_E_INVALID, "%s: eps must be >= 0", fn);
+  CIDER_TRY(need(fn, norm_w_f16, "norm_w", true));
+  if ((add_f16 == nullptr) != (sum_f16 == nullptr))
+    return fail(CIDER_E_INVALID, "%s: add and sum come together", fn);
+  if (!aligned16(add_f16) || !aligned16(sum_f16) || !aligned16(norm_w_f16) ||
+      ((uintptr_t)bias_f16 & 1) != 0)
+    return fail(CIDER_E_INVALID, "%s: add, sum and norm_w must be 16-byte aligned", fn);
+  const size_t row = (size_t)K * 2;
+  if (overlaps(sum_f16, row, x_f16, row) || overlaps(sum_f16, row, add_f16, row))
+    return fail(CIDER_E_INVALID, "%s: sum must not overlap x or add (other workgroups read them)",
+                fn);
+  if (overlaps(y_f16, (size_t)N * 2, x_f16, row) || overlaps(y_f16, (size_t)N * 2, add_f16, row) ||
+      overlaps(y_f16, (size_t)N * 2, sum_f16, row))
+    return fail(CIDER_E_INVALID, "%s: y must not overlap x, add or sum", fn);
+  return hip_status(
+      cider::launch_mv_producer(
+          add_f16 ? cider::XM_ADDNORM : cider::XM_NORM, reinterpret_cast<const uint16_t*>(x_f16),
+          reinterpret_cast<const uint16_t*>(add_f16), reinterpret_cast<uint16_t*>(sum_f16),
+          reinterpret_cast<const uint16_t*>(norm_w_f16), eps, w, scale_w,
+          reinterpret_cast<const uint16_t*>(bias_f16), reinterpret_cast<uint16_t*>(y_f16), (int)N,
+          (int)K, (hipStream_t)stream),
+      fn);
+}
+
+int cider_swiglu_mv(const void* gate_up_f16, const int8_t* w, const float* scale_w,
+                    const void* bias_f16, void* y_f16, int64_t N, int64_t K, void* stream) {
+  static const char* fn = "cider_swiglu_mv";
+  CIDER_TRY(check_producer_mv(fn, gate_up_f16, w, scale_w, y_f16, N, K));
+  if (((uintptr_t)bias_f16 & 1) != 0)
+    return fail(CIDER_E_INVALID, "%s: bias must be 2-byte aligned", fn);
+  if (overlaps(y_f16, (size_t)N * 2, gate_up_f16, (size_t)K * 4))
+    return fail(CIDER_E_INVALID, "%s: y must not overlap gate_up", fn);
+  return hip_status(
+      cider::launch_mv_producer(cider::XM_SWIGLU, reinterpret_cast<const uint16_t*>(gate_up_f16),
+                                nullptr, nullptr, nullptr, 0.0f, w, scale_w,
+                                reinterpret_cast<const uint16_t*>(bias_f16),
+                                reinterpret_cast<uint16_t*>(y_f16), (int)N, (int)K,
+                                (hipStream_t)stream),
+      fn);
+}
+
 int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* sa, int64_t M,
                             int64_t I, void* stream) {
   static const char* fn = "cider_silu_mul_quantize";

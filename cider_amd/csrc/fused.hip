@@ -36,69 +36,12 @@
 // and max), and SwiGLU without quantization is elementwise over the grid.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "norm_common.hpp"
 #include "quant_common.hpp"
 
 namespace cider {
 
 namespace {
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
-  return v;
-}
-
-__device__ __forceinline__ uint16_t lo16(int32_t w) { return (uint16_t)((uint32_t)w & 0xffffu); }
-__device__ __forceinline__ uint16_t hi16(int32_t w) { return (uint16_t)((uint32_t)w >> 16); }
-__device__ __forceinline__ int32_t pack2(uint16_t a, uint16_t b) {
-  return (int32_t)((uint32_t)a | ((uint32_t)b << 16));
-}
-
-// h(a + b) elementwise on 8 fp16 values
-__device__ __forceinline__ i32x4 add8(i32x4 a, i32x4 b) {
-  i32x4 r;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    r[j] = pack2(f2h(h2f(lo16(a[j])) + h2f(lo16(b[j]))), f2h(h2f(hi16(a[j])) + h2f(hi16(b[j]))));
-  return r;
-}
-
-__device__ __forceinline__ float sumsq8(i32x4 v, float s) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const float a = h2f(lo16(v[j])), b = h2f(hi16(v[j]));
-    s = s + a * a;
-    s = s + b * b;
-  }
-  return s;
-}
-
-// RMSNorm output of one element: h(f32(w) * f32(h(x * r)))
-__device__ __forceinline__ uint16_t norm1(uint16_t x, uint16_t w, float r) {
-  return f2h(h2f(w) * h2f(f2h(h2f(x) * r)));
-}
-
-__device__ __forceinline__ i32x4 norm8(i32x4 v, i32x4 w, float r) {
-  i32x4 o;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    o[j] = pack2(norm1(lo16(v[j]), lo16(w[j]), r), norm1(hi16(v[j]), hi16(w[j]), r));
-  return o;
-}
-
-__device__ __forceinline__ uint16_t swiglu1(uint16_t g, uint16_t u) {
-  const float gf = h2f(g);
-  const uint16_t a = f2h(gf / (1.0f + expf(-gf)));
-  return f2h(h2f(a) * h2f(u));
-}
-
-__device__ __forceinline__ i32x4 swiglu8(i32x4 g, i32x4 u) {
-  i32x4 o;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    o[j] = pack2(swiglu1(lo16(g[j]), lo16(u[j])), swiglu1(hi16(g[j]), hi16(u[j])));
-  return o;
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm (+ residual add) (+ per-token quantize)
@@ -234,15 +177,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(
 // Few rows (decode): one 256-thread workgroup per row, so a row's loads come
 // from four waves at once; the sums and maxima go through LDS in wave order.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float block_sum4(float v, float* red) {
-  const int wave = threadIdx.x >> 6;
-  v = wave_sum(v);
-  __syncthreads();  // red may still be read from the previous reduction
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  return ((red[0] + red[1]) + red[2]) + red[3];
-}
-
 __device__ __forceinline__ float block_max4(float v, float* red) {
   const int wave = threadIdx.x >> 6;
   v = wave_max(v);

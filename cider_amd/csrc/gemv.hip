@@ -27,6 +27,7 @@
 //     waves to cover HBM latency on short-N shapes.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "norm_common.hpp"
 
 namespace cider {
 
@@ -259,11 +260,26 @@ __device__ __forceinline__ float dot8f(uint32_t w0, uint32_t w1, const f32x4& xa
   return d;
 }
 
-template <bool PG, int U>
+// Producer run inside the x staging of the M == 1 linear (XM):
+//   XM_PLAIN   x is the fp16 input row;
+//   XM_NORM    x' = RMSNorm(x) with weight nw (fused.hip's rmsnorm order);
+//   XM_ADDNORM h = x + add (fp16), written to hsum by workgroup 0, x' = RMSNorm(h);
+//   XM_SWIGLU  x is a [gate | up] row of 2K, x' = h(h(silu(gate)) * up).
+// Thread t stages the 8-element chunks t, t + 256, ... as the producer
+// kernels do (the RMSNorm sum of squares in that order, then block_sum4), so
+// x' is bit-identical to what the producer kernel writes.
+struct MvProducer {
+  const uint16_t* add = nullptr;  // XM_ADDNORM
+  uint16_t* hsum = nullptr;       // XM_ADDNORM: h = x + add
+  const uint16_t* nw = nullptr;   // XM_NORM / XM_ADDNORM
+  float eps = 0.0f;
+};
+
+template <bool PG, int U, int XM = XM_PLAIN>
 __global__ __launch_bounds__(256) void mv_wide_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ y, int N, int K, int gs) {
+    uint16_t* __restrict__ y, int N, int K, int gs, MvProducer pp) {
   constexpr int kRows = 8;  // rows per workgroup: 2 per wave
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn[];
   float* xs = reinterpret_cast<float*>(dyn);
@@ -285,11 +301,22 @@ __global__ __launch_bounds__(256) void mv_wide_kernel(
 
   // ---- stage x as fp32 (and the group scales); x reads first, then the
   // first 2U weight blocks, then the conversions and LDS stores
-  constexpr int XR = 4;
+  // fused modes hold the whole row: ceil(K / 2048) chunks per thread (U <= 4:
+  // K <= 2048; U <= 8: K <= 4096; U <= 12: K <= 6144; U == 16: K <= 16384)
+  constexpr int XR = XM == XM_PLAIN ? 4 : (U <= 4 ? 1 : U <= 8 ? 2 : U <= 12 ? 3 : 8);
   const int nchunk = K >> 3;
   i32x4 xr[XR];
+  float ss = 0.0f;  // XM_NORM / XM_ADDNORM: the sum of squares of this thread's chunks
 #pragma unroll
-  for (int q = 0; q < XR; ++q) xr[q] = ld16(x + 8 * min(tid + q * 256, nchunk - 1));
+  for (int q = 0; q < XR; ++q) {
+    const int e = min(tid + q * 256, nchunk - 1);
+    if constexpr (XM == XM_SWIGLU) {
+      xr[q] = swiglu8(ld16(x + 8 * e), ld16(x + K + 8 * e));
+    } else {
+      xr[q] = ld16(x + 8 * e);
+      if constexpr (XM == XM_ADDNORM) xr[q] = add8(xr[q], ld16(pp.add + 8 * e));
+    }
+  }
   constexpr int SR = 4;
   float sr[SR];
   auto load_s = [&](int e) -> float {
@@ -309,6 +336,27 @@ __global__ __launch_bounds__(256) void mv_wide_kernel(
 #pragma unroll
   for (int u = 0; u < U; ++u) wb[u] = load_w(U + u);
 
+  if constexpr (XM == XM_NORM || XM == XM_ADDNORM) {
+    // whole row in registers (XR * 256 chunks cover K <= 16384): the sum of
+    // squares in chunk order, h written out once, then the normalisation
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      const int e = tid + q * 256;
+      if (e < nchunk) {
+        if constexpr (XM == XM_ADDNORM)
+          if (blockIdx.x == 0) *reinterpret_cast<i32x4*>(pp.hsum + 8 * e) = xr[q];
+        ss = sumsq8(xr[q], ss);
+      }
+    }
+    __shared__ float red[4];
+    ss = block_sum4(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)K + pp.eps);
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      const int e = tid + q * 256;
+      if (e < nchunk) xr[q] = norm8(xr[q], ld16(pp.nw + 8 * e), r);
+    }
+  }
   auto store_x = [&](int e, i32x4 v) {
     f32x4 lo, hi;
 #pragma unroll
@@ -326,7 +374,8 @@ __global__ __launch_bounds__(256) void mv_wide_kernel(
     const int e = tid + q * 256;
     if (e < nchunk) store_x(e, xr[q]);
   }
-  for (int e = tid + XR * 256; e < nchunk; e += 256) store_x(e, ld16(x + 8 * e));
+  if constexpr (XM == XM_PLAIN)
+    for (int e = tid + XR * 256; e < nchunk; e += 256) store_x(e, ld16(x + 8 * e));
   if constexpr (PG) {
 #pragma unroll
     for (int q = 0; q < SR; ++q) {
@@ -414,10 +463,11 @@ hipError_t pick_u(const uint16_t* x, const int8_t* w, const float* sw, const uin
 
 namespace {
 
-template <bool PG, int U>
+template <bool PG, int U, int XM = XM_PLAIN>
 hipError_t run_wide(const uint16_t* x, const int8_t* w, const float* sw, const uint16_t* bias,
-                    uint16_t* y, int N, int K, int gs, size_t lds, hipStream_t s) {
-  mv_wide_kernel<PG, U><<<(N + 7) / 8, 256, lds, s>>>(x, w, sw, bias, y, N, K, gs);
+                    uint16_t* y, int N, int K, int gs, size_t lds, hipStream_t s,
+                    const MvProducer& pp = MvProducer{}) {
+  mv_wide_kernel<PG, U, XM><<<(N + 7) / 8, 256, lds, s>>>(x, w, sw, bias, y, N, K, gs, pp);
   return hipGetLastError();
 }
 
@@ -434,6 +484,45 @@ hipError_t pick_wide(const uint16_t* x, const int8_t* w, const float* sw, const 
 }
 
 }  // namespace
+
+namespace {
+
+template <int XM>
+hipError_t pick_producer(const uint16_t* x, const int8_t* w, const float* sw,
+                         const uint16_t* bias, uint16_t* y, int N, int K, size_t lds,
+                         hipStream_t s, const MvProducer& pp) {
+  const int nb = K >> 8;
+  if (nb <= 8) return run_wide<false, 4, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+  if (nb <= 10) return run_wide<false, 5, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+  if (nb <= 12) return run_wide<false, 6, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+  if (nb <= 16) return run_wide<false, 8, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+  if (nb <= 24) return run_wide<false, 12, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+  return run_wide<false, 16, XM>(x, w, sw, bias, y, N, K, 0, lds, s, pp);
+}
+
+}  // namespace
+
+bool mv_producer_supported(const void* x, const void* w, int K) {
+  return K % 256 == 0 && K <= kMaxF32K && (((uintptr_t)w & 15) == 0) &&
+         (((uintptr_t)x & 15) == 0);
+}
+
+hipError_t launch_mv_producer(int xm, const uint16_t* x, const uint16_t* add, uint16_t* hsum,
+                              const uint16_t* nw, float eps, const int8_t* w, const float* sw,
+                              const uint16_t* bias, uint16_t* y, int N, int K, hipStream_t s) {
+  MvProducer pp;
+  pp.add = add;
+  pp.hsum = hsum;
+  pp.nw = nw;
+  pp.eps = eps;
+  const size_t lds = (size_t)K * sizeof(float);
+  switch (xm) {
+    case XM_NORM: return pick_producer<XM_NORM>(x, w, sw, bias, y, N, K, lds, s, pp);
+    case XM_ADDNORM: return pick_producer<XM_ADDNORM>(x, w, sw, bias, y, N, K, lds, s, pp);
+    case XM_SWIGLU: return pick_producer<XM_SWIGLU>(x, w, sw, bias, y, N, K, lds, s, pp);
+    default: return hipErrorInvalidValue;
+  }
+}
 
 hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,

@@ -38,6 +38,15 @@ hipError_t launch_gemv_qx(const uint16_t* x, const GemmArgs& a, int wf, int epi,
                           hipStream_t s);
 
 // M == 1 fp16-activation MV (per-channel when gs == 0, else per-group).
+// M == 1 per-channel linear with a producer run in its x staging (gemv.hip):
+// XM_NORM x' = RMSNorm(x); XM_ADDNORM h = x + add (written to hsum by one
+// workgroup), x' = RMSNorm(h); XM_SWIGLU x = [gate | up] of 2K, x' = SwiGLU.
+// Requires mv_producer_supported (K % 256 == 0, K <= 16384, 16-byte aligned).
+enum { XM_PLAIN = 0, XM_NORM = 1, XM_ADDNORM = 2, XM_SWIGLU = 3 };
+bool mv_producer_supported(const void* x, const void* w, int K);
+hipError_t launch_mv_producer(int xm, const uint16_t* x, const uint16_t* add, uint16_t* hsum,
+                              const uint16_t* nw, float eps, const int8_t* w, const float* sw,
+                              const uint16_t* bias, uint16_t* y, int N, int K, hipStream_t s);
 hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,
                      hipStream_t s);

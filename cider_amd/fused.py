@@ -167,3 +167,61 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                                          float(scale), _ptr(ws), ws.numel(), _ptr(out), H, KV, d,
                                          T, _stream_ptr(dev, stream)))
     return out
+
+
+def _mv_linear(fn: str, linear, K: int):
+    """(w_int8, scale_w, bias, N) of a per-channel int8 CiderLinear with in_features K."""
+    if getattr(linear, "group_size", None) != 0 or not hasattr(linear, "w_int8"):
+        raise ValueError(f"{fn}: linear must be a per-channel int8 CiderLinear")
+    N, Kw = linear.w_int8.shape
+    if Kw != K:
+        raise ValueError(f"{fn}: linear takes K={Kw}, the input has K={K}")
+    return linear.w_int8, linear.scale_w, linear.bias, N
+
+
+def rmsnorm_mv(x: torch.Tensor, weight: torch.Tensor, eps: float, linear,
+               add: Optional[torch.Tensor] = None, stream=None):
+    """Decode (one token): ``linear(RMSNorm(h))`` in one launch, with
+    h = x, or h = fp16(x + add) when ``add`` is given.  Bit-identical to
+    ``linear(rmsnorm_quantize(x, weight, eps, add).y)``.  Returns (h, y): h
+    [1, K] (a new tensor when add is given, else x) and y [1, N] fp16.  x and
+    add are [1, K] or [K] fp16; linear is a per-channel int8 CiderLinear."""
+    fn = "rmsnorm_mv"
+    dev = _require_gpu(fn, x, weight, add)
+    K = x.numel()
+    _f16(fn, "x", x)
+    _f16(fn, "weight", weight)
+    if weight.numel() != K:
+        raise ValueError(f"{fn}: weight has {weight.numel()} elements, expected K={K}")
+    if add is not None:
+        _f16(fn, "add", add)
+        if add.numel() != K:
+            raise ValueError(f"{fn}: add has {add.numel()} elements, x has {K}")
+    w, sw, bias, N = _mv_linear(fn, linear, K)
+    lib = _lib.load()
+    with _on_stream(dev, stream):
+        h = torch.empty((1, K), dtype=torch.float16, device=dev) if add is not None else None
+        y = torch.empty((1, N), dtype=torch.float16, device=dev)
+        _lib.check(lib.cider_rmsnorm_mv(_ptr(x), _ptr(add), _ptr(h), _ptr(weight), float(eps),
+                                        _ptr(w), _ptr(sw), _ptr(bias), _ptr(y), N, K,
+                                        _stream_ptr(dev, stream)))
+    return (x.reshape(1, K) if h is None else h), y
+
+
+def swiglu_mv(gate_up: torch.Tensor, linear, stream=None) -> torch.Tensor:
+    """Decode (one token): ``linear(SwiGLU(gate_up))`` in one launch, gate_up
+    [1, 2I] (gate first).  Bit-identical to
+    ``linear(silu_mul_quantize(gate_up, want_q=False)[0])``.  Returns y [1, N]."""
+    fn = "swiglu_mv"
+    dev = _require_gpu(fn, gate_up)
+    _f16(fn, "gate_up", gate_up)
+    if gate_up.numel() % 2:
+        raise ValueError(f"{fn}: gate_up must hold [gate | up] of equal halves")
+    K = gate_up.numel() // 2
+    w, sw, bias, N = _mv_linear(fn, linear, K)
+    lib = _lib.load()
+    with _on_stream(dev, stream):
+        y = torch.empty((1, N), dtype=torch.float16, device=dev)
+        _lib.check(lib.cider_swiglu_mv(_ptr(gate_up), _ptr(w), _ptr(sw), _ptr(bias), _ptr(y),
+                                       N, K, _stream_ptr(dev, stream)))
+    return y

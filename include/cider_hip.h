@@ -160,6 +160,28 @@ int cider_rmsnorm_quantize(const void* x_f16, const void* add_f16, void* sum_f16
 int cider_silu_mul_quantize(const void* gu_f16, void* y_f16, int8_t* q, float* sa,
                             int64_t M, int64_t I, void* stream);
 
+/* Decode (M == 1) per-channel linear y = W8A8(x') with the producer of its
+ * input x' run inside the linear's x staging, one launch instead of two:
+ *   cider_rmsnorm_mv: x' = RMSNorm(h) as cider_rmsnorm_quantize's y, with
+ *     h = x, or h = h(x + add) written to sum when add != NULL (sum must not
+ *     overlap x or add: every workgroup reads them);
+ *   cider_swiglu_mv: x' = SwiGLU of gate_up [2K] (gate first), as
+ *     cider_silu_mul_quantize's y.
+ * then y [N] exactly as cider_perchannel_linear at M == 1 (the fp16 MV) on
+ * x'. Both are bit-identical to the pair of calls they replace (same per-
+ * element formulas, same sum-of-squares order). The reference has no
+ * counterpart: its models run the producer as an MLX op before the linear
+ * (cider/fused_hybrid.py:142-213). Requires K % 256 == 0, K <= 16384 and
+ * 16-byte aligned x / gate_up, w, add, sum, norm_w; else CIDER_E_UNSUPPORTED
+ * (use the two calls). y must not overlap any input. */
+int cider_rmsnorm_mv(const void* x_f16, const void* add_f16, void* sum_f16,
+                     const void* norm_w_f16, float eps, const int8_t* w,
+                     const float* scale_w, const void* bias_f16, void* y_f16,
+                     int64_t N, int64_t K, void* stream);
+int cider_swiglu_mv(const void* gate_up_f16, const int8_t* w, const float* scale_w,
+                    const void* bias_f16, void* y_f16, int64_t N, int64_t K,
+                    void* stream);
+
 /* Per-head RMSNorm of q and k (weights [D]) and rotate-half RoPE on the rows
  * of a fused q/k/v projection qkv [L, (H + 2 KV) * D]:
  *   q_out [L, H, D]          <- RoPE(RMSNorm(q))

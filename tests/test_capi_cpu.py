@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 16, syms
+    assert len(syms) == 18, syms
 
 
 def test_library_exports_every_header_symbol(lib):
@@ -138,6 +138,47 @@ def test_producer_and_attention_validation_without_gpu(lib):
     # empty problems succeed
     assert lib.cider_rmsnorm_quantize(n, n, n, n, 1e-6, p, n, n, 0, 16, n) == _lib.CIDER_OK
     assert lib.cider_qk_norm_rope(*(args[:12] + [0] + args[13:])) == _lib.CIDER_OK
+
+
+
+def test_producer_mv_validation_without_gpu(lib):
+    """cider_rmsnorm_mv / cider_swiglu_mv reject bad shapes, pointers and
+    overlaps before any launch (no GPU needed)."""
+    from cider_amd import _lib
+    E, U = _lib.CIDER_E_INVALID, _lib.CIDER_E_UNSUPPORTED
+    n = None
+    x, a, sm, nw, w, sw, y = (ctypes.c_void_p(v) for v in
+                              (0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000, 0x70000))
+    K, N = 4096, 6144
+    # K % 256 != 0 or K > 16384 or misaligned x / w: unsupported (use the two calls)
+    assert lib.cider_rmsnorm_mv(x, n, n, nw, 1e-6, w, sw, n, y, N, 4000, n) == U
+    assert lib.cider_rmsnorm_mv(x, n, n, nw, 1e-6, w, sw, n, y, N, 16640, n) == U
+    assert lib.cider_rmsnorm_mv(ctypes.c_void_p(0x10008), n, n, nw, 1e-6, w, sw, n, y, N, K,
+                                n) == U
+    assert "256" in _err(lib)
+    # add without sum, sum without add
+    assert lib.cider_rmsnorm_mv(x, a, n, nw, 1e-6, w, sw, n, y, N, K, n) == E
+    assert lib.cider_rmsnorm_mv(x, n, sm, nw, 1e-6, w, sw, n, y, N, K, n) == E
+    assert "together" in _err(lib)
+    # sum overlapping x (another workgroup still reads x), y overlapping inputs
+    assert lib.cider_rmsnorm_mv(x, a, ctypes.c_void_p(0x10000 + 4096), nw, 1e-6, w, sw, n, y,
+                                N, K, n) == E
+    assert "sum must not overlap" in _err(lib)
+    assert lib.cider_rmsnorm_mv(x, a, sm, nw, 1e-6, w, sw, n, ctypes.c_void_p(0x30000 + 64),
+                                N, K, n) == E
+    assert "y must not overlap" in _err(lib)
+    # NULLs, eps, sizes
+    assert lib.cider_rmsnorm_mv(x, n, n, n, 1e-6, w, sw, n, y, N, K, n) == E
+    assert "norm_w is NULL" in _err(lib)
+    assert lib.cider_rmsnorm_mv(x, n, n, nw, -1.0, w, sw, n, y, N, K, n) == E
+    assert lib.cider_rmsnorm_mv(x, n, n, nw, 1e-6, w, n, n, y, N, K, n) == E
+    assert lib.cider_rmsnorm_mv(x, n, n, nw, 1e-6, w, sw, n, y, 0, K, n) == E
+    # SwiGLU: gate_up is [2K]; y must not overlap it
+    assert lib.cider_swiglu_mv(x, w, sw, n, y, N, 12290, n) == U
+    assert lib.cider_swiglu_mv(x, w, sw, n, ctypes.c_void_p(0x10000 + 2 * 4096 + 2), N, K,
+                               n) == E
+    assert "overlap" in _err(lib)
+    assert lib.cider_swiglu_mv(x, n, sw, n, y, N, K, n) == E
 
 
 def test_check_maps_codes_to_exceptions(lib):

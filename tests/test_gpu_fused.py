@@ -270,3 +270,51 @@ def test_attn_decode_graph_replays_follow_device_length():
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"n={n}"
+
+
+# Decode producers run inside the consuming M == 1 linear: bit-identical to
+# the producer launch followed by the linear on its fp16 output.
+def _pc_linear(N, K, seed):
+    from cider_amd import nn as cnn
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randint(-127, 128, (N, K), dtype=torch.int8, device="cuda", generator=g)
+    sw = torch.rand(N, device="cuda", generator=g) * 9e-3 + 1e-3
+    b = (torch.randn(N, device="cuda", generator=g) * 0.1).half()
+    return cnn.CiderLinear(w, sw, 0, K, N, b)
+
+
+@pytest.mark.parametrize("N,K,with_add", [(6144, 4096, True), (24576, 4096, True),
+                                          (4096, 2048, False), (33, 16384, True),
+                                          (40, 256, False), (3000, 2560, True)])
+def test_rmsnorm_mv_equals_two_launches(N, K, with_add):
+    g = torch.Generator(device="cuda").manual_seed(N + K)
+    x = (torch.randn(1, K, device="cuda", generator=g) * 3).half()
+    add = torch.randn(1, K, device="cuda", generator=g).half() if with_add else None
+    w = (torch.rand(K, device="cuda", generator=g) * 2).half()
+    lin = _pc_linear(N, K, N * 3 + K)
+    h, y = F.rmsnorm_mv(x, w, 1e-6, lin, add=add)
+    r = F.rmsnorm_quantize(x, w, 1e-6, add=add, want_q=False)
+    y2 = lin(r.y)
+    torch.cuda.synchronize()
+    assert torch.equal(h.view(-1), r.h.view(-1)), "residual sum differs"
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), f"rmsnorm_mv {N}x{K}"
+
+
+@pytest.mark.parametrize("N,I", [(4096, 12288), (2048, 6144), (33, 512), (4096, 16384)])
+def test_swiglu_mv_equals_two_launches(N, I):
+    g = torch.Generator(device="cuda").manual_seed(N + I)
+    gu = (torch.randn(1, 2 * I, device="cuda", generator=g) * 3).half()
+    lin = _pc_linear(N, I, N * 5 + I)
+    y = F.swiglu_mv(gu, lin)
+    hs, _, _ = F.silu_mul_quantize(gu, want_y=True, want_q=False)
+    y2 = lin(hs)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), f"swiglu_mv {N}x{I}"
+
+
+def test_producer_mv_rejects_unsupported_shapes():
+    lin = _pc_linear(16, 264, 1)
+    x = torch.randn(1, 264, device="cuda").half()
+    w = torch.ones(264, device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="256"):
+        F.rmsnorm_mv(x, w, 1e-6, lin)

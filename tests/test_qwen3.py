@@ -190,3 +190,24 @@ def test_tiny_generate_graph_equals_eager():
     ta = a.generate(ids, 16, graph=True)
     tb = b.generate(ids, 16, graph=False)
     assert torch.equal(ta, tb)
+
+
+@pytest.mark.gpu
+def test_tiny_decode_fused_mv_equals_unfused():
+    """Decode with RMSNorm (+ residual) and SwiGLU run inside the consuming MV
+    (cider_rmsnorm_mv / cider_swiglu_mv) equals decode with the separate
+    launches bit for bit: same logits, same caches, step after step."""
+    ids = torch.randint(0, TINY.vocab_size, (30,), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(12))
+    a = Q.Qwen3(TINY, max_len=64, seed=11)
+    b = Q.Qwen3(TINY, max_len=64, seed=11)
+    for layer in b.layers:
+        layer.fuse_mv = False
+    assert torch.equal(a.prefill(ids), b.prefill(ids))
+    tok = ids[-1:].clone()
+    for t in range(6):
+        pos = torch.tensor([30 + t], device="cuda")
+        la, lb = a.decode_step(tok, pos), b.decode_step(tok, pos)
+        assert torch.equal(la, lb), f"step {t}"
+        tok = torch.argmax(la[0].float()).reshape(1)
+    assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.v_cache, b.v_cache)
