@@ -217,9 +217,12 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   // (PS per wave inside one sub-step) outrun what the CU's vector-memory path
   // accepts (one 1 KB load per ~23 cycles) and stall the issuing waves.  Every
   // part is out before the next barrier, so the counts waited for are as if
-  // the stage were issued at once.  Exception, measured: int4 weights at
-  // 256 x 256 (three slots) ran 25-40% slower split than whole.
-  constexpr int DS = (NS >= 3 && !(W4 && BM == 256)) ? SUBS : 1;
+  // the stage were issued at once.  With two slots (int8 256 x 256) the parts
+  // issued in stage kt+1 have only the sub-steps before its barrier to land:
+  // two parts measured 4-11% faster than one, four parts no faster than one.
+  // Exception, measured: int4 weights at 256 x 256 (three slots) ran 25-40%
+  // slower split than whole.
+  constexpr int DS = (W4 && BM == 256) ? 1 : NS >= 3 ? SUBS : 2;
 
   // One k sub-step in a fixed instruction order (sched_barrier): the TN*TM
   // MFMAs on fragments (wc, xc); between them the operands of the next
