@@ -46,8 +46,10 @@
 //     instead of one: the CU's vector-memory path accepts one 1 KB load per
 //     ~23 cycles, and a whole stage's loads inside one sub-step stalled the
 //     issuing waves for ~440 of its 512 MFMA cycles (measured at 256 x 256).
-//     Two slots (int8 256 x 256) leave the loads no later sub-step to go to;
-//     int4 weights at 256 x 256 (three slots) measured slower split.
+//     Two slots (int8 256 x 256) split a stage in two parts only: the second
+//     part, issued in the first sub-step of stage kt+1, must land by that
+//     stage's barrier.  int4 weights at 256 x 256 (three slots) measured
+//     slower split.
 //   * The one barrier per stage sits before its last sub-step: it publishes
 //     stage kt + 1 and frees the slot of stage kt, which then receives stage
 //     kt + NS.
@@ -57,8 +59,9 @@
 //     bank groups.  The DMA destination is contiguous, so each lane picks the
 //     global chunk of the slot it writes.
 //   * Epilogue (per-channel): the tile's sw, sa and bias are requested at the
-//     start of the last stage and staged in LDS; each wave dequantizes its
-//     accumulators to fp16 into a BM x BN LDS tile (rows padded by 16 bytes),
+//     start of the last stage and staged in LDS; each wave reads the column
+//     scales it needs into registers, then dequantizes its accumulators to
+//     fp16 into a BM x BN LDS tile (rows padded by 16 bytes),
 //     then the workgroup stores whole 2*BN-byte rows with 16-byte lanes, so
 //     HBM sees full 128-byte lines instead of 32-byte row fragments.
 //   * int4 weights: a k-stage of a weight row is 64 bytes of nibbles (the ring
@@ -393,17 +396,33 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     for (int b = 0; b < TM; ++b) sam[b] = ssa[wm * WM + b * 32 + frow];
     // the bias test is uniform: taken once, outside the conversion loops (a
     // per-element select would cost two VALU ops per accumulator)
+    // Every column scale this lane needs is read before the conversion, so no
+    // LDS wait (which would also wait for the tile stores already issued)
+    // sits inside it.
+    f32x4 swv[TN][4];
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        swv[a][g] = *reinterpret_cast<const f32x4*>(ssw + wn * WN + a * 32 + 8 * g + 4 * h);
     auto convert = [&](auto biasc) {
       constexpr bool BIAS = decltype(biasc)::value != 0;
+      i32x2 bbv[TN][4];
+      if constexpr (BIAS) {
+#pragma unroll
+        for (int a = 0; a < TN; ++a)
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+            bbv[a][g] = *reinterpret_cast<const i32x2*>(sbias + wn * WN + a * 32 + 8 * g + 4 * h);
+      }
 #pragma unroll
       for (int a = 0; a < TN; ++a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int nl = wn * WN + a * 32 + 8 * g + 4 * h;  // column in tile
-          const f32x4 swv = *reinterpret_cast<const f32x4*>(ssw + nl);
           float bv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
           if constexpr (BIAS) {
-            const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+            const i32x2 bb = bbv[a][g];
             bv[0] = h2f((uint16_t)((uint32_t)bb[0] & 0xffffu));
             bv[1] = h2f((uint16_t)((uint32_t)bb[0] >> 16));
             bv[2] = h2f((uint16_t)((uint32_t)bb[1] & 0xffffu));
@@ -415,8 +434,14 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
             float o[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              float v = (float)acc[a][b][4 * g + r] * sam[b];
-              v = v * swv[r];
+              // The volatile asm keeps each path's int -> float conversions
+              // inside that path: hoisted above the bias test, the converted
+              // accumulators were parked back in AGPRs and the 256 x 256 tile
+              // spilled.
+              int iv = acc[a][b][4 * g + r];
+              asm volatile("" : "+v"(iv));
+              float v = (float)iv * sam[b];
+              v = v * swv[a][g][r];
               if constexpr (BIAS) v = v + bv[r];
               o[r] = v;
             }
