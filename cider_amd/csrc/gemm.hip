@@ -381,10 +381,16 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // touch 16 rows x 32-64 B, once they fill half the CUs or past M = 48
     // (N=12288 K=4096 M=16: 12.9 vs 18.7 us; N=4096 K=12288 M=16, 64 tiles:
     // 24.1 vs 17.1 us).
-    // Per-group stays on the skinny kernel: at 64-row tiles the exact group
-    // flush outweighs the tile's MFMAs (M=16 N=12288 K=4096 int4: 22.1 vs
-    // 19.9 us).
+    // Per-group: the 128-row per-group DMA tiles (N / 64 of them at any M)
+    // win once they fill half the CUs and M > 32, where the skinny kernel
+    // moves to 4 row blocks per wave and 4 waves per workgroup (N=12288
+    // K=4096 M=48, int8 gs 64: 45.1 vs 30.7 us; int4 gs 128: 36.2 vs 25.8 us),
+    // and for int8 weights at gs 128 from the smallest M (N=10240 K=2560 M=8:
+    // 16.8 vs 14.2 us).  Below that the skinny kernel keeps int4 and gs 64
+    // (N=12288 K=4096 M=16, int4 gs 128: 16.2 vs 25.7 us).
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
+    if (dma_pg && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
+      return launch_gemm_dma_pg(a, gs, sw_half, wf, s);
     return launch_skinny(a, wf, epi, sw_half, gs, s);
   }
   if (dma) return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)

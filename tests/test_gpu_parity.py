@@ -428,9 +428,12 @@ def test_skinny_wave_splits_exact(M, N, K):
 # 5 <= M <= 64 with at least 128 column tiles of 64 (or M > 48) runs the
 # LDS-DMA kernel's 64 x 64 tiles (per-channel, int32, int4 weights) instead of
 # the skinny kernel: rows past M are loaded from the last valid row and never
-# stored.  Per-group stays on the skinny kernel at these shapes, checked too.
+# stored.  Per-group at >= 128 column tiles runs the 128-row per-group DMA
+# tiles for M > 32, and for int8 weights at gs 128 at every M: (16, 10240,
+# 2560) and (5, 12288, 512) int8 gs 128; (33, 8192, 1024) and (64, 8192, 512)
+# every per-group variant; the others stay on the skinny kernel.
 @pytest.mark.parametrize("M,N,K", [(16, 10240, 2560), (5, 12288, 512), (33, 8192, 1024),
-                                   (64, 512, 4096), (49, 96, 256)])
+                                   (64, 8192, 512), (64, 512, 4096), (49, 96, 256)])
 def test_small_m_dma_tiles(M, N, K):
     x, w, sw, b = synth_pc(M, N, K, 98 + M)
     y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
@@ -442,7 +445,7 @@ def test_small_m_dma_tiles(M, N, K):
     packed, sw4 = O.pack_weight_int4(wf)
     y4 = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
     assert_bits_equal(y4, O.w4a8_linear(x, packed, sw4), f"small-M dma w4 {M}x{N}x{K}")
-    # per-group at the same shapes (skinny kernel, sequential group chain)
+    # per-group at the same shapes (skinny or per-group DMA kernel, sequential group chain)
     for gs in (64, 128):
         if K % gs:
             continue
