@@ -375,17 +375,17 @@ hipError_t run_skinny_pg_kw(const GemmArgs& a, bool vec, size_t lds, hipStream_t
 // Waves per workgroup: 4, raised to 8 or 16 while the grid has fewer than 16
 // waves per CU and every wave keeps at least 4 k-steps of its own (per-group:
 // two rounds of groups).  The LDS slices (KW x TM x 1 KB per buffer) cap KW at
-// 16 for TM = 1 and 8 for TM = 2 and 4.  Per-group at TM = 4 holds ~200 VGPRs
-// per lane, so an 8-wave workgroup fills a CU: 8 waves only while the grid is
-// one round of workgroups (N=4096 K=12288 M=33, int8 gs 64: 60.0 vs 39.4 us;
-// at N=6144, 384 workgroups, 4 waves stay faster: 19.0 vs 23.6 us).  The
-// per-channel kernel keeps 4 waves at TM = 4.
+// 16 for TM = 1 and 8 for TM = 2 and 4.  At TM = 4 a lane holds ~200 VGPRs,
+// so an 8-wave workgroup fills a CU: 8 waves only while the grid is one round
+// of workgroups (N=4096 K=12288 M=33, per-group int8 gs 64: 60.0 vs 39.4 us,
+// per-channel int4: 23.7 vs 21.8 us; at N=6144, 384 workgroups, 4 waves stay
+// faster: 19.0 vs 23.6 us per-group, 15.6 vs 17.5 us per-channel).
 template <int TM, int WF, int EPI, bool SWH, int GS>
 hipError_t run_skinny(const GemmArgs& a, bool vec, hipStream_t s) {
   // per-group: the workgroup's 16 columns of every group's scales in LDS
   const size_t lds = (EPI == EPI_PG) ? (size_t)(a.K / GS) * 16 * sizeof(float) : 0;
   if (lds > 64 * 1024) return hipErrorInvalidValue;
-  constexpr int kMaxKW = TM == 1 ? 16 : (TM == 2 || EPI == EPI_PG ? 8 : 4);
+  constexpr int kMaxKW = TM == 1 ? 16 : 8;
   const int64_t blocks = (a.N + 15) / 16;
   const int nkb = (a.K + 63) / 64;
   int kw = 4;
@@ -400,6 +400,7 @@ hipError_t run_skinny(const GemmArgs& a, bool vec, hipStream_t s) {
     return run_skinny_pg_kw<TM, WF, SWH, GS, 4>(a, vec, lds, s);
   } else {
     while (kw < kMaxKW && blocks * kw < 16 * 256 && nkb >= 2 * kw * 4) kw *= 2;
+    if (TM == 4 && kw == 8 && blocks > 256) kw = 4;
     if constexpr (kMaxKW >= 16)
       if (kw == 16) return run_skinny_kw<TM, WF, EPI, SWH, GS, 16>(a, vec, lds, s);
     if constexpr (kMaxKW >= 8)
