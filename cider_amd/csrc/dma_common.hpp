@@ -34,6 +34,19 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
       : "memory", "m0");
 }
 
+// As dma16, from `base` + off: base is wave-uniform and held in scalar
+// registers (the instruction's saddr form), off a per-lane 32-bit byte offset.
+// A k-stage then advances the scalar base only, with no per-lane 64-bit
+// address arithmetic in the k-loop.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(off), "s"(base), "s"(lds_base)
+      : "memory", "m0");
+}
+
 // Waits until at most N vector-memory loads of this wave are outstanding
 // (they complete in order).
 template <int N>

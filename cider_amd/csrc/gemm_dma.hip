@@ -149,23 +149,23 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   // DMA: instruction i of this wave fills tile rows R0 = (wave*WI + i)*RPIW ..
   // + RPIW (X: RPI); lane l writes row R0 + l / CHW, slot l % CHW, which holds
   // global chunk slot ^ swz(row).
-  const int8_t* wsrc[WI];
-  const int8_t* xsrc[XI];
-  {
-    const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
-    const int64_t ldw = W4 ? (K >> 1) : K;
+  // Sources: the tile's first W (X) row as a wave-uniform base, and per
+  // lane and instruction a 32-bit byte offset from it (< 256 rows x K).
+  const int64_t ldw = W4 ? (K >> 1) : K;
+  const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * ldw;
+  const int8_t* const xbase = p.x + (int64_t)m0 * K;
+  uint32_t woff[WI], xoff[XI];
 #pragma unroll
-    for (int i = 0; i < WI; ++i) {
-      const int row = (wave * WI + i) * RPIW + lane / CHW;
-      const int n = min(n0 + row, N - 1);
-      wsrc[i] = W + (int64_t)n * ldw + ((lane % CHW) ^ swz<WB>(row)) * 16;
-    }
+  for (int i = 0; i < WI; ++i) {
+    const int row = (wave * WI + i) * RPIW + lane / CHW;
+    const int n = min(n0 + row, N - 1);
+    woff[i] = (uint32_t)((int64_t)(n - n0) * ldw + ((lane % CHW) ^ swz<WB>(row)) * 16);
+  }
 #pragma unroll
-    for (int i = 0; i < XI; ++i) {
-      const int row = (wave * XI + i) * RPI + lane / CH;
-      const int m = min(m0 + row, M - 1);
-      xsrc[i] = p.x + (int64_t)m * K + ((lane % CH) ^ swz<BK>(row)) * 16;
-    }
+  for (int i = 0; i < XI; ++i) {
+    const int row = (wave * XI + i) * RPI + lane / CH;
+    const int m = min(m0 + row, M - 1);
+    xoff[i] = (uint32_t)((int64_t)(m - m0) * K + ((lane % CH) ^ swz<BK>(row)) * 16);
   }
   const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem);
@@ -174,10 +174,10 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   auto dma_one = [&](int st, int slot, int d) {
     const uint32_t sb = lds0 + (uint32_t)(slot * STAGE);
     if (d < WI)
-      dma16(wsrc[d < WI ? d : 0] + st * WB, sb + (wave * WI + d) * 1024);
+      dma16s(wbase + (int64_t)st * WB, woff[d < WI ? d : 0], sb + (wave * WI + d) * 1024);
     else
-      dma16(xsrc[d >= WI ? d - WI : 0] + st * BK,
-            sb + W_BYTES + (wave * XI + d - WI) * 1024);
+      dma16s(xbase + (int64_t)st * BK, xoff[d >= WI ? d - WI : 0],
+             sb + W_BYTES + (wave * XI + d - WI) * 1024);
   };
 
   // k mapping of sub-step j for lane half h (the same for both operands):

@@ -131,21 +131,23 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
   int m0, n0;
   tile_coords<PG_BM, PG_BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
 
-  const int8_t* wsrc[PG_WI];
-  const int8_t* xsrc[PG_XI];
-  {
-    const int8_t* W = reinterpret_cast<const int8_t*>(p.w);
-    const int64_t ldw = W4 ? (K >> 1) : K;
+  // Sources: the tile's first W (X) row as a wave-uniform base, and per
+  // lane and instruction a 32-bit byte offset from it (< 128 rows x K).
+  const int64_t ldw = W4 ? (K >> 1) : K;
+  const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * ldw;
+  const int8_t* const xbase = p.x + (int64_t)m0 * K;
+  uint32_t woff[PG_WI], xoff[PG_XI];
 #pragma unroll
-    for (int i = 0; i < PG_WI; ++i) {
-      const int row = (wave * PG_WI + i) * RPIW + lane / CHW;
-      wsrc[i] = W + (int64_t)min(n0 + row, N - 1) * ldw + ((lane % CHW) ^ swz<WB>(row)) * 16;
-    }
+  for (int i = 0; i < PG_WI; ++i) {
+    const int row = (wave * PG_WI + i) * RPIW + lane / CHW;
+    woff[i] = (uint32_t)((int64_t)(min(n0 + row, N - 1) - n0) * ldw +
+                         ((lane % CHW) ^ swz<WB>(row)) * 16);
+  }
 #pragma unroll
-    for (int i = 0; i < PG_XI; ++i) {
-      const int row = (wave * PG_XI + i) * PG_RPI + lane / PG_CH;
-      xsrc[i] = p.x + (int64_t)min(m0 + row, M - 1) * K + ((lane % PG_CH) ^ swz<PG_BK>(row)) * 16;
-    }
+  for (int i = 0; i < PG_XI; ++i) {
+    const int row = (wave * PG_XI + i) * PG_RPI + lane / PG_CH;
+    xoff[i] = (uint32_t)((int64_t)(min(m0 + row, M - 1) - m0) * K +
+                         ((lane % PG_CH) ^ swz<PG_BK>(row)) * 16);
   }
   // scale DMA (wave 0): lane l moves chunk l % CPR of row l / CPR of a stage's
   // scale block; rows past the stage's groups (or past G) repeat a valid row
@@ -159,18 +161,19 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
   auto dma_stage = [&](int st, int slot) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
 #pragma unroll
-    for (int i = 0; i < PG_WI; ++i) dma16(wsrc[i] + st * WB, sb + (wave * PG_WI + i) * 1024);
+    for (int i = 0; i < PG_WI; ++i)
+      dma16s(wbase + (int64_t)st * WB, woff[i], sb + (wave * PG_WI + i) * 1024);
 #pragma unroll
     for (int i = 0; i < PG_XI; ++i)
-      dma16(xsrc[i] + st * PG_BK, sb + PG_W_BYTES + (wave * PG_XI + i) * 1024);
+      dma16s(xbase + (int64_t)st * PG_BK, xoff[i], sb + PG_W_BYTES + (wave * PG_XI + i) * 1024);
   };
   auto dma_one = [&](int st, int slot, int d) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + (uint32_t)(slot * PG_STAGE);
     if (d < PG_WI)
-      dma16(wsrc[d < PG_WI ? d : 0] + st * WB, sb + (wave * PG_WI + d) * 1024);
+      dma16s(wbase + (int64_t)st * WB, woff[d < PG_WI ? d : 0], sb + (wave * PG_WI + d) * 1024);
     else
-      dma16(xsrc[d >= PG_WI ? d - PG_WI : 0] + st * PG_BK,
-            sb + PG_W_BYTES + (wave * PG_XI + d - PG_WI) * 1024);
+      dma16s(xbase + (int64_t)st * PG_BK, xoff[d >= PG_WI ? d - PG_WI : 0],
+             sb + PG_W_BYTES + (wave * PG_XI + d - PG_WI) * 1024);
   };
   auto dma_scales = [&](int st) __attribute__((always_inline)) {
     const int g = min(st * GPS + srow, G - 1);
