@@ -393,6 +393,10 @@ hipError_t run_skinny(const GemmArgs& a, bool vec, hipStream_t s) {
     const int G = a.K / GS;
     while (kw < kMaxKW && blocks * kw < 16 * 256 && G >= 2 * 2 * kw) kw *= 2;
     if (TM == 4 && kw == 8 && blocks > 256) kw = 4;
+    // int8 weights, one row block, >= 512 column blocks: 4 waves per
+    // workgroup (measured: N=12288 K=4096 M=16 gs 64: 27.7 vs 20.3 us at 8;
+    // N=10240 K=2560 M=8: 19.3 vs 13.5 us).  int4 weights measured level.
+    if (WF == W_I8 && TM == 1 && blocks >= 512) kw = 4;
     if constexpr (kMaxKW >= 16)
       if (kw == 16) return run_skinny_pg_kw<TM, WF, SWH, GS, 16>(a, vec, lds, s);
     if constexpr (kMaxKW >= 8)
