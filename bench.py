@@ -583,7 +583,7 @@ def bench_qwen3vl(torch, args, dev):
 
 # (bm, bn, rate) for int8 weights, as pick_tile in cider_amd/csrc/gemm_dma.hip
 _TILES_I8 = [(256, 256, 1.0), (128, 256, 0.87), (128, 128, 0.75), (128, 64, 0.517),
-             (64, 128, 0.508), (64, 64, 0.40)]
+             (64, 128, 0.508), (64, 64, 0.40), (192, 256, 0.90)]
 
 
 def gemm_kernel_name(M, N, K, dev):

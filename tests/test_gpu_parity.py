@@ -100,11 +100,12 @@ def test_int8_matmul_reference_shapes(bitexact_shapes):
 # M > 64, K % 128 == 0, N % 8 == 0: the LDS-DMA kernel at each int32 tile the
 # dispatcher picks (64x64: 256x256 and 300x520; the mixed 256x256 + 128x256
 # grid: 2048x10240; 128x256: 2048x4096; 128x128: 1024x4096; 128x64: 128x10240;
-# 64x128: 192x10240; 256x256: 4096x8192).
+# 64x128: 192x10240; 256x256: 4096x8192; 192x256: 1100x10240).
 @pytest.mark.parametrize("M,N,K", [(65, 64, 64), (256, 256, 128), (300, 520, 384),
                                    (1000, 130, 1000), (2, 3, 1), (70, 90, 17),
                                    (2048, 10240, 128), (1024, 4096, 256), (128, 10240, 128),
-                                   (192, 10240, 128), (4096, 8192, 256), (2048, 4096, 256)])
+                                   (192, 10240, 128), (4096, 8192, 256), (2048, 4096, 256),
+                                   (1100, 10240, 128)])
 def test_int8_matmul_more_shapes(M, N, K):
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
@@ -130,14 +131,15 @@ def test_int8_matmul_extremes():
 # Shapes cover every GEMM variant: skinny (M <= 64), the register-staged tiled
 # kernel (K % 128 != 0 or N % 8 != 0) and the LDS-DMA kernel at each tile the
 # dispatcher picks: 128x64 (M=128, N=10240), 64x64 (M=300/257), 128x128
-# (M=2048, N=2048), 128x256 (M=600), 256x256 (M=1024, N=10240), and the mixed
-# 256x256 + 128x256 grid (M=2048, N=10240; M=1000, N=16640 with a partial last
-# tile row; the full-size tests below); 64x128 in the midpoint test below.
+# (M=2048, N=2048), 128x256 (M=600), 192x256 (M=1024, N=10240), 256x256
+# (M=4096, N=8192), and the mixed 256x256 + 128x256 grid (M=2048, N=10240;
+# M=1000, N=16640 with a partial last tile row; the full-size tests below);
+# 64x128 in the midpoint test below.
 @pytest.mark.parametrize("M,N,K", [(2, 16, 64), (7, 33, 130), (16, 1000, 2560), (33, 257, 513),
                                    (64, 128, 256), (65, 200, 320), (128, 10240, 2560),
                                    (300, 1000, 1024), (257, 512, 4096), (100, 70, 100),
                                    (1024, 10240, 2560), (2048, 2048, 1024), (600, 8192, 768),
-                                   (2048, 10240, 256), (1000, 16640, 128)])
+                                   (2048, 10240, 256), (1000, 16640, 128), (4096, 8192, 128)])
 def test_perchannel_linear_bitexact(M, N, K):
     for bias in (True, False):
         x, w, sw, b = synth_pc(M, N, K, 1000 + M + N + K, bias)
@@ -160,11 +162,12 @@ def test_perchannel_gemm_matches_linear():
 # where the binary32 product lands exactly on an fp16 midpoint.  Random int8
 # operands with random binary32 scales put a few hundred such elements in each
 # case (the test asserts that they are there); the shapes select, in order,
-# the 128 x 64, 64 x 64 (twice) and 64 x 128 LDS-DMA tiles, the mixed grid,
-# the register-staged kernel (K % 128 != 0), the skinny kernel and the GEMV.
+# the 128 x 64, 64 x 64 (twice), 64 x 128 and 192 x 256 LDS-DMA tiles, the
+# mixed grid, the register-staged kernel (K % 128 != 0), the skinny kernel and
+# the GEMV.
 @pytest.mark.parametrize("M,N,K,rows", [
     (128, 10240, 2560, None), (128, 2560, 10240, None), (1000, 1000, 1024, None),
-    (192, 10240, 2560, None),
+    (192, 10240, 2560, None), (1100, 10240, 256, None),
     (4096, 10240, 2560, np.r_[0:64, 4032:4096]), (300, 1000, 1000, None),
     (48, 4096, 4096, None), (3, 10240, 2560, None)])
 def test_perchannel_gemm_double_rounding_midpoints(M, N, K, rows):
