@@ -49,8 +49,8 @@
 //     issuing waves for ~440 of its 512 MFMA cycles (measured at 256 x 256).
 //     Two slots (int8 256 x 256) split a stage in two parts only: the second
 //     part, issued in the first sub-step of stage kt+1, must land by that
-//     stage's barrier.  int4 weights at 256 x 256 (three slots) measured
-//     slower split.
+//     stage's barrier.  int4 weights at 256 x 256 (three slots) issue a
+//     stage whole: 4 parts measured 25-40 % slower, 2 parts level.
 //   * The one barrier per stage sits before its last sub-step: it publishes
 //     stage kt + 1 and frees the slot of stage kt, which then receives stage
 //     kt + NS.
@@ -226,7 +226,7 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
   // issued in stage kt+1 have only the sub-steps before its barrier to land:
   // two parts measured 4-11% faster than one, four parts no faster than one.
   // Exception, measured: int4 weights at 256 x 256 (three slots) ran 25-40%
-  // slower split than whole.
+  // slower in 4 parts than whole, and level in 2.
   constexpr int DS = (W4 && BM == 256) ? 1 : NS >= 3 ? SUBS : 2;
 
   // One k sub-step in a fixed instruction order (sched_barrier): the TN*TM
