@@ -10,8 +10,10 @@
 //   EPI_I32 cider/kernels/w8a8_matmul.metal:301-453
 //   EPI_PC  cider/kernels/w8a8_matmul.metal:63-81
 //   int4    cider/kernels/w4a8_matmul.metal:47-89,189-246 (no bias)
-// (Per-group stays on the register-staged kernel: its in-loop scale loads
-// would make the compiler wait for every LDS-DMA load in flight.)
+// (Per-group gs 64 / 128 runs gemm_dma_pg.hip, which brings the group scales
+// in by LDS-DMA too: a compiler-visible scale load in the k-loop would make
+// the compiler wait for every LDS-DMA load in flight.  gs 256 and shapes this
+// kernel does not take run the register-staged kernel of gemm.hip.)
 //
 // MI355X design
 //   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
