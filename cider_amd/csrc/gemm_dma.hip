@@ -17,8 +17,8 @@
 //
 // MI355X design
 //   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
-//     (n) from {256 x 256, 192 x 256 (int8), 128 x 256, 128 x 128, 128 x 64,
-//     64 x 128, 64 x 64},
+//     (n) from {256 x 256, 192 x 256, 128 x 256, 128 x 128, 128 x 64, 64 x 128,
+//     64 x 64},
 //     picked per shape by measured rate and the rounds the grid needs on the
 //     256 CUs.  At 256 x 256 (the large-M tile) each wave owns a 128 x 128
 //     sub-tile = 4 x 4 blocks of 32 x 32 (16 int32 accumulators per lane per
@@ -520,22 +520,22 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
   // launches, over M = 128 .. 8192 and (N, K) from (10240, 2560) to
   // (4096, 12288).  A last round only partly full runs with less contention:
   // it counts 0.6 + 0.4 x its occupancy.  Ties go to the earlier candidate.
-  // int8 weights also have 192 x 256 (waves of 96 x 128), for grids whose
-  // 256 x 256 tiles make one partial round (M=4096 N=2560 K=10240: 97.3 vs
-  // 105.8 us; M=1024 N=10240 K=2560: 33.5 vs 35.8 us).  The mixed grid below
-  // reads candidates 0 and 1.
+  // 192 x 256 (waves of 96 x 128) serves grids whose 256 x 256 tiles make one
+  // partial round (int8: M=4096 N=2560 K=10240: 97.3 vs 105.8 us; M=1024
+  // N=10240 K=2560: 33.5 vs 35.8 us; int4: M=1024 N=10240 K=2560: 38.6 vs
+  // 42.8 us).  The mixed grid below reads candidates 0 and 1.
   struct Cand { int bm, bn; double rate; };
   static const Cand c8[] = {{256, 256, 1.0},   {128, 256, 0.87}, {128, 128, 0.75},
                             {128, 64, 0.517},  {64, 128, 0.508}, {64, 64, 0.40},
                             {192, 256, 0.90}};
   static const Cand c4[] = {{256, 256, 1.0},   {128, 256, 0.77}, {128, 128, 0.60},
-                            {128, 64, 0.41},   {64, 128, 0.40},  {64, 64, 0.32}};
+                            {128, 64, 0.41},   {64, 128, 0.40},  {64, 64, 0.32},
+                            {192, 256, 0.92}};
   const Cand* cands = WF == W_I4 ? c4 : c8;
-  const int ncand = WF == W_I4 ? 6 : 7;
   const int cus = num_cus();
   int best = 0;
   double best_cost = 1e300;
-  for (int i = 0; i < ncand; ++i) {
+  for (int i = 0; i < 7; ++i) {
     const int64_t tiles =
         (int64_t)((a.M + cands[i].bm - 1) / cands[i].bm) * ((a.N + cands[i].bn - 1) / cands[i].bn);
     const int64_t full = tiles / cus, rest = tiles % cus;
@@ -568,8 +568,7 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
   }
   const int bm = cands[best].bm, bn = cands[best].bn;
   if (bm == 256) return run_dma<256, 256, 128, EPI, WF>(a, s);
-  if constexpr (WF == W_I8)
-    if (bm == 192) return run_dma<192, 256, 128, EPI, WF>(a, s);
+  if (bm == 192) return run_dma<192, 256, 128, EPI, WF>(a, s);
   if (bm == 128 && bn == 256) return run_dma<128, 256, 128, EPI, WF>(a, s);
   if (bm == 128 && bn == 128) return run_dma<128, 128, 128, EPI, WF>(a, s);
   if (bm == 128) return run_dma<128, 64, 128, EPI, WF>(a, s);

@@ -324,14 +324,15 @@ def test_w4_repack_matches_unpack():
 # M > 64, K % 128 == 0, N % 8 == 0 runs the LDS-DMA kernel with int4 weights
 # (512x640, 256x1024 and 300x136 -- an odd stage count -- on 64x64 tiles,
 # 192x6144 and 192x10240 on 64x128, 2048x2048 on 128x128, 2048x4096 on
-# 128x256, 2048x10240 on the mixed grid; 256x256 in the full-size test and
-# 128x64 in the midpoint test below); N % 8 != 0 the register-staged kernel;
-# M <= 64 the skinny kernel.
+# 128x256, 2048x10240 on the mixed grid, 1024x10240 on 192x256; 256x256 in the
+# full-size test and 128x64 in the midpoint test below); N % 8 != 0 the
+# register-staged kernel; M <= 64 the skinny kernel.
 @pytest.mark.parametrize("M,N,K", [(1, 32, 64), (9, 70, 160), (1, 12288, 4096),
                                    (16, 4096, 12288), (64, 300, 1024), (100, 300, 1024),
                                    (512, 640, 2048), (7, 33, 98), (256, 1024, 512),
                                    (300, 136, 384), (2048, 10240, 256), (192, 6144, 1024),
-                                   (192, 10240, 2560), (2048, 2048, 1024), (2048, 4096, 1024)])
+                                   (192, 10240, 2560), (2048, 2048, 1024), (2048, 4096, 1024),
+                                   (1024, 10240, 256)])
 def test_w4a8_linear_ref_layout(M, N, K):
     x = O.synth_activations(M, K, 60 + M)
     wf = np.random.default_rng(61 + N).standard_normal((K, N)).astype(np.float32)
