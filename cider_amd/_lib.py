@@ -33,6 +33,7 @@ CIDER_OP_PERCHANNEL = 1
 CIDER_OP_PERGROUP = 2
 CIDER_OP_W4A8 = 3
 CIDER_OP_W4A8_PERGROUP = 4
+CIDER_OP_W4A8_REF = 5
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -52,6 +53,7 @@ SIGNATURES = {
     "cider_pergroup_linear": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I, _P]),
     "cider_w4_repack_ref": (_I, [_P, _P, _I64, _I64, _P]),
     "cider_w4a8_linear": (_I, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _P]),
+    "cider_w4a8_linear_ref": (_I, [_P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _P]),
     "cider_w4a8_pergroup_linear": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I, _P]),
     "cider_rmsnorm_quantize": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _I64, _I64, _P]),
     "cider_silu_mul_quantize": (_I, [_P, _P, _P, _P, _I64, _I64, _P]),
@@ -85,7 +87,12 @@ def load():
         except OSError as e:  # pragma: no cover - depends on the machine
             raise RuntimeError(f"cider_amd HIP extension failed to load: {e}") from e
         for name, (res, args) in SIGNATURES.items():
-            fn = getattr(lib, name)
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as e:
+                raise RuntimeError(
+                    f"cider_amd HIP extension at {LIB_PATH} lacks {name}: it is older "
+                    "than its sources; rebuild it") from e
             fn.restype = res
             fn.argtypes = args
         _lib = lib

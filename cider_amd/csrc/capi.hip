@@ -131,6 +131,9 @@ size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K, int group_
     case CIDER_OP_W4A8:
     case CIDER_OP_W4A8_PERGROUP:
       return quant_ws_bytes(M, K);
+    case CIDER_OP_W4A8_REF:
+      if (N < 0) return 0;
+      return quant_ws_bytes(M, K) + align256((size_t)N * (size_t)(K / 2));
     default:
       return 0;
   }
@@ -279,6 +282,29 @@ int cider_w4a8_linear(const void* x_f16, const uint8_t* w4_nk, const float* sw, 
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
   cider::GemmArgs g{q, w4_nk, sa, sw, nullptr, y_f16, (int)M, (int)N, (int)K};
   return hip_status(cider::launch_gemm(g, cider::W_I4, cider::EPI_PC, false, 0, s), fn);
+}
+
+int cider_w4a8_linear_ref(const void* x_f16, const uint8_t* packed_kn, const float* sw,
+                          void* y_f16, void* ws, size_t ws_bytes, int64_t M, int64_t N,
+                          int64_t K, void* stream) {
+  static const char* fn = "cider_w4a8_linear_ref";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (K % 2 != 0)
+    return fail(CIDER_E_INVALID, "%s: K=%lld must be even", fn, (long long)K);
+  if (M == 0 || N == 0) return ok();
+  CIDER_TRY(need(fn, x_f16, "x", K > 0));
+  CIDER_TRY(need(fn, packed_kn, "packed_w", K > 0));
+  CIDER_TRY(need(fn, sw, "scale_w", true));
+  CIDER_TRY(need(fn, y_f16, "y", true));
+  const size_t qbytes = quant_ws_bytes(M, K);
+  CIDER_TRY(check_ws(fn, ws, ws_bytes, qbytes + align256((size_t)N * (size_t)(K / 2))));
+  const hipStream_t s = (hipStream_t)stream;
+  // The library-layout copy of the weights lives after the quantization
+  // scratch; the repack is enqueued ahead of the GEMM on the same stream.
+  uint8_t* w4_nk = reinterpret_cast<uint8_t*>(ws) + qbytes;
+  if (K > 0)
+    CIDER_TRY(hip_status(cider::launch_w4_repack_ref(packed_kn, w4_nk, (int)N, (int)K, s), fn));
+  return cider_w4a8_linear(x_f16, w4_nk, sw, y_f16, ws, qbytes, M, N, K, stream);
 }
 
 int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,

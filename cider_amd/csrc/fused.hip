@@ -313,7 +313,17 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     return;
   }
   const int64_t rr = rope_row[t];
-  if (rr < 0 || rr >= P) return;
+  if (rr < 0 || rr >= P) {
+    // No RoPE row: the k cache is left alone, and the q heads get a quiet
+    // NaN, so a caller that feeds them on sees the error instead of stale
+    // memory.
+    if (hh < H) {
+      uint16_t* dst = q_out + (t * H + hh) * D;
+      dst[lane] = 0x7E00;
+      dst[lane + 64] = 0x7E00;
+    }
+    return;
+  }
   const float a = h2f(x0), b = h2f(x1);
   float ss = a * a;
   ss = ss + b * b;

@@ -371,10 +371,14 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
                    (a.sw == nullptr || aligned16(a.sw));
+  // The LDS-DMA kernels address a tile's rows as a 64-bit base plus a 32-bit
+  // per-lane offset of up to 256 rows * K bytes; longer rows take the
+  // register-staged kernel, whose addresses are 64-bit throughout.
+  const bool off32 = (int64_t)a.K * 256 < ((int64_t)1 << 32);
   const bool dma = epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 &&
-                   a.N % 8 == 0;
+                   a.N % 8 == 0 && off32;
   const bool dma_pg = epi == EPI_PG && (gs == 64 || gs == 128) && vec && a.K % 128 == 0 &&
-                      a.N % 8 == 0;
+                      a.N % 8 == 0 && off32;
   if (a.M <= 64) {
     // The LDS-DMA kernel's 64 x 64 tiles load whole weight rows (one 16-byte
     // lane after another) and beat the skinny kernel, whose MFMA operand loads

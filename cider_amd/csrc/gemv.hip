@@ -9,7 +9,12 @@
 // lanes are summed by an xor butterfly (16, 8, 4, 2, 1), and
 //   per-channel: y = h(f32(sw[n] * R) + f32(bias[n]))
 //   per-group:   y = h(f32(R + f32(bias[n])))
-// This kernel reproduces exactly that order, for every shape.
+// This kernel reproduces exactly that order, for every shape.  It serves the
+// shapes outside the table of the streaming MV (mv_stream.hip, which sums in
+// its own order within the fp32 reassociation bound): K < 1024, K > 16384,
+// K % 256 != 0, or unaligned operands.  launch_mv and launch_mv_producer pick
+// between the two by the same rule, so a fused producer launch still equals
+// the producer launch followed by launch_mv bit for bit.
 //
 // MI355X design
 //   * 16 lanes per row, four rows per 64-lane wave.  Lane j carries the two
@@ -268,13 +273,6 @@ __device__ __forceinline__ float dot8f(uint32_t w0, uint32_t w1, const f32x4& xa
 // Thread t stages the 8-element chunks t, t + 256, ... as the producer
 // kernels do (the RMSNorm sum of squares in that order, then block_sum4), so
 // x' is bit-identical to what the producer kernel writes.
-struct MvProducer {
-  const uint16_t* add = nullptr;  // XM_ADDNORM
-  uint16_t* hsum = nullptr;       // XM_ADDNORM: h = x + add
-  const uint16_t* nw = nullptr;   // XM_NORM / XM_ADDNORM
-  float eps = 0.0f;
-};
-
 template <bool PG, int U, int XM = XM_PLAIN>
 __global__ __launch_bounds__(256) void mv_wide_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
@@ -515,6 +513,10 @@ hipError_t launch_mv_producer(int xm, const uint16_t* x, const uint16_t* add, ui
   pp.hsum = hsum;
   pp.nw = nw;
   pp.eps = eps;
+  // the same kernel choice as launch_mv, so a fused launch equals the
+  // producer launch followed by launch_mv bit for bit
+  if (mv_stream_supported(x, w, sw, K, 0))
+    return launch_mv_stream(xm, x, w, sw, bias, y, N, K, 0, pp, s);
   const size_t lds = (size_t)K * sizeof(float);
   switch (xm) {
     case XM_NORM: return pick_producer<XM_NORM>(x, w, sw, bias, y, N, K, lds, s, pp);
@@ -527,6 +529,14 @@ hipError_t launch_mv_producer(int xm, const uint16_t* x, const uint16_t* add, ui
 hipError_t launch_mv(const uint16_t* x, const int8_t* w, const float* sw,
                      const uint16_t* bias, uint16_t* y, int N, int K, int gs,
                      hipStream_t s) {
+  if (mv_stream_supported(x, w, sw, K, gs))
+    return launch_mv_stream(XM_PLAIN, x, w, sw, bias, y, N, K, gs, MvProducer{}, s);
+  return launch_mv_lanes(x, w, sw, bias, y, N, K, gs, s);
+}
+
+hipError_t launch_mv_lanes(const uint16_t* x, const int8_t* w, const float* sw,
+                           const uint16_t* bias, uint16_t* y, int N, int K, int gs,
+                           hipStream_t s) {
   if (K % 256 == 0 && K <= kMaxF32K && (((uintptr_t)w & 15) == 0) &&
       (((uintptr_t)x & 15) == 0)) {
     const int G = gs > 0 ? K / gs : 0;

@@ -43,6 +43,24 @@ hipError_t launch_gemv_qx(const uint16_t* x, const GemmArgs& a, int wf, int epi,
 // workgroup), x' = RMSNorm(h); XM_SWIGLU x = [gate | up] of 2K, x' = SwiGLU.
 // Requires mv_producer_supported (K % 256 == 0, K <= 16384, 16-byte aligned).
 enum { XM_PLAIN = 0, XM_NORM = 1, XM_ADDNORM = 2, XM_SWIGLU = 3 };
+struct MvProducer {
+  const uint16_t* add = nullptr;  // XM_ADDNORM
+  uint16_t* hsum = nullptr;       // XM_ADDNORM: h = x + add
+  const uint16_t* nw = nullptr;   // XM_NORM / XM_ADDNORM
+  float eps = 0.0f;
+};
+// Streaming MV (mv_stream.hip): K in its table (1024 <= K <= 16384,
+// K % 256 == 0), 16-byte aligned x and w, gs % 16 == 0.
+bool mv_stream_supported(const void* x, const void* w, const void* sw, int K, int gs);
+hipError_t launch_mv_stream(int xm, const uint16_t* x, const int8_t* w, const float* sw,
+                            const uint16_t* bias, uint16_t* y, int N, int K, int gs,
+                            const MvProducer& pp, hipStream_t s);
+// The lane-order MV of gemv.hip alone (reproduces the reference's 32-lane
+// order); launch_mv / launch_mv_producer use it where the streaming MV does
+// not apply.
+hipError_t launch_mv_lanes(const uint16_t* x, const int8_t* w, const float* sw,
+                           const uint16_t* bias, uint16_t* y, int N, int K, int gs,
+                           hipStream_t s);
 bool mv_producer_supported(const void* x, const void* w, int K);
 hipError_t launch_mv_producer(int xm, const uint16_t* x, const uint16_t* add, uint16_t* hsum,
                               const uint16_t* nw, float eps, const int8_t* w, const float* sw,

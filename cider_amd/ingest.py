@@ -128,6 +128,63 @@ class AffineQuantized:
         return int(np.asarray(self.scales).shape[1]) * self.group_size
 
 
+class QuantizedLinear(torch.nn.Module):
+    """An affine-quantized linear layer as MLX's ``nn.QuantizedLinear`` holds
+    it, on torch tensors: ``weight`` 32-bit words [N, K*bits/32] (int32
+    storage of the uint32 words), ``scales`` and ``biases`` [N, K/group_size],
+    ``group_size``, ``bits`` and an optional ``bias`` [N].
+
+    It is the source layer ``convert_model`` and ``CiderLinear.from_float``
+    convert, as the reference's converter does with ``nn.QuantizedLinear``
+    (``cider/convert.py:25``, ``cider/nn.py:127-171``).  Its own forward
+    dequantizes with torch ops (``w = q * scale + bias`` per group) and runs
+    a floating-point matmul; it is the unconverted model, not a path of this
+    library.
+    """
+
+    def __init__(self, weight, scales, biases, group_size: int, bits: int, bias=None):
+        super().__init__()
+        if bits not in (2, 4, 8):
+            raise ValueError(f"unsupported bit width {bits}")
+        w = torch.as_tensor(weight)
+        if w.dtype != torch.int32:
+            w = torch.from_numpy(np.ascontiguousarray(_np(w)).astype(np.uint32).view(np.int32))
+        self.register_buffer("weight", w.contiguous())
+        self.register_buffer("scales", torch.as_tensor(scales).contiguous())
+        self.register_buffer("biases", None if biases is None
+                             else torch.as_tensor(biases).contiguous())
+        self.register_buffer("bias", None if bias is None else torch.as_tensor(bias).contiguous())
+        self.group_size = int(group_size)
+        self.bits = int(bits)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        per = 32 // self.bits
+        words = self.weight.to(torch.int64) & 0xFFFFFFFF
+        shifts = torch.arange(per, device=words.device, dtype=torch.int64) * self.bits
+        q = ((words[..., None] >> shifts) & ((1 << self.bits) - 1)).reshape(words.shape[0], -1)
+        K = self.scales.shape[1] * self.group_size
+        s = self.scales.float().repeat_interleave(self.group_size, dim=1)
+        w = q[:, :K].float() * s
+        if self.biases is not None:
+            w = w + self.biases.float().repeat_interleave(self.group_size, dim=1)
+        b = None if self.bias is None else self.bias.to(x.dtype)
+        return torch.nn.functional.linear(x, w.to(x.dtype), b)
+
+    @property
+    def out_features(self) -> int:
+        return int(self.scales.shape[0])
+
+    @property
+    def in_features(self) -> int:
+        return int(self.scales.shape[1]) * self.group_size
+
+
+def is_affine_quantized(layer) -> bool:
+    """True for a layer holding affine-quantized weights (``QuantizedLinear``
+    or any object with ``weight``, ``scales``, ``group_size`` and ``bits``)."""
+    return all(hasattr(layer, a) for a in ("weight", "scales", "group_size", "bits"))
+
+
 def affine_dequantize(weight, scales, biases, group_size: int, bits: int) -> np.ndarray:
     """w = q * scale + bias per group (fp32; biases None -> 0)."""
     s = np.asarray(scales, dtype=np.float32)
@@ -163,7 +220,12 @@ def from_affine(layer, target_group_size: Optional[int] = None, device=None) -> 
     biases = getattr(layer, "biases", None)
     w = affine_dequantize(_np(layer.weight), scales, None if biases is None else _np(biases),
                           gs, bits)
-    dev = torch.device(device) if device is not None else torch.device("cpu")
+    if device is not None:
+        dev = torch.device(device)
+    elif isinstance(layer.weight, torch.Tensor):
+        dev = layer.weight.device
+    else:
+        dev = torch.device("cpu")
     lin_bias = getattr(layer, "bias", None)
     if lin_bias is not None:
         lin_bias = torch.as_tensor(_np(lin_bias)).to(device=dev, dtype=torch.float16)

@@ -199,13 +199,23 @@ class W4A8Linear(torch.nn.Module):
         self.register_buffer("scale", torch.as_tensor(scale, dtype=torch.float32, device=dev)
                              .contiguous())
         self._K = K
-        self._w4_nk = None  # library layout, made on first use on the GPU
+        # library layout, made on first use on the GPU; valid for the
+        # (version, address, shape, device) of packed_weight it was made from
+        self._w4_nk = None
+        self._w4_sig = None
 
     def _packed_nk(self) -> torch.Tensor:
         w = self.packed_weight
-        if self._w4_nk is None or self._w4_nk.device != w.device:
+        sig = (w._version, w.data_ptr(), tuple(w.shape), w.device)
+        if self._w4_nk is None or self._w4_sig != sig:
             self._w4_nk = ops.repack_w4_ref(w)
+            self._w4_sig = sig
         return self._w4_nk
+
+    def _load_from_state_dict(self, *args, **kwargs):
+        self._w4_nk = None
+        self._w4_sig = None
+        super()._load_from_state_dict(*args, **kwargs)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         orig_shape = x.shape

@@ -27,7 +27,9 @@ Extensions beyond the reference surface (same kernels): ``quantize_per_token``,
 
 from __future__ import annotations
 
+import collections
 import ctypes
+import threading
 import weakref
 from typing import Optional
 
@@ -370,24 +372,58 @@ def repack_w4_ref(packed_w: torch.Tensor, stream=None) -> torch.Tensor:
 
 
 class _RepackCache:
-    """Repacked copies of reference-layout W4 tensors, valid while the source
-    tensor is alive and unmodified (same object, same version counter)."""
+    """Repacked copies of reference-layout W4 tensors.
+
+    An entry is valid while its source tensor is alive and unmodified: same
+    object, version counter, storage address and shape.  The dict is guarded
+    by a lock (callers may run on several threads).  A repack runs on the
+    stream of the call that misses; an event recorded after it makes every
+    later caller's stream wait for it, and the copy is marked as used by that
+    stream so the caching allocator keeps its memory until the stream's work
+    is done, even if the entry is evicted meanwhile.  An entry leaves when its
+    source tensor is freed (``weakref.finalize``) or, least recently used
+    first, when the cache is full.
+    """
 
     def __init__(self, capacity: int = 16):
         self.capacity = capacity
-        self.entries = {}
+        self.entries = collections.OrderedDict()
+        self._lock = threading.Lock()
+
+    @staticmethod
+    def _sig(t: torch.Tensor):
+        return (t._version, t.data_ptr(), tuple(t.shape), t.device)
+
+    def _drop(self, key, ref):
+        with self._lock:
+            e = self.entries.get(key)
+            if e is not None and e[0] is ref:
+                del self.entries[key]
 
     def get(self, t: torch.Tensor, stream) -> torch.Tensor:
+        use = torch.cuda.current_stream(t.device) if stream is None else stream
         key = id(t)
-        e = self.entries.get(key)
-        if e is not None:
-            ref, version, shape, out = e
-            if ref() is t and version == t._version and shape == tuple(t.shape):
-                return out
+        with self._lock:
+            e = self.entries.get(key)
+            if e is not None and e[0]() is t and e[1] == self._sig(t):
+                self.entries.move_to_end(key)
+                out, done = e[2], e[3]
+            else:
+                out = None
+        if out is not None:
+            use.wait_event(done)
+            out.record_stream(use)
+            return out
         out = repack_w4_ref(t, stream)
-        if len(self.entries) >= self.capacity:
-            self.entries.pop(next(iter(self.entries)))
-        self.entries[key] = (weakref.ref(t), t._version, tuple(t.shape), out)
+        done = torch.cuda.Event()
+        done.record(use)
+        ref = weakref.ref(t)
+        with self._lock:
+            self.entries[key] = (ref, self._sig(t), out, done)
+            self.entries.move_to_end(key)
+            while len(self.entries) > self.capacity:
+                self.entries.popitem(last=False)
+        weakref.finalize(t, self._drop, key, ref)
         return out
 
 

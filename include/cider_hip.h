@@ -41,6 +41,7 @@ extern "C" {
 #define CIDER_OP_PERGROUP 2
 #define CIDER_OP_W4A8 3
 #define CIDER_OP_W4A8_PERGROUP 4
+#define CIDER_OP_W4A8_REF 5
 
 /* Library version (major*10000 + minor*100 + patch). */
 int cider_version(void);
@@ -121,6 +122,21 @@ int cider_w4a8_linear(const void* x_f16, const uint8_t* w4_nk, const float* sw,
                       void* y_f16, void* ws, size_t ws_bytes, int64_t M,
                       int64_t N, int64_t K, void* stream);
 
+/* W4A8 linear on weights in the reference W4 layout, one call:
+ * packed_kn uint8 [K/2, N] (high nibble = even k, value = nibble - 8,
+ * cider/ops.py:93-116), sw fp32 [N], no bias. The weights are repacked into
+ * the caller's workspace (cider_workspace_bytes(CIDER_OP_W4A8_REF, ...):
+ * the quantization scratch plus N*K/2 bytes), then the call proceeds as
+ * cider_w4a8_linear; results are identical to cider_w4_repack_ref followed
+ * by cider_w4a8_linear. A caller that reuses the weights saves the repack
+ * (N*K bytes of traffic per call) by holding the repacked copy itself.
+ * Replaces _cider_prim.w4a8_linear argument for argument
+ * (csrc/src/prim_bindings.cpp:23-25, csrc/src/w4a8_primitive.mm:266-283). */
+int cider_w4a8_linear_ref(const void* x_f16, const uint8_t* packed_kn,
+                          const float* sw, void* y_f16, void* ws,
+                          size_t ws_bytes, int64_t M, int64_t N, int64_t K,
+                          void* stream);
+
 /* W4A8 per-group linear (library W4 layout, fp16 scales [K/gs, N],
  * gs in {64,128}; bias fp16 [N] or NULL):
  *   acc = sum_g f32(f32(D_g) * f32(scale[g,n])); y = h(f32(acc*sa[m]) [+ bias])
@@ -190,7 +206,8 @@ int cider_swiglu_mv(const void* gate_up_f16, const int8_t* w, const float* scale
  * using rows rope_row[t] of the cos / sin tables [P, D] (fp16); RoPE is
  * out = h(h(x*cos) + h(rot(x)*sin)), rot(x) = [-x[D/2:], x[:D/2]].
  * rope_row and slot are int64 device arrays [L]; a token whose rope_row is
- * outside [0, P) is skipped, and a slot outside [0, T) writes nothing.
+ * outside [0, P) gets quiet-NaN q heads and no k-cache write, and a slot
+ * outside [0, T) writes nothing to the caches.
  * D must be 128. */
 int cider_qk_norm_rope(const void* qkv_f16, const void* q_norm_w_f16,
                        const void* k_norm_w_f16, float eps, const void* cos_f16,

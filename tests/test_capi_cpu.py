@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 18, syms
+    assert len(syms) == 19, syms
 
 
 def test_library_exports_every_header_symbol(lib):
@@ -53,6 +53,10 @@ def test_workspace_bytes(lib):
     assert ws(_lib.CIDER_OP_W4A8, 1, 64, 64) == 256 + 256
     assert ws(_lib.CIDER_OP_PERCHANNEL, 3, 8, 10) == 256 + 256
     assert ws(_lib.CIDER_OP_PERCHANNEL, 0, 8, 10) == 0
+    # the one-call reference-layout W4A8 adds room for the repacked weights
+    assert ws(_lib.CIDER_OP_W4A8_REF, 4096, 12288, 4096) == \
+        4096 * 4096 + 4096 * 4 + 12288 * 2048
+    assert ws(_lib.CIDER_OP_W4A8_REF, 1, 70, 64) == 256 + 256 + 2304
 
 
 def _err(lib):
@@ -88,6 +92,13 @@ def test_validation_errors_without_gpu(lib):
     assert rc == _lib.CIDER_E_INVALID and "even" in _err(lib)
     rc = lib.cider_w4_repack_ref(p, p, 8, 15, n)
     assert rc == _lib.CIDER_E_INVALID
+    # the one-call reference-layout W4A8: odd K, and a workspace without room
+    # for the repacked weights
+    rc = lib.cider_w4a8_linear_ref(p, p, p, p, p, 1 << 20, 4, 8, 15, n)
+    assert rc == _lib.CIDER_E_INVALID and "even" in _err(lib)
+    need = _lib.workspace_bytes(_lib.CIDER_OP_W4A8_REF, 4, 4096, 4096)
+    rc = lib.cider_w4a8_linear_ref(p, p, p, p, p, need - 1, 4, 4096, 4096, n)
+    assert rc == _lib.CIDER_E_INVALID and "workspace" in _err(lib)
     # empty problems are no-ops that succeed
     assert lib.cider_perchannel_linear(n, n, n, n, n, n, 0, 0, 8, 16, n) == _lib.CIDER_OK
     assert lib.cider_int8_matmul_int32(n, n, n, 5, 0, 16, n) == _lib.CIDER_OK
@@ -239,3 +250,26 @@ def test_cpu_tensors_rejected():
         assert C.is_available() is False
         with pytest.raises(RuntimeError):
             C.convert_model(torch.nn.Linear(4, 4), verbose=False)
+
+
+def test_reference_import_path():
+    """``import cider`` and its submodules resolve to this implementation
+    (the reference's surface, cider/__init__.py:18-57)."""
+    import cider
+    import cider.convert
+    import cider_amd
+    from cider.nn import CiderLinear, W4A8Linear, W8A8Linear
+    from cider.ops import (int8_matmul_int32, pack_weight_int4, perchannel_linear,
+                           pergroup_linear, quantize_weight_int8, w4a8_linear)
+    assert cider.ops is cider_amd.ops and cider.nn is cider_amd.nn
+    assert cider.convert is cider_amd.convert
+    assert CiderLinear is cider_amd.CiderLinear and W8A8Linear is CiderLinear
+    for name in ("convert_model", "set_mode", "get_mode", "CiderLinear", "W8A8Linear",
+                 "W4A8Linear", "perchannel_linear", "w4a8_linear", "pergroup_linear",
+                 "int8_matmul_int32", "quantize_weight_int8", "pack_weight_int4",
+                 "is_available", "kernel_dir"):
+        assert hasattr(cider, name), name
+    assert callable(perchannel_linear) and callable(pergroup_linear)
+    assert callable(int8_matmul_int32) and callable(w4a8_linear)
+    assert callable(pack_weight_int4) and callable(quantize_weight_int8)
+    assert W4A8Linear is cider_amd.W4A8Linear

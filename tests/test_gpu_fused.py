@@ -207,6 +207,15 @@ def test_qk_norm_rope_skips_out_of_range_slots():
     written = (kc != 0).any(dim=2).any(dim=0).cpu().numpy()
     assert written[3] and written.sum() == 1
     assert torch.equal(vc[:, 3], qkv[0].reshape(H + 2 * KV, D)[H + KV:])
+    # a token without a RoPE row: its q heads are NaN (not stale memory), and
+    # it writes no k row even where its slot is valid
+    kc.zero_()
+    q = F.qk_norm_rope(qkv, w, w, 1e-6, cos, sin, torch.tensor([1, 8], device="cuda"),
+                       torch.tensor([3, 5], device="cuda"), kc, vc, H, KV)
+    torch.cuda.synchronize()
+    assert torch.isfinite(q[0]).all() and torch.isnan(q[1]).all()
+    written = (kc != 0).any(dim=2).any(dim=0).cpu().numpy()
+    assert written[3] and written.sum() == 1
 
 
 def _attn_ref(q, kc, vc, n, scale):

@@ -87,6 +87,51 @@ def test_from_float_on_symmetric_8bit_affine_layer_keeps_the_values():
     assert np.array_equal(m4.w_int8.numpy(), q) and np.array_equal(m4.scale_w.numpy(), s)
 
 
+def test_quantized_linear_module_forward_and_conversion_walk():
+    """The torch QuantizedLinear holds MLX's affine tensors; its float forward
+    is the affine formula, and the conversion walk (cider/convert.py:28-47)
+    replaces it, an nn.Linear and a duck-typed affine module, keeping the
+    source's 8-bit group size as cider/nn.py:134-139 does."""
+    from cider_amd import convert as cconv
+    rng = np.random.default_rng(4)
+    N, K, gs = 16, 256, 64
+    codes = rng.integers(0, 256, (N, K))
+    scales = rng.uniform(1e-3, 1e-2, (N, K // gs)).astype(np.float32)
+    biases = (-128.0 * scales).astype(np.float32)
+    words = I.pack_words(codes, 8)
+    ql = I.QuantizedLinear(words, scales, biases, gs, 8)
+    assert ql.in_features == K and ql.out_features == N
+    assert ql.weight.dtype == torch.int32
+    x = torch.from_numpy(rng.standard_normal((3, K)).astype(np.float32))
+    w = I.affine_dequantize(words, scales, biases, gs, 8)
+    np.testing.assert_allclose(ql(x).numpy(), x.numpy() @ w.T, rtol=1e-5, atol=1e-5)
+
+    class Duck(torch.nn.Module):   # an affine layer of another class
+        def __init__(self):
+            super().__init__()
+            self.weight = I.pack_words(rng.integers(0, 16, (8, 128)), 4)
+            self.scales = np.full((8, 2), 0.01, np.float32)
+            self.biases = np.full((8, 2), -0.08, np.float32)
+            self.group_size, self.bits = 64, 4
+
+    model = torch.nn.Sequential(ql, torch.nn.ReLU(),
+                                torch.nn.Sequential(torch.nn.Linear(16, 128), Duck()))
+    counter = [0]
+    cconv._convert_children(model, counter, set(), None)
+    assert counter[0] == 3
+    assert isinstance(model[0], cnn.CiderLinear) and model[0].group_size == gs
+    qe, se = O.quantize_weight_pergroup(w, gs)
+    assert np.array_equal(model[0].w_int8.numpy(), qe)
+    assert np.array_equal(model[0].scale_w.numpy(), np.ascontiguousarray(se.T))
+    assert isinstance(model[2][0], cnn.CiderLinear) and model[2][0].group_size == 0
+    assert isinstance(model[2][1], cnn.CiderLinear) and model[2][1].group_size == 0
+    # group_size given: every layer per-group at that size
+    model2 = torch.nn.Sequential(I.QuantizedLinear(words, scales, biases, gs, 8),
+                                 torch.nn.Linear(128, 64))
+    cconv._convert_children(model2, [0], set(), 128)
+    assert model2[0].group_size == 128 and model2[1].group_size == 128
+
+
 # --------------------------------------------------------------------------
 # compressed-tensors
 # --------------------------------------------------------------------------

@@ -20,6 +20,7 @@ from oracle import cider_oracle as O
 from oracle import c_oracle as C
 from tests import exact_fp as X
 from tests.golden.make_golden import bitexact_inputs
+from tests.util import f16_ulp
 
 F32 = np.float32
 
@@ -338,6 +339,75 @@ def test_pergroup_mv_exact_model():
             assert Fraction(float(y[0, n])) == X.f16(X.f32(r[0] + Fraction(float(bias[n]))))
 
 
+def _pg_mv_closed_form(x, w, sw_gn, bias, gs):
+    """float64 value of sum_g sw[g,n] * sum_{k in g} w[n,k] x[k] + bias[n] and
+    sum of |terms|, straight from the definition (no lanes, no blocks)."""
+    K = w.shape[1]
+    G = K // gs
+    xv = x.reshape(-1).astype(np.float64)
+    prod = w.astype(np.float64) * xv[None, :]                          # [N, K]
+    dg = prod.reshape(w.shape[0], G, gs).sum(axis=2)                   # [N, G]
+    ag = np.abs(prod).reshape(w.shape[0], G, gs).sum(axis=2)
+    sw = sw_gn.astype(np.float64).T                                    # [N, G]
+    return (sw * dg).sum(axis=1) + bias.astype(np.float64), (np.abs(sw) * ag).sum(axis=1)
+
+
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_pergroup_mv_closed_form_and_layout_kats(gs):
+    """mv_pergroup against the float64 definition with a derived fp32 bound.
+
+    Every term w*x is exact in fp32 (8-bit by 11-bit significands); a term
+    then passes through at most 7 in-chunk adds, one scale multiply, nb block
+    adds, 5 butterfly adds and the bias add, so the fp32 result is within
+    gamma_(14+nb) * sum|sw*w*x| (+ u*|bias|) of the exact value (Higham,
+    Accuracy and Stability, 2nd ed., Lemma 3.1 and section 4.2), and the fp16
+    output within half an fp16 ulp of that.  The scales span 2^-16 .. 2^-3
+    across groups and columns, so reading them transposed ([N, G]) or with a
+    wrong group index (the block's group, or the lane's offset without the
+    block's) moves outputs by orders of magnitude more than the bound."""
+    rng = np.random.default_rng(gs)
+    N, K = 24, 1024
+    G = K // gs
+    x = rng.standard_normal((1, K)).astype(np.float16)
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = np.ldexp(1.0, rng.integers(-16, -3, (G, N))).astype(F32) * \
+        rng.uniform(1.0, 2.0, (G, N)).astype(F32)
+    bias = (rng.standard_normal(N) * 0.5).astype(np.float16)
+    y = O.mv_pergroup(x, w, sw, bias, gs)[0].astype(np.float64)
+    exact, mag = _pg_mv_closed_form(x, w, sw, bias, gs)
+    u = 2.0 ** -24
+    nb = K // 256
+    n = 14 + nb
+    bound = n * u / (1 - n * u) * mag + u * np.abs(bias.astype(np.float64))
+    half_ulp = 0.5 * f16_ulp(exact)
+    assert (np.abs(y - exact) <= bound + half_ulp * (1 + 1e-9)).all()
+    # the plausible mistakes fail the same check
+    mistakes = {
+        "transposed scale": np.ascontiguousarray(sw.T).reshape(G, N),
+        "groups in reverse": np.ascontiguousarray(sw[::-1]),
+    }
+    if gs < 256:
+        mistakes["group of the block"] = sw[np.arange(G) * gs // 256 * 256 // gs]
+    for name, swm in mistakes.items():
+        ym = O.mv_pergroup(x, w, swm, bias, gs)[0].astype(np.float64)
+        assert not (np.abs(ym - exact) <= bound + half_ulp).all(), name
+
+
+def test_pergroup_mv_group_index_kat():
+    """Hand-worked: K=512, gs=64, one nonzero product per group, scale of
+    group g = 2^g; the output is sum_g 2^g * (g+1) = 1793 exactly."""
+    gs, K = 64, 512
+    x = np.zeros((1, K), np.float16)
+    w = np.zeros((1, K), np.int8)
+    for g in range(K // gs):
+        k = g * gs + 37 % gs          # not the first element of its 8-lane chunk
+        x[0, k] = 1.0
+        w[0, k] = g + 1
+    sw = np.array([[2.0 ** g] for g in range(K // gs)], F32)
+    y = O.mv_pergroup(x, w, sw, np.zeros(1, np.float16), gs)
+    assert float(y[0, 0]) == sum(2.0 ** g * (g + 1) for g in range(K // gs)) == 1793.0
+
+
 def test_pergroup_validation():
     x = O.synth_activations(2, 192, 1)
     w = O.synth_weights_i8(4, 192, 2)
@@ -406,6 +476,46 @@ def test_weight_quantizer_half_even_and_zero_rows():
     assert q.tolist() == [[127, 2, 4, -2, -127], [0, 0, 0, 0, 0]]
     qg, sg = O.quantize_weight_pergroup(np.tile(w, (1, 2))[:, :8], 4)
     assert sg.shape == (2, 2)
+
+
+def test_weight_quantizer_pergroup_whole_row_equals_per_channel():
+    """gs = K is one group per row: bit for bit the per-channel quantizer."""
+    rng = np.random.default_rng(21)
+    for N, K in [(7, 64), (33, 256), (5, 1000)]:
+        w = (rng.standard_normal((N, K)) * rng.uniform(0.01, 10, (N, 1))).astype(F32)
+        w[1] = 0.0
+        qg, sg = O.quantize_weight_pergroup(w, K)
+        q, s = O.quantize_weight_int8(w)
+        assert sg.shape == (N, 1)
+        np.testing.assert_array_equal(qg, q)
+        np.testing.assert_array_equal(sg[:, 0].view(np.uint32), s.view(np.uint32))
+
+
+def test_weight_quantizer_pergroup_kat_and_exact_model():
+    """Hand-worked values: row 0 has groups of max 4 and 40, row 1 of 127
+    and 0; 2/(4/127) = 63.5 rounds half to even (64), and the all-zero
+    group gets scale 1.  Reshaping along the wrong axis (groups taken down
+    the columns) gives other scales."""
+    w = np.array([[1, 2, 3, 4, 10, 20, 30, 40],
+                  [127, -2.5, 3.5, 1, 0, 0, 0, 0]], F32)
+    q, s = O.quantize_weight_pergroup(w, 4)
+    np.testing.assert_array_equal(s, np.array([[4 / 127, 40 / 127], [1.0, 1.0]], F32))
+    assert q.tolist() == [[32, 64, 95, 127, 32, 64, 95, 127], [127, -2, 4, 1, 0, 0, 0, 0]]
+    wrong = np.abs(w.T.reshape(2, 4, 2)).max(axis=1) / F32(127.0)
+    assert not np.array_equal(wrong, s)
+    # exact-rational model, element by element
+    rng = np.random.default_rng(22)
+    w = (rng.standard_normal((3, 192)) * 3).astype(F32)
+    for gs in (64, 96):
+        q, s = O.quantize_weight_pergroup(w, gs)
+        for n in range(3):
+            for g in range(192 // gs):
+                seg = w[n, g * gs:(g + 1) * gs]
+                sc = X.f32(Fraction(float(np.max(np.abs(seg)))) / 127)
+                assert Fraction(float(s[n, g])) == sc
+                for j, v in enumerate(seg):
+                    e = max(-128, min(127, X.rne(X.f32(Fraction(float(v)) / sc))))
+                    assert int(q[n, g * gs + j]) == e
 
 
 # --------------------------------------------------------------------------
@@ -480,3 +590,31 @@ def test_golden_cases_reproduce(golden_cases):
             O.w4a8_pergroup_linear(g[f"w4g{i}_x"], g[f"w4g{i}_packed"], g[f"w4g{i}_scale"],
                                    int(g[f"w4g{i}_gs"])).view(np.uint16),
             g[f"w4g{i}_y"].view(np.uint16))
+
+
+@pytest.mark.parametrize("gs", [0, 64, 128])
+def test_mv_bar_accepts_the_oracle_and_rejects_planted_mistakes(gs):
+    """The MV parity bar (tests/util.py assert_mv_close) passes the oracle's
+    own output and fails outputs with one product dropped, one product
+    counted twice, or a scale off by 1 %."""
+    from tests.util import assert_mv_close
+    N, K = 64, 2560
+    x = O.synth_activations(1, K, 71)
+    w = O.synth_weights_i8(N, K, 72)
+    sw = O.synth_scales(N if gs == 0 else (K // gs, N), 73)
+    b = (np.random.default_rng(74).standard_normal(N) * 0.1).astype(np.float16)
+
+    def run(ww, ss):
+        return (O.mv_perchannel(x, ww, ss, b) if gs == 0 else O.mv_pergroup(x, ww, ss, b, gs))
+
+    assert_mv_close(run(w, sw), x, w, sw, b, gs, "oracle")
+    k = int(np.argmax(np.abs(x[0].astype(np.float32))))
+    dropped = w.copy()
+    dropped[:, k] = 0
+    doubled = w.astype(np.int16)
+    doubled[:, k] = np.clip(2 * doubled[:, k], -127, 127)
+    for name, bad in (("dropped product", run(dropped, sw)),
+                      ("doubled product", run(doubled.astype(np.int8), sw)),
+                      ("scale off by 1%", run(w, (sw * F32(1.01)).astype(F32)))):
+        with pytest.raises(AssertionError):
+            assert_mv_close(bad, x, w, sw, b, gs, name)

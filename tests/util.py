@@ -63,3 +63,61 @@ def assert_bits_equal(got, exp, what=""):
 
 
 gpu = pytest.mark.gpu
+
+
+def mv_exact(x, w, sw, bias, gs):
+    """float64 value and magnitude of the M == 1 MV, from its definition:
+    y[n] = sum_k s(n, k) w[n, k] x[k] + bias[n], s = sw[n] per channel
+    (gs 0) or sw[k // gs, n] per group; returns (exact [N], sum of |terms|
+    [N] including |bias|)."""
+    xv = np.asarray(x, np.float16).reshape(-1).astype(np.float64)
+    prod = np.asarray(w).astype(np.float64) * xv[None, :]
+    N, K = prod.shape
+    if gs == 0:
+        s = np.asarray(sw, np.float32).astype(np.float64).reshape(N, 1)
+        exact, mag = s[:, 0] * prod.sum(1), np.abs(s[:, 0]) * np.abs(prod).sum(1)
+    else:
+        G = K // gs
+        s = np.asarray(sw, np.float32).astype(np.float64).reshape(G, N).T      # [N, G]
+        exact = (s * prod.reshape(N, G, gs).sum(2)).sum(1)
+        mag = (np.abs(s) * np.abs(prod).reshape(N, G, gs).sum(2)).sum(1)
+    b = np.zeros(N) if bias is None else np.asarray(bias, np.float16).astype(np.float64)
+    return exact + b, mag + np.abs(b)
+
+
+def assert_mv_close(got, x, w, sw, bias, gs, what="", ref=None):
+    """Bar for the fp16-activation MV (M == 1), whose reduction order the
+    reference leaves to Metal's ``simd_sum`` (unspecified).  Every output must
+    be within the north-star bar of the oracle's order -- 1e-3 relative or
+    1 fp16 ulp -- or, where cancellation makes the sum small, within the
+    fp32 error bound of an evaluation of depth d of the exact value:
+    gamma_d * sum|terms| + 1 fp16 ulp, with d = 2 * ceil(K / 64) + 16, which
+    covers a 64-lane split of each row with paired products, the cross-lane
+    tree, the scale multiply and the bias add (and the oracle's 32-lane
+    order).  Dropping, duplicating or misplacing a single product, or a
+    wrong scale, fails both parts.  ``ref``: the oracle's output if already
+    at hand (e.g. a committed fixture)."""
+    from oracle import cider_oracle as O
+    got = np.asarray(got, np.float16).reshape(-1)
+    x = np.asarray(x, np.float16)
+    N, K = np.asarray(w).shape
+    if bias is None:
+        bias = np.zeros(N, np.float16)
+    if ref is None:
+        ref = (O.mv_perchannel(x, w, sw, bias) if gs == 0 else
+               O.mv_pergroup(x, w, sw, bias, gs))
+    ref = np.asarray(ref, np.float16).reshape(-1)
+    exact, mag = mv_exact(x, w, sw, bias, gs)
+    g, r = got.astype(np.float64), ref.astype(np.float64)
+    assert np.isfinite(g).all() == np.isfinite(r).all(), f"{what}: non-finite outputs differ"
+    d = 2 * (-(-K // 64)) + 16
+    u = 2.0 ** -24
+    bound = d * u / (1 - d * u) * mag + f16_ulp(exact)
+    near_ref = (np.abs(g - r) <= f16_ulp(r)) | (np.abs(g - r) <= 1e-3 * np.abs(r))
+    near_exact = np.abs(g - exact) <= bound
+    ok = near_ref | near_exact
+    if not ok.all():
+        idx = np.flatnonzero(~ok)[:5]
+        raise AssertionError(
+            f"{what}: {np.count_nonzero(~ok)} of {ok.size} outputs outside the MV bar; "
+            f"e.g. at {idx}: got {g[idx]} oracle {r[idx]} exact {exact[idx]} bound {bound[idx]}")
