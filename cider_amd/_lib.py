@@ -35,6 +35,8 @@ CIDER_OP_W4A8 = 3
 CIDER_OP_W4A8_PERGROUP = 4
 CIDER_OP_W4A8_REF = 5
 
+CIDER_NOALLOC_SCRATCH_BYTES = 32 << 20
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
@@ -49,6 +51,7 @@ SIGNATURES = {
     "cider_quantize_per_token": (_I, [_P, _P, _P, _I64, _I64, _P]),
     "cider_int8_matmul_int32": (_I, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "cider_perchannel_linear": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _P]),
+    "cider_perchannel_linear_noalloc": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cider_perchannel_gemm": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "cider_pergroup_linear": (_I, [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I, _P]),
     "cider_w4_repack_ref": (_I, [_P, _P, _I64, _I64, _P]),

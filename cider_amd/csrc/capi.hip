@@ -16,6 +16,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "cider_hip.h"
@@ -110,6 +111,38 @@ int quantize_into_ws(const char* fn, const void* x, void* ws, int64_t M, int64_t
   return hip_status(cider::launch_quantize(reinterpret_cast<const uint16_t*>(x), *q, *sa,
                                            (int)M, (int)K, s),
                     fn);
+}
+
+// ---- scratch of the entry points that allocate nothing --------------------
+//
+// One array per GPU, in the library's code object: it exists on every device
+// the library is loaded on, until the process ends.  Host code must not use
+// the name `scratch` as an address (it is a host-side stand-in); each
+// device's address is read once with hipGetSymbolAddress, with that device
+// current, and kept in scratch_dev[].
+static __device__ __attribute__((aligned(256))) int8_t scratch[CIDER_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kMaxDevices] = {};
+
+// The current device's address of `scratch`.
+int scratch_ptr(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, fn);
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(CIDER_E_UNSUPPORTED, "%s: device %d beyond the %d the library tracks", fn, dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, fn);
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return CIDER_OK;
 }
 
 }  // namespace
@@ -210,6 +243,24 @@ int cider_perchannel_linear(const void* x_f16, const int8_t* w_nk, const float* 
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
   cider::GemmArgs g{q, w_nk, sa, sw, bias, y_f16, (int)M, (int)N, (int)K};
   return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PC, false, 0, s), fn);
+}
+
+int cider_perchannel_linear_noalloc(const void* x_f16, const int8_t* w_nk, const float* sw,
+                                    const void* bias_f16, void* y_f16, int64_t M, int64_t N,
+                                    int64_t K, void* stream) {
+  static const char* fn = "cider_perchannel_linear_noalloc";
+  CIDER_TRY(check_dims(fn, M, N, K));
+  if (M == 0 || N == 0) return ok();
+  const size_t need = cider_workspace_bytes(CIDER_OP_PERCHANNEL, M, N, K, 0);
+  if (need > (size_t)CIDER_NOALLOC_SCRATCH_BYTES)
+    return fail(CIDER_E_INVALID,
+                "%s: M=%lld K=%lld needs %zu bytes of scratch, above the library's %zu "
+                "(M*K + 4*M, each 256-byte aligned); use cider_perchannel_linear with a "
+                "workspace",
+                fn, (long long)M, (long long)K, need, (size_t)CIDER_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) CIDER_TRY(scratch_ptr(fn, &ws));
+  return cider_perchannel_linear(x_f16, w_nk, sw, bias_f16, y_f16, ws, need, M, N, K, stream);
 }
 
 int cider_pergroup_linear(const void* x_f16, const int8_t* w_nk, const float* sw_gn,

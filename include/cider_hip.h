@@ -82,6 +82,26 @@ int cider_perchannel_linear(const void* x_f16, const int8_t* w_nk,
                             void* y_f16, void* ws, size_t ws_bytes, int64_t M,
                             int64_t N, int64_t K, void* stream);
 
+/* Maximum scratch of cider_perchannel_linear_noalloc, in bytes (32 MiB:
+ * M*K + 4*M rounded up to 256-byte pieces, e.g. M*K up to about 33.5M). */
+#define CIDER_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* cider_perchannel_linear without a workspace argument, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference, whose
+ * primitives allocate their temporaries through MLX. The quantized
+ * activations and scales go to a scratch array the library holds in device
+ * memory, one per GPU for the life of the process
+ * (CIDER_NOALLOC_SCRATCH_BYTES); problems needing more return
+ * CIDER_E_INVALID. The call allocates nothing. Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU (other streams, other
+ * threads) race, so a caller must order them. Results are identical to
+ * cider_perchannel_linear. */
+int cider_perchannel_linear_noalloc(const void* x_f16, const int8_t* w_nk,
+                                    const float* sw, const void* bias_f16,
+                                    void* y_f16, int64_t M, int64_t N,
+                                    int64_t K, void* stream);
+
 /* Per-channel GEMM on already-quantized activations (q int8 [M,K], sa fp32
  * [M]); any M >= 1. This is dispatch 2 of csrc/src/w8a8_primitive.mm:207-247
  * on its own, for callers that quantize once and reuse q (e.g. a fused

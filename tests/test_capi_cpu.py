@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 19, syms
+    assert len(syms) == 20, syms
 
 
 def test_library_exports_every_header_symbol(lib):
@@ -99,7 +99,13 @@ def test_validation_errors_without_gpu(lib):
     need = _lib.workspace_bytes(_lib.CIDER_OP_W4A8_REF, 4, 4096, 4096)
     rc = lib.cider_w4a8_linear_ref(p, p, p, p, p, need - 1, 4, 4096, 4096, n)
     assert rc == _lib.CIDER_E_INVALID and "workspace" in _err(lib)
+    # the entry point without a workspace rejects problems beyond its scratch
+    rc = lib.cider_perchannel_linear_noalloc(p, p, p, n, p, 8192, 16, 8192, n)
+    assert rc == _lib.CIDER_E_INVALID and "scratch" in _err(lib)
+    assert _lib.workspace_bytes(_lib.CIDER_OP_PERCHANNEL, 4096, 16, 8000) <= \
+        _lib.CIDER_NOALLOC_SCRATCH_BYTES
     # empty problems are no-ops that succeed
+    assert lib.cider_perchannel_linear_noalloc(n, n, n, n, n, 0, 8, 16, n) == _lib.CIDER_OK
     assert lib.cider_perchannel_linear(n, n, n, n, n, n, 0, 0, 8, 16, n) == _lib.CIDER_OK
     assert lib.cider_int8_matmul_int32(n, n, n, 5, 0, 16, n) == _lib.CIDER_OK
     assert _err(lib) == ""
