@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--K", type=int, default=2560)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--no-decode", action="store_true", help="skip the M=1 decode leg")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the compact sweep (per-group, W4A8, M=1 / 16 / 8192 cases)")
     ap.add_argument("--qwen3", action="store_true",
                     help="instead of the default line, print one JSON line for configs[3]: "
                          "Qwen3-8B-shaped W8A8 stack, 2048-token prefill + 128 greedy "
@@ -205,6 +207,8 @@ def main():
 
     if not args.no_decode:
         result["decode"] = bench_decode(torch, lib, _lib, N, K, args, dev, stream)
+    if not args.no_sweep:
+        result["sweep"] = compact_sweep(torch, lib, _lib, args, dev, stream)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(x, w, sw, bias, y, N, K)
@@ -283,9 +287,129 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
             "us_per_call": round(us, 3), "algorithmic_bytes": nbytes,
             "achieved_gbs": round(gbs, 1), "peak_gbs": HBM_PEAK_GBS,
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm",
-            "kernel": "mv_wide_kernel<per-channel> (cider_amd/csrc/gemv.hip)",
+            "kernel": "mv_stream_kernel<2, 5, per-channel> (cider_amd/csrc/mv_stream.hip)",
             "launch_floor_us": round(floor_us, 3),
             "streaming_gbs_above_floor": None if above is None else round(above, 1)}
+
+
+def time_case(torch, stream, settle_ms, name, call_for, ncopies, M, N, K, nbytes_alg, ops,
+              mode):
+    """GPU time per call of call_for(i) (i cycling over ncopies weight copies):
+    a run of calls captured in one HIP graph, replayed (untimed) for settle_ms
+    of GPU time, then timed over 5 replays; the median per call."""
+    reps = max(24, 2 * ncopies)
+    for i in range(max(4, ncopies)):
+        call_for(i % ncopies)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(reps):
+            call_for(i % ncopies)
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    while True:
+        g.replay()
+        s1.record(stream)
+        s1.synchronize()
+        if s0.elapsed_time(s1) >= settle_ms:
+            break
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / reps)
+    ms = statistics.median(times)
+    del g
+    return {"case": name, "mode": mode, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
+            "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+            "frac_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "gbs": round(nbytes_alg / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "weight_copies": ncopies, "timing": "HIP graph of %d calls" % reps}
+
+
+def compact_sweep(torch, lib, _lib, args, dev, stream):
+    """The cases of the configs[1] / configs[2] sweep that the headline line
+    does not cover, timed as in sweep(): per-group gs 128 / 64 at M=4096, the
+    M=1 MV on the down-projection shape, W4A8 per-group gs 128 at M=4096 and
+    M=16 (the decode-batch path), per-channel at M=16 and M=8192."""
+    vp = ctypes.c_void_p
+
+    def cur():
+        return vp(torch.cuda.current_stream(dev).cuda_stream)
+
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 7)
+
+    def synth_x(M, K):
+        x = torch.randn(M, K, generator=g)
+        x[:, torch.randperm(K, generator=g)[: K // 100]] *= 20.0
+        return x.to(torch.float16).to(dev)
+
+    def copies(M, wbytes):
+        return max(1, -(-2 * MALL_BYTES // wbytes) + 1) if M <= 64 else 1
+
+    recs = []
+
+    def w8_case(M, N, K, gs):
+        nc = copies(M, N * K)
+        ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
+              for _ in range(nc)]
+        sw = ((torch.rand(N, generator=g) * 9e-3 + 1e-3) if gs == 0 else
+              (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3)).to(dev)
+        bias = torch.zeros(N, dtype=torch.float16, device=dev)
+        x = synth_x(M, K)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        op = _lib.CIDER_OP_PERCHANNEL if gs == 0 else _lib.CIDER_OP_PERGROUP
+        nb = _lib.workspace_bytes(op, M, N, K, gs)
+        wsp = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+
+        def call_for(i):
+            if gs == 0:
+                _lib.check(lib.cider_perchannel_linear(
+                    vp(x.data_ptr()), vp(ws[i].data_ptr()), vp(sw.data_ptr()),
+                    vp(bias.data_ptr()), vp(y.data_ptr()), vp(wsp.data_ptr()), nb, M, N, K,
+                    cur()))
+            else:
+                _lib.check(lib.cider_pergroup_linear(
+                    vp(x.data_ptr()), vp(ws[i].data_ptr()), vp(sw.data_ptr()),
+                    vp(bias.data_ptr()), vp(y.data_ptr()), vp(wsp.data_ptr()), nb, M, N, K, gs,
+                    cur()))
+        sbytes = 4 * N if gs == 0 else 4 * N * (K // gs)
+        nbytes = N * K + 2 * M * K + sbytes + 2 * N + 2 * M * N
+        mode = "per-channel" if gs == 0 else f"per-group-{gs}"
+        recs.append(time_case(torch, stream, args.settle_ms, "configs[1]", call_for, nc, M, N,
+                              K, nbytes, 2.0 * M * N * K, mode))
+
+    def w4_case(M, N, K, gs):
+        nc = copies(M, N * K // 2)
+        pk = [torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).to(dev)
+              for _ in range(nc)]
+        sc = (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3).to(torch.float16).to(dev)
+        x = synth_x(M, K)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        nb = _lib.workspace_bytes(_lib.CIDER_OP_W4A8_PERGROUP, M, N, K, gs)
+        wsp = torch.empty(max(nb, 1), dtype=torch.uint8, device=dev)
+
+        def call_for(i):
+            _lib.check(lib.cider_w4a8_pergroup_linear(
+                vp(x.data_ptr()), vp(pk[i].data_ptr()), vp(sc.data_ptr()), None,
+                vp(y.data_ptr()), vp(wsp.data_ptr()), nb, M, N, K, gs, cur()))
+        nbytes = N * K // 2 + 2 * M * K + 2 * N * (K // gs) + 2 * M * N
+        recs.append(time_case(torch, stream, args.settle_ms, "configs[2]", call_for, nc, M, N,
+                              K, nbytes, 2.0 * M * N * K, f"w4a8-per-group-{gs}"))
+
+    w8_case(4096, 10240, 2560, 128)
+    w8_case(4096, 10240, 2560, 64)
+    w8_case(1, 2560, 10240, 0)
+    w8_case(16, 10240, 2560, 0)
+    w8_case(8192, 10240, 2560, 0)
+    w4_case(4096, 12288, 4096, 128)
+    w4_case(16, 12288, 4096, 128)
+    torch.cuda.synchronize()
+    return recs
 
 
 def sweep(torch, args, dev):
@@ -314,41 +438,8 @@ def sweep(torch, args, dev):
         return x.to(torch.float16).to(dev)
 
     def run(name, call_for, ncopies, M, N, K, nbytes_alg, ops, mode):
-        reps = max(24, 2 * ncopies)
-        for i in range(max(4, ncopies)):
-            call_for(i % ncopies)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(reps):
-                call_for(i % ncopies)
-        # replay (untimed) for settle_ms of GPU time, so the timed replays run
-        # at settled clocks after the host-side setup of the case
-        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s0.record(stream)
-        while True:
-            g.replay()
-            s1.record(stream)
-            s1.synchronize()
-            if s0.elapsed_time(s1) >= args.settle_ms:
-                break
-        times = []
-        for _ in range(5):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            g.replay()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            times.append(e0.elapsed_time(e1) / reps)
-        ms = statistics.median(times)
-        rec = {"case": name, "mode": mode, "M": M, "N": N, "K": K, "us": round(ms * 1e3, 2),
-               "tops": round(ops / (ms * 1e-3) / 1e12, 1),
-               "frac_int8_peak": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
-               "gbs": round(nbytes_alg / (ms * 1e-3) / 1e9, 1),
-               "frac_hbm": round(nbytes_alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-               "weight_copies": ncopies, "timing": "HIP graph of %d calls" % reps}
-        del g
-        print(json.dumps(rec), flush=True)
+        print(json.dumps(time_case(torch, stream, args.settle_ms, name, call_for, ncopies, M,
+                                   N, K, nbytes_alg, ops, mode)), flush=True)
 
     def copies_for(M, wbytes):
         return max(1, -(-2 * MALL_BYTES // wbytes) + 1) if M <= 64 else 1
@@ -408,11 +499,17 @@ def sweep(torch, args, dev):
 
 
 def cpu_baseline(x, w, sw, bias, y, N, K):
-    """The oracle's C restatement (reference math, reference order) on rows
-    0..127 of the workload, timed on this host; also checks those rows."""
+    """The reference math on the host, on rows 0..127 of the workload
+    (= configs[0], M=128): the oracle's C restatement (all host threads) is
+    the reported value; BASELINE.md's two numpy restatements are timed beside
+    it (per-token quantize, then (i) a literal int32 np.matmul -- numpy runs
+    integer matmul single-threaded without BLAS -- or (ii) an exact float64
+    BLAS GEMM, then the dequant in the reference order).  The GPU's rows are
+    checked bit for bit against the C result."""
     import numpy as np
 
     from oracle import c_oracle
+    from oracle import cider_oracle as O
 
     rows = 128
     xs = x[:rows].cpu().numpy()
@@ -420,25 +517,58 @@ def cpu_baseline(x, w, sw, bias, y, N, K):
     swn = sw.cpu().numpy()
     bn = bias.cpu().numpy()
     threads = c_oracle.num_threads()
-    times = []
-    out = None
-    deadline = time.perf_counter() + 30.0
-    for _ in range(5):
-        t0 = time.perf_counter()
-        out = c_oracle.perchannel_linear_gemm(xs, wn, swn, bn)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > deadline:
-            break
-    med = statistics.median(times)
+
+    def timed(fn, runs, budget_s):
+        times, out = [], None
+        deadline = time.perf_counter() + budget_s
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            out = fn()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > deadline:
+                break
+        return statistics.median(times), len(times), out
+
+    med, nruns, out = timed(lambda: c_oracle.perchannel_linear_gemm(xs, wn, swn, bn), 5, 30.0)
     gpu_rows = y[:rows].cpu().numpy()
     exact = bool(np.array_equal(gpu_rows.view(np.uint16), out.view(np.uint16)))
+
+    # numpy restatements; the int32 matmul runs on 16 of the rows (its rate
+    # does not depend on M), the float64 BLAS one on all 128
+    w32, w64 = wn.astype(np.int32), wn.astype(np.float64)
+
+    def np_int32(xr):
+        q, sa = O.quantize_per_token(xr)
+        acc = np.matmul(q.astype(np.int32), w32.T)
+        return O.dequant_perchannel(acc, sa, swn, bn)
+
+    def np_f64(xr):
+        q, sa = O.quantize_per_token(xr)
+        acc = (q.astype(np.float64) @ w64.T).astype(np.int64).astype(np.int32)
+        return O.dequant_perchannel(acc, sa, swn, bn)
+
+    r32 = 16
+    m32, n32, o32 = timed(lambda: np_int32(xs[:r32]), 3, 20.0)
+    m64, n64, o64 = timed(lambda: np_f64(xs), 5, 10.0)
+    np_exact = bool(np.array_equal(o64.view(np.uint16), out.view(np.uint16)) and
+                    np.array_equal(o32.view(np.uint16), out[:r32].view(np.uint16)))
     return {"value": round(2.0 * rows * N * K / med / 1e12, 4), "unit": "TOPS",
             "cores": threads, "kind": "port",
             "sample": f"rows 0..{rows - 1} of the M=4096 workload (configs[0] shape "
                       f"M={rows},N={N},K={K}); C oracle, quantize+int32 GEMM+dequant; "
-                      f"median of {len(times)} runs",
-            "ms": round(med * 1e3, 2), "cpu": cpu_model(),
-            "gpu_rows_bit_exact": exact}
+                      f"median of {nruns} runs",
+            "ms": round(med * 1e3, 2), "cpu": cpu_model(), "nproc": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "openblas_num_threads": os.environ.get("OPENBLAS_NUM_THREADS"),
+            "gpu_rows_bit_exact": exact,
+            "numpy": {
+                "int32_matmul": {"ms": round(m32 * 1e3, 2), "rows": r32, "runs": n32,
+                                 "tops": round(2.0 * r32 * N * K / m32 / 1e12, 5),
+                                 "threads": 1},
+                "float64_blas": {"ms": round(m64 * 1e3, 2), "rows": rows, "runs": n64,
+                                 "tops": round(2.0 * rows * N * K / m64 / 1e12, 4),
+                                 "threads": "BLAS default"},
+                "bit_exact_vs_c": np_exact}}
 
 
 def cpu_model():
