@@ -392,6 +392,14 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // and for int8 weights at gs 128 from the smallest M (N=10240 K=2560 M=8:
     // 16.8 vs 14.2 us).  Below that the skinny kernel keeps int4 and gs 64
     // (N=12288 K=4096 M=16, int4 gs 128: 16.2 vs 25.7 us).
+    // M <= 16, per-group or int4 weights: the weight-stream kernel
+    // (skinny_stream.hip), which beat the skinny and per-group DMA kernels
+    // at every such shape measured (N=12288 K=4096 M=16, int4 gs 128: 13.4
+    // vs 17.2 us; int4 per-channel: 11.5 vs 16.4 us; int8 gs 64: 18.3 vs
+    // 20.5 us).  int8 per-channel keeps the DMA tiles and the skinny kernel
+    // (N=12288 K=4096 M=16: 13.3 us DMA vs 16.0 us stream).
+    if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
+      return launch_skinny_stream(a, wf, epi, gs, s);
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
     if (dma_pg && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
       return launch_gemm_dma_pg(a, gs, sw_half, wf, s);

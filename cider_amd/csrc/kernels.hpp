@@ -29,6 +29,17 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
 hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                        int gs, hipStream_t s);
 
+// Small-M GEMM as a weight stream (skinny_stream.hip): 1 <= M <= 64,
+// K % 64 == 0, K <= 16384, N % 4 == 0, aligned operands.
+bool skinny_stream_supported(const GemmArgs& a, int wf, int epi, int gs);
+hipError_t launch_skinny_stream(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s);
+// The earlier small-M kernel (skinny.hip), for shapes the stream kernel does
+// not take.
+hipError_t launch_skinny(const GemmArgs& a, int wf, int epi, bool sw_half, int gs,
+                         hipStream_t s);
+hipError_t launch_gemm_dma(const GemmArgs& a, int epi, int wf, hipStream_t s);
+hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s);
+
 // Decode-sized GEMV on quantized activations (1 <= M <= 4), gemv_q.hip.
 bool gemv_q_supported(const GemmArgs& a, int wf, bool fused);
 hipError_t launch_gemv_q(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s);

@@ -606,3 +606,32 @@ def test_device_errors():
         C.perchannel_linear(x.cpu(), w.cpu(), s.cpu())
     y = C.perchannel_linear(x[:0], w, s)
     assert tuple(y.shape) == (0, 8)
+
+
+# 5 <= M <= 16, per-group or int4 weights: the weight-stream kernel
+# (skinny_stream.hip).  K=12288 at gs 64 has 192 groups, taken in three
+# phases; K=10240 at gs 128 runs 8-wave workgroups; int4 loads pairs of
+# k-steps (K % 128 == 0, per-channel and gs 128) or single k-steps (gs 64);
+# N=100 / 260 / 36 leave the last 16-row block partly past N.
+@pytest.mark.parametrize("M,N,K", [(5, 100, 12288), (16, 260, 10240), (9, 4096, 2560),
+                                   (16, 36, 4096), (12, 64, 128)])
+def test_stream_small_m_exact(M, N, K):
+    x = O.synth_activations(M, K, 120 + M + K)
+    w = O.synth_weights_i8(N, K, 121 + N)
+    b = (np.random.default_rng(122).standard_normal(N) * 0.1).astype(np.float16)
+    for gs in (64, 128, 256):
+        if K % gs:
+            continue
+        sw = O.synth_scales((K // gs, N), 123 + gs)
+        y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+        assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"stream pg{gs} {M}x{N}x{K}")
+    w4 = np.random.default_rng(124).integers(-8, 8, (N, K), dtype=np.int8)
+    pk = O.pack_w4_lo_first(w4)
+    for gs in (64, 128):
+        sc = O.synth_scales((K // gs, N), 125 + gs).astype(np.float16)
+        y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b)))
+        assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, b), f"stream w4g{gs} {M}x{N}x{K}")
+    wf = np.random.default_rng(126).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"stream w4 {M}x{N}x{K}")
