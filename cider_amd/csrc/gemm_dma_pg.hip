@@ -1,6 +1,5 @@
-// Per-group int8 GEMM on the LDS-DMA pipeline (int8 weights, K % 128 == 0,
-// N % 8 == 0, M > 64).  The dispatcher sends gs = 128 here; gs = 64 compiles
-// and is bit-exact too, but its four accumulator sets spill.
+// Per-group int8 GEMM on the LDS-DMA pipeline (int8 or packed int4 weights,
+// gs 64 / 128, K % 128 == 0, N % 8 == 0).
 //
 // Reference semantics (cider/kernels/pergroup_int8_gemm.metal:90-191), kept
 // operation for operation, so results are bit-identical to the restatement:
@@ -9,28 +8,28 @@
 //   y[m,n]   = h(f32(acc * sa[m]) [+ f32(bias[n])])
 //
 // MI355X design
-//   * Tile 128 x 128, 4 waves of 64 x 64 (TM = TN = 2 blocks of 32 x 32),
+//   * Waves of 64 x 32 (TM = 2 blocks of 32 x 32 along m, TN = 1 along n),
 //     v_mfma_i32_32x32x32_i8; operands reach LDS by global_load_lds_dwordx4
-//     through a 4-slot ring of 128-byte k-stages,
-//     with the constant-count waits, swizzle and fixed-order sub-steps of
-//     the per-channel kernel (gemm_dma.hip).
+//     through a ring of 128-byte k-stages, with the constant-count waits,
+//     swizzle and fixed-order sub-steps of the per-channel kernel
+//     (gemm_dma.hip).  Two launch shapes: 128 x 128 tiles of 8 waves (two
+//     per SIMD, 4 ring slots; gs 64 at M > 64) and 128 x 64 tiles of 4 waves
+//     (gs 128 at two workgroups per CU, gs 64 at M <= 64).
 //   * Group accumulators: two int32 sets alternate by group.  A group's first
 //     MFMA takes C = 0 (an inline constant), so starting a group costs
 //     nothing.  While group g accumulates, group g-1 is flushed into the fp32
 //     accumulators, a slice per sub-step interleaved with group g's MFMAs in
-//     the same fixed order: 4 VALU ops per accumulator (convert, multiply by
-//     the scale, add; a register read when the set lives in AGPRs).  The
-//     flush is the VALU bound of the kernel: about 2x the MFMA time at
-//     gs = 128, 4x at gs = 64.  Before the first group the other set is zero
-//     and its "scales" are group 0's, so the first flush adds +0.0; the last
-//     stage flushes the last group after its MFMAs.
-//   * Tile 128 x 64.  gs = 128 runs two workgroups per CU: the sets and the
-//     fp32 accumulators then fit in VGPRs, and one workgroup's LDS / barrier
-//     waits hide behind the other's flush.  gs = 64 (twice the flush per
-//     sub-step) runs one workgroup per CU, where it needs no spill: a spill
+//     the same fixed order: 3 VALU ops per accumulator (convert, multiply by
+//     the scale, add: the reference's two roundings rule out a fused
+//     multiply-add).  That flush is the kernel's bound: 12 VALU ops per MFMA
+//     at gs = 128, 24 at gs = 64, against the MFMA's 32 cycles and 4 per
+//     wave64 VALU op.  Before the first group the other set is zero and its
+//     "scales" are group 0's, so the first flush adds +0.0; the last stage
+//     flushes the last group after its MFMAs.  Every register is
+//     architectural (no AGPR reads in the flush) and nothing spills: a spill
 //     reload is a vector-memory load the compiler tracks, and waiting for it
 //     would also wait for every LDS-DMA load in flight.
-//   * Scales: wave 0 DMAs the scale rows of a stage's groups (sw[g, n0..n0+127])
+//   * Scales: wave 0 DMAs the scale rows of a stage's groups (sw[g, n0..n0+BN))
 //     into an 8-slot LDS ring of its own, so a row stays in LDS until its
 //     group has been flushed during the next stage.  Wave 0 therefore moves one
 //     more load per stage than the others, and waits with its own count.
@@ -46,17 +45,17 @@ namespace cider {
 
 namespace {
 
-// Geometry of a BM x BN tile, 4 waves of (BM / 2) x (BN / 2); int8 or packed
-// int4 weights (WF); OCC workgroups per CU share the LDS.
-template <int BM, int BN_, int WF, int OCC>
+// Geometry of a BM x BN tile, WGM x WGN waves of (BM / WGM) x (BN / WGN);
+// int8 or packed int4 weights (WF); OCC workgroups per CU share the LDS.
+template <int BM, int BN_, int WF, int OCC, int WGM, int WGN>
 struct PgCfg {
-  static constexpr int BN = BN_, BK = 128;
-  static constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  static constexpr int BN = BN_, BK = 128, NW = WGM * WGN;
+  static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   static constexpr int CH = BK / 16, RPI = 1024 / BK;        // X: 8 chunks, 8 rows per DMA
   static constexpr int WB = (WF == W_I4) ? BK / 2 : BK;      // weight bytes per row and stage
   static constexpr int CHW = WB / 16, RPIW = 1024 / WB;
-  static constexpr int WI = BN / RPIW / 4;                   // DMA instructions (W rows)
-  static constexpr int XI = BM / RPI / 4;                    // DMA instructions (X rows)
+  static constexpr int WI = BN / RPIW / NW;                  // DMA instructions (W rows)
+  static constexpr int XI = BM / RPI / NW;                   // DMA instructions (X rows)
   static constexpr int PS = WI + XI;                         // per wave and stage (+1 on wave 0)
   static constexpr int W_BYTES = BN * WB;
   static constexpr int STAGE = W_BYTES + BM * BK;
@@ -68,7 +67,9 @@ struct PgCfg {
   static constexpr int SMEM = RING + SNS * SSLOT;
   static constexpr int OUT_LD = BN * 2 + 16;
   static constexpr int OUT = BM * OUT_LD;
-  static_assert(WI >= 1 && XI >= 1 && TN >= 1, "tile too small for the DMA split");
+  static_assert(WI >= 1 && XI >= 1 && TN >= 1 && TM >= 1, "tile too small for the DMA split");
+  static_assert(WI * RPIW * NW == BN && XI * RPI * NW == BM, "whole DMA instructions");
+  static_assert(64 * NW >= BM && 64 * NW >= BN, "one thread per tile row / column in the epilogue");
   static_assert(OUT + BM * 4 + BN * 2 <= RING, "epilogue staging fits the ring");
   static_assert(SMEM <= LDS, "LDS budget");
   static_assert(NS >= 2 && (NS - 1) * (PS + 1) <= 63, "vmcnt range");
@@ -86,19 +87,17 @@ __device__ __forceinline__ i32x4 pg_unpack_w4_8(uint32_t w0, uint32_t w1) {
 template <int V>
 using ic = std::integral_constant<int, V>;
 
-// Dispatched tile: 128 x 64.  gs = 128 runs two workgroups per CU (each
-// workgroup's waits hide behind the other's flush; the int32 group sets then
-// fit in VGPRs, so the flush reads them without v_accvgpr_read).  gs = 64
-// does not fit 256 registers that way (a spill would make the compiler wait
-// for every LDS-DMA load in flight), so it runs one workgroup per CU.
+// Width of the 4-wave tile (128 x 64).  gs = 128 runs two of its workgroups
+// per CU: each workgroup's waits hide behind the other's flush.
 constexpr int PG_LAUNCH_BN = 64;
 
 }  // namespace
 
-template <int BM, int BN, int GS, bool SWH, int WF, int OCC>
-__global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p) {
+template <int BM, int BN, int GS, bool SWH, int WF, int OCC, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128, "group size");
-  using C = PgCfg<BM, BN, WF, OCC>;
+  using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
+  constexpr int NW = C::NW;
   constexpr bool W4 = (WF == W_I4);
   constexpr int WB = C::WB, CHW = C::CHW, RPIW = C::RPIW;
   constexpr int PG_BM = BM, PG_BN = C::BN, PG_BK = C::BK, PG_WM = C::WM, PG_WN = C::WN;
@@ -123,7 +122,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WGM, wn = wave / WGM;
   const int h = lane >> 5;
   const int M = p.M, N = p.N, K = p.K;
   const int G = K / GS;
@@ -132,7 +131,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
   tile_coords<PG_BM, PG_BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
 
   // Sources: the tile's first W (X) row as a wave-uniform base, and per
-  // lane and instruction a 32-bit byte offset from it (< 128 rows x K).
+  // lane and instruction a 32-bit byte offset from it (< 256 rows x K).
   const int64_t ldw = W4 ? (K >> 1) : K;
   const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * ldw;
   const int8_t* const xbase = p.x + (int64_t)m0 * K;
@@ -329,6 +328,11 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
         const int aa = combo / 4, r = 4 * (combo % 4) + rr;
         const float t = (float)D[1 - CS][aa][bb][r] * sv[SVDB ? (J & 1) : 0][c][rr];
         facc[aa][bb][r] = facc[aa][bb][r] + t;
+        // Pins this flush element to its slot: without it the compiler sinks
+        // the whole flush of a group below the next group's MFMAs, in one
+        // VALU block that the MFMAs no longer hide (and, at 64 x 64 waves,
+        // with both versions of the set alive at once).
+        asm volatile("" : "+v"(facc[aa][bb][r]));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -482,7 +486,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
   const int cl = (lane % LPR) * 8;
   const int n = n0 + cl;
 #pragma unroll 4
-  for (int rr = wave * RPS + lane / LPR; rr < PG_BM; rr += 4 * RPS) {
+  for (int rr = wave * RPS + lane / LPR; rr < PG_BM; rr += NW * RPS) {
     const int m = m0 + rr;
     if (m < M && n < N)
       *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
@@ -490,27 +494,44 @@ __global__ __launch_bounds__(256, OCC) void gemm_dma_pg_kernel(const GemmArgs p)
   }
 }
 
-// Eligible: int8 weights, per-group gs 64 / 128, K % 128 == 0, N % 8 == 0,
-// 16-byte aligned operands (launch_gemm checks).
+// Eligible: int8 or int4 weights, per-group gs 64 / 128, K % 128 == 0,
+// N % 8 == 0, 16-byte aligned operands (launch_gemm checks).
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
+  if (gs == 64 && a.M > 64) {
+    // 128 x 128 tiles, 8 waves of 64 x 32 (two per SIMD), all registers
+    // architectural: 1.65x the rate of the one-wave-per-SIMD 128 x 64 tile
+    // at M=4096 N=10240 K=2560 (229 vs 382 us), and ahead even where its
+    // fewer tiles leave CUs idle, since each tile runs at twice the rate.
+    constexpr int BM = 128, BN = 128;
+    const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    if (wf == W_I4)
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+    else if (sw_half)
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+    else
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+    return hipGetLastError();
+  }
+  // 128 x 64 tiles, 4 waves of 64 x 32: gs 128 runs two workgroups per CU
+  // (the 8-wave 128 x 128 tile measured level with it), gs 64 at M <= 64 one
   constexpr int BM = 128, BN = PG_LAUNCH_BN;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (wf == W_I4) {
     // int4 weights come with fp16 group scales ([K/gs, N])
     if (gs == 64)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
   } else if (gs == 64) {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
   } else {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
   }
   return hipGetLastError();
 }
