@@ -89,15 +89,21 @@ int check_ws(const char* fn, const void* ws, size_t ws_bytes, size_t needed) {
   return CIDER_OK;
 }
 
-// Decode-sized calls (M <= 4, K <= 16384, aligned) run one GEMV kernel that
-// quantizes x per token while staging it (same helpers as the quantize
-// kernel, so the same q and scale_a) instead of a quantize launch followed by
-// a GEMM launch.  Returns true and the launch status in *rc if it ran.
+// Decode-sized calls run one GEMV kernel that quantizes x per token while
+// staging it (same helpers as the quantize kernel, so the same q and scale_a)
+// instead of a quantize launch followed by a GEMM launch: M == 1 (W4A8; the
+// int8 formats run the fp16 MV there), and 2 <= M <= 4 while the quantization
+// every 16-row workgroup repeats stays small (N / 16 * M * K <= 2^20
+// elements).  Past that the repeated quantization costs more than the launch
+// it saves: N=10240 K=2560 M=2 ran 13.3 us fused against 10.8 us as quantize
+// + GEMV, M=4 24.9 against 13.3 us (W4A8 gs 128, N=12288 K=4096 M=4: 22.5
+// against 15.0 us).  Returns true and the launch status in *rc if it ran.
 bool try_fused_gemv(const char* fn, const void* x, const cider::GemmArgs& g, int wf, int epi,
                     int gs, hipStream_t s, int* rc) {
   cider::GemmArgs t = g;
   t.x = reinterpret_cast<const int8_t*>(x);
   if (!cider::gemv_q_supported(t, wf, true)) return false;
+  if (g.M > 1 && (int64_t)((g.N + 15) / 16) * g.M * g.K > ((int64_t)1 << 20)) return false;
   *rc = hip_status(cider::launch_gemv_qx(reinterpret_cast<const uint16_t*>(x), g, wf, epi, gs, s),
                    fn);
   return true;

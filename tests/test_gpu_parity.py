@@ -635,3 +635,47 @@ def test_stream_small_m_exact(M, N, K):
     packed, sw4 = O.pack_weight_int4(wf)
     y = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
     assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"stream w4 {M}x{N}x{K}")
+
+
+# 2 <= M <= 16 through the quantizing linears, with rows of special values:
+# q and scale_a must be those of the quantize kernel whichever kernel runs
+# (the fused decode GEMV at small N, or quantize + GEMV / stream / DMA tiles),
+# and the output of a row with inf or NaN is then NaN / +-inf exactly as the
+# oracle's.  K=64 leaves 7 of 8 waves of the stream kernel without a k-step;
+# N=24 / 264 / 8200 leave the last workgroup partly past N.
+@pytest.mark.parametrize("M,N,K", [(2, 24, 64), (3, 40, 128), (7, 264, 320), (16, 4096, 2560),
+                                   (16, 12288, 4096), (11, 8200, 4096), (5, 1024, 1024)])
+def test_small_m_quantized_exact(M, N, K):
+    x = O.synth_activations(M, K, 130 + M + K)
+    if M >= 5:
+        x[1, :] = 0                                 # s = 1, q = 0
+        x[2, :4] = [np.nan, 3.0, -6.0, 0.5]         # NaN ignored by the absmax, q = -128
+        x[3, 7] = np.inf                            # s = inf
+        x[4, :3] = [65504.0, -65504.0, 1.0]
+    w = O.synth_weights_i8(N, K, 131 + N)
+    sw = O.synth_scales(N, 132)
+    b = (np.random.default_rng(133).standard_normal(N) * 0.1).astype(np.float16)
+    for bias in (b, None):
+        y = H(C.perchannel_linear(T(x), T(w), T(sw), None if bias is None else T(bias)))
+        assert_bits_equal(y, O.perchannel_linear(x, w, sw, bias), f"small-M pc {M}x{N}x{K}")
+    for gs in (64, 128):
+        if K % gs:
+            continue
+        swg = O.synth_scales((K // gs, N), 134 + gs)
+        y = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
+        assert_bits_equal(y, O.pergroup_linear(x, w, swg, gs, b), f"small-M pg{gs} {M}x{N}x{K}")
+    w4 = np.random.default_rng(135).integers(-8, 8, (N, K), dtype=np.int8)
+    pk = O.pack_w4_lo_first(w4)
+    for gs in (64, 128):
+        if K % gs:
+            continue
+        sc = O.synth_scales((K // gs, N), 136 + gs).astype(np.float16)
+        for bias in (b, None):
+            y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs,
+                                         None if bias is None else T(bias)))
+            assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, bias),
+                              f"small-M w4g{gs} {M}x{N}x{K}")
+    wf = np.random.default_rng(137).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"small-M w4 {M}x{N}x{K}")
