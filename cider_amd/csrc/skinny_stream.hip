@@ -9,8 +9,9 @@
 //           fp32 chain per output over the groups in order
 //
 // MI355X layout
-//   * A workgroup owns 16 weight rows n0 .. n0 + 15 and every activation row
-//     (TM blocks of 16).  v_mfma_i32_16x16x64_i8 takes the weights as A (lane
+//   * A workgroup owns RB blocks of 16 weight rows (n0 .. n0 + 16 RB - 1) and
+//     every activation row (TM blocks of 16); RB = 2 or 3 at M <= 16 on wide
+//     N, so the activations of a k-range are read once for several blocks.  v_mfma_i32_16x16x64_i8 takes the weights as A (lane
 //     l: row l % 16, k slice 16 (l / 16) of a 64-wide k-step) and the
 //     quantized activations as B, so a lane's weight bytes go from HBM
 //     straight into the MFMA operand.
@@ -26,7 +27,8 @@
 //   * Per-group: each wave writes its groups' terms f32(f32(D_g) * sw[g, n])
 //     to LDS, and after one barrier the owner of each output adds all G terms
 //     in group order -- the reference's chain.  Groups are taken in phases of
-//     at most 64 KB of terms, each phase loading its own k-steps.
+//     at most 64 KB of terms (128 KB when RB > 1), each phase loading its own
+//     k-steps.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -45,7 +47,7 @@ __device__ __forceinline__ f32x4 load_scale4(const void* base, int64_t idx) {
   }
 }
 
-constexpr int kTermBytes = 64 * 1024;  // LDS for one phase of per-group terms
+constexpr int kTermBytes = 64 * 1024;  // LDS for one phase of per-group terms (RB == 1)
 
 // int4 weights load pairs of k-steps (16 bytes per lane) unless a group
 // boundary falls inside a pair (gs 64)
@@ -53,26 +55,30 @@ constexpr bool pair_slots(int WF, int EPI, int GS) {
   return WF == W_I4 && (EPI != EPI_PG || GS >= 128);
 }
 
+// LDS for the per-group terms of a phase: RB > 1 runs one workgroup per CU
+// and takes 128 KB, so the groups of the shapes it serves fit one phase.
+constexpr int term_bytes(int RB) { return RB == 1 ? kTermBytes : 2 * kTermBytes; }
+
 // Groups per phase of the per-group kernel: the phase's terms fit
-// kTermBytes, and a wave's share (every KW-th group) fits its NB load slots.
-constexpr int phase_groups(int TM, int WF, int EPI, int GS, int KW, int NB) {
+// term_bytes, and a wave's share (every KW-th group) fits its NB load slots.
+constexpr int phase_groups(int TM, int WF, int EPI, int GS, int KW, int NB, int RB = 1) {
   const int slots = EPI == EPI_PG ? GS / (pair_slots(WF, EPI, GS) ? 128 : 64) : 1;
-  const int by_lds = kTermBytes / (TM * 256 * 4);
+  const int by_lds = term_bytes(RB) / (RB * TM * 256 * 4);
   const int by_regs = KW * (NB / slots);
   return by_lds < by_regs ? by_lds : by_regs;
 }
 
 }  // namespace
 
-template <int TM, int WF, int EPI, bool SWH, int GS, int KW, int NB>
+template <int TM, int WF, int EPI, bool SWH, int GS, int KW, int NB, int RB>
 __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p) {
   constexpr int kThreads = KW * 64;
   constexpr bool PG = EPI == EPI_PG;
   constexpr int SUB = PG ? GS / 64 : 1;     // k-steps per group
-  constexpr int NOUT = TM * 256;            // outputs of the workgroup (16 n x 16 TM m)
-  // per-group: groups per phase -- the terms of a phase fit kTermBytes and
+  constexpr int NOUT = RB * TM * 256;       // outputs of the workgroup (16 RB n x 16 TM m)
+  // per-group: groups per phase -- the terms of a phase fit term_bytes and
   // each wave's share of them fits its NB load slots
-  constexpr int GP = phase_groups(TM, WF, EPI, GS, KW, NB);
+  constexpr int GP = phase_groups(TM, WF, EPI, GS, KW, NB, RB);
   constexpr int RED = PG ? GP * NOUT * 4 : KW * NOUT * 4;
   __shared__ __attribute__((aligned(16))) uint8_t lds[RED];
 
@@ -80,13 +86,15 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lrow = lane & 15, lq = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
-  const int n0 = blockIdx.x * 16;
-  const int nw = min(n0 + lrow, N - 1);      // weight row of this lane (clamped)
+  const int n0 = blockIdx.x * 16 * RB;
   const int8_t* __restrict__ X = p.x;
   const int8_t* __restrict__ W = reinterpret_cast<const int8_t*>(p.w);
   const int64_t ldw = (WF == W_I4) ? (K >> 1) : K;
-  // load slots of KSTEP k (below): K / 64 or K / 128
-  const int8_t* wrow = W + (int64_t)nw * ldw;
+  // load slots of KSTEP k (below): K / 64 or K / 128; block rb's weight row
+  // of this lane (clamped)
+  const int8_t* wrow[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) wrow[rb] = W + (int64_t)min(n0 + 16 * rb + lrow, N - 1) * ldw;
   const int8_t* xrow[TM];
 #pragma unroll
   for (int b = 0; b < TM; ++b) xrow[b] = X + (int64_t)min(b * 16 + lrow, M - 1) * K;
@@ -102,20 +110,24 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
   constexpr bool P2 = pair_slots(WF, EPI, GS);
   constexpr int KSTEP = P2 ? 128 : 64;       // k per load slot
   constexpr int NX = P2 ? 2 : 1;             // MFMA k-steps per load slot
-  auto load_k = [&](int k, i32x4& wv, i32x4 (&xv)[NX][TM]) {
+  auto load_k = [&](int k, i32x4 (&wv)[RB], i32x4 (&xv)[NX][TM]) {
     if constexpr (P2) {
-      wv = ld16(wrow + k * 64 + 16 * lq);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) wv[rb] = ld16(wrow[rb] + k * 64 + 16 * lq);
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
         xv[0][b] = ld16(xrow[b] + k * 128 + 32 * lq);
         xv[1][b] = ld16(xrow[b] + k * 128 + 32 * lq + 16);
       }
     } else {
-      if constexpr (WF == W_I4) {
-        const i32x2 v = ld8(wrow + k * 32 + 8 * lq);
-        wv = i32x4{v[0], v[1], 0, 0};
-      } else {
-        wv = ld16(wrow + k * 64 + 16 * lq);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        if constexpr (WF == W_I4) {
+          const i32x2 v = ld8(wrow[rb] + k * 32 + 8 * lq);
+          wv[rb] = i32x4{v[0], v[1], 0, 0};
+        } else {
+          wv[rb] = ld16(wrow[rb] + k * 64 + 16 * lq);
+        }
       }
 #pragma unroll
       for (int b = 0; b < TM; ++b) xv[0][b] = ld16(xrow[b] + k * 64 + 16 * lq);
@@ -139,12 +151,14 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
     const int nk = K / KSTEP;
     const int per = (nk + KW - 1) / KW;
     const int k0 = min(wave * per, nk), kend = min(k0 + per, nk);
-    i32x4 acc[TM];
+    i32x4 acc[RB][TM];
 #pragma unroll
-    for (int b = 0; b < TM; ++b) acc[b] = i32x4{0, 0, 0, 0};
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) acc[rb][b] = i32x4{0, 0, 0, 0};
     for (int kr = k0; kr < kend; kr += NB) {
       const int cnt = min(NB, kend - kr);
-      i32x4 wv[NB], xv[NB][NX][TM];
+      i32x4 wv[NB][RB], xv[NB][NX][TM];
       // unconditional: even a wave-uniform branch around a load makes the
       // compiler wait for the loads before it; surplus slots re-read the
       // round's last slot
@@ -157,46 +171,55 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
         // the loop must unroll, or the fragment arrays go to scratch memory
         if (j < cnt) {
 #pragma unroll
-          for (int h = 0; h < NX; ++h) {
-            const i32x4 a = operand(wv[j], h);
+          for (int h = 0; h < NX; ++h)
 #pragma unroll
-            for (int b = 0; b < TM; ++b) acc[b] = mfma_i8(a, xv[j][h][b], acc[b]);
-          }
+            for (int rb = 0; rb < RB; ++rb) {
+              const i32x4 a = operand(wv[j][rb], h);
+#pragma unroll
+              for (int b = 0; b < TM; ++b) acc[rb][b] = mfma_i8(a, xv[j][h][b], acc[rb][b]);
+            }
         }
       }
     }
     // ---- the KW partial tiles, summed through LDS (int32: exact)
     i32x4* red = reinterpret_cast<i32x4*>(lds);
 #pragma unroll
-    for (int b = 0; b < TM; ++b) red[(wave * TM + b) * 64 + lane] = acc[b];
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) red[((wave * RB + rb) * TM + b) * 64 + lane] = acc[rb][b];
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int b = 0; b < TM; ++b)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int w = 1; w < KW; ++w) acc[b] += red[(w * TM + b) * 64 + lane];
-    // lane holds C[n][m] for n = n0 + 4 lq + r (r < 4), m = 16 b + lrow
-    const int ncol = n0 + 4 * lq;
-    if (ncol >= N) return;
+      for (int b = 0; b < TM; ++b)
 #pragma unroll
-    for (int b = 0; b < TM; ++b) {
-      const int m = b * 16 + lrow;
-      if (m >= M) continue;
-      if constexpr (EPI == EPI_I32) {
-        *reinterpret_cast<i32x4*>(reinterpret_cast<int32_t*>(p.y) + (int64_t)m * N + ncol) =
-            acc[b];
-      } else {
-        const float sam = p.sa[m];
-        const f32x4 swv = load_scale4<false>(p.sw, ncol);
-        float v[4];
+        for (int w = 1; w < KW; ++w) acc[rb][b] += red[((w * RB + rb) * TM + b) * 64 + lane];
+    // lane holds C[n][m] for n = n0 + 16 rb + 4 lq + r (r < 4), m = 16 b + lrow
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[r] = (float)acc[b][r] * sam;
-          v[r] = v[r] * swv[r];
-          if (p.bias) v[r] = v[r] + h2f(p.bias[ncol + r]);
+    for (int rb = 0; rb < RB; ++rb) {
+      const int ncol = n0 + 16 * rb + 4 * lq;
+      if (ncol >= N) continue;
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int m = b * 16 + lrow;
+        if (m >= M) continue;
+        if constexpr (EPI == EPI_I32) {
+          *reinterpret_cast<i32x4*>(reinterpret_cast<int32_t*>(p.y) + (int64_t)m * N + ncol) =
+              acc[rb][b];
+        } else {
+          const float sam = p.sa[m];
+          const f32x4 swv = load_scale4<false>(p.sw, ncol);
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            v[r] = (float)acc[rb][b][r] * sam;
+            v[r] = v[r] * swv[r];
+            if (p.bias) v[r] = v[r] + h2f(p.bias[ncol + r]);
+          }
+          *reinterpret_cast<i32x2*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + ncol) =
+              i32x2{(int)f2h2(v[0], v[1]), (int)f2h2(v[2], v[3])};
         }
-        *reinterpret_cast<i32x2*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + ncol) =
-            i32x2{(int)f2h2(v[0], v[1]), (int)f2h2(v[2], v[3])};
       }
     }
   } else {
@@ -213,8 +236,8 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
     for (int g0 = 0; g0 < G; g0 += GP) {
       const int gp = min(GP, G - g0);
       const int ng = (gp - wave + KW - 1) / KW;  // groups of this wave (>= 0)
-      i32x4 wv[NB], xv[NB][NX][TM];
-      f32x4 sv[NG];
+      i32x4 wv[NB][RB], xv[NB][NX][TM];
+      f32x4 sv[NG][RB];
 #pragma unroll
       for (int q = 0; q < NG; ++q) {
         // unconditional (see above): surplus slots re-read a valid group
@@ -222,30 +245,37 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s)
           load_k(gc * SLOTS + s, wv[q * SLOTS + s], xv[q * SLOTS + s]);
-        sv[q] = load_scale4<SWH>(p.sw, (int64_t)gc * N + min(n0 + 4 * lq, N - 4));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sv[q][rb] = load_scale4<SWH>(p.sw, (int64_t)gc * N + min(n0 + 16 * rb + 4 * lq, N - 4));
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int q = 0; q < NG; ++q) {
         if (q >= ng) continue;  // uniform; not a break (see above)
-        i32x4 d[TM];
+        i32x4 d[RB][TM];
 #pragma unroll
         for (int s = 0; s < SLOTS; ++s)
 #pragma unroll
-          for (int h = 0; h < NX; ++h) {
-            const i32x4 a = operand(wv[q * SLOTS + s], h);
+          for (int h = 0; h < NX; ++h)
 #pragma unroll
-            for (int b = 0; b < TM; ++b)
-              d[b] = mfma_i8(a, xv[q * SLOTS + s][h][b], s + h == 0 ? i32x4{0, 0, 0, 0} : d[b]);
-          }
+            for (int rb = 0; rb < RB; ++rb) {
+              const i32x4 a = operand(wv[q * SLOTS + s][rb], h);
+#pragma unroll
+              for (int b = 0; b < TM; ++b)
+                d[rb][b] = mfma_i8(a, xv[q * SLOTS + s][h][b],
+                                   s + h == 0 ? i32x4{0, 0, 0, 0} : d[rb][b]);
+            }
         const int gl = wave + KW * q;  // group within the phase
 #pragma unroll
-        for (int b = 0; b < TM; ++b) {
-          f32x4 t;
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) t[e] = (float)d[b][e] * sv[q][e];
-          *reinterpret_cast<f32x4*>(terms + (gl * TM + b) * 256 + lane * 4) = t;
-        }
+          for (int b = 0; b < TM; ++b) {
+            f32x4 t;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] = (float)d[rb][b][e] * sv[q][rb][e];
+            *reinterpret_cast<f32x4*>(terms + ((gl * RB + rb) * TM + b) * 256 + lane * 4) = t;
+          }
       }
       __syncthreads();
       // the chain: output idx adds the phase's terms in group order
@@ -257,14 +287,14 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
       }
       __syncthreads();  // terms are rewritten by the next phase
     }
-    // output idx = (b, lane, e): weight row n0 + 4 (lane / 16) + e, activation
-    // row 16 b + lane % 16 (the MFMA's C layout)
+    // output idx = (rb, b, lane, e): weight row n0 + 16 rb + 4 (lane / 16) + e,
+    // activation row 16 b + lane % 16 (the MFMA's C layout)
 #pragma unroll
     for (int o = 0; o < OWN; ++o) {
       const int idx = tid + o * kThreads;
       if (idx >= NOUT) continue;
-      const int b = idx >> 8, l = (idx >> 2) & 63, e = idx & 3;
-      const int n = n0 + 4 * (l >> 4) + e, m = b * 16 + (l & 15);
+      const int rb = idx / (TM * 256), b = (idx >> 8) % TM, l = (idx >> 2) & 63, e = idx & 3;
+      const int n = n0 + 16 * rb + 4 * (l >> 4) + e, m = b * 16 + (l & 15);
       if (m >= M || n >= N) continue;
       float v = facc[o] * p.sa[m];
       if (p.bias) v = v + h2f(p.bias[n]);
@@ -275,10 +305,31 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
 
 namespace {
 
-template <int TM, int WF, int EPI, bool SWH, int GS, int KW, int NB>
+template <int TM, int WF, int EPI, bool SWH, int GS, int KW, int NB, int RB = 1>
 hipError_t run_ss(const GemmArgs& a, hipStream_t s) {
-  skinny_stream_kernel<TM, WF, EPI, SWH, GS, KW, NB><<<(a.N + 15) / 16, KW * 64, 0, s>>>(a);
+  skinny_stream_kernel<TM, WF, EPI, SWH, GS, KW, NB, RB>
+      <<<(a.N + 16 * RB - 1) / (16 * RB), KW * 64, 0, s>>>(a);
   return hipGetLastError();
+}
+
+// Row blocks per workgroup at M <= 16: every workgroup reads the activations
+// of its k-range once for its RB blocks, so 3 blocks read a third of the
+// activation bytes of 1 (for int4 weights at M = 16 those bytes are twice the
+// weight bytes).  RB > 1 runs 8 waves of NB = 8 slots (4 pair slots) and
+// keeps about 256 workgroups; per-group needs every group in one phase.
+// Measured (kernel only, N=12288 K=4096 M=16, int4 gs 128): 9.9 us at RB = 3
+// against 14.7 us at RB = 1.
+template <int WF, int EPI, bool SWH, int GS>
+int pick_rb(const GemmArgs& a) {
+  constexpr int NB = pair_slots(WF, EPI, GS) ? 4 : 8;
+  int rb = a.N >= 48 * 240 ? 3 : a.N >= 32 * 240 ? 2 : 1;
+  if constexpr (EPI == EPI_PG) {
+    const int G = a.K / GS;
+    while (rb > 1 && (rb == 3 ? G > phase_groups(1, WF, EPI, GS, 8, NB, 3)
+                              : G > phase_groups(1, WF, EPI, GS, 8, NB, 2)))
+      --rb;
+  }
+  return rb;
 }
 
 // KW waves per workgroup, 4 or 8 (a 16-wave workgroup's 128 VGPRs per lane
@@ -291,6 +342,12 @@ hipError_t pick_kw(const GemmArgs& a, hipStream_t s) {
   // load slots per lane and round: a pair slot holds twice the activations
   constexpr int NB0 = TM == 1 ? 16 : TM == 2 ? 12 : 8;
   constexpr int NB = P2 ? NB0 / 2 : NB0;
+  if constexpr (TM == 1 && EPI != EPI_I32) {
+    constexpr int NBR = P2 ? 4 : 8;
+    const int rb = pick_rb<WF, EPI, SWH, GS>(a);
+    if (rb == 3) return run_ss<TM, WF, EPI, SWH, GS, 8, NBR, 3>(a, s);
+    if (rb == 2) return run_ss<TM, WF, EPI, SWH, GS, 8, NBR, 2>(a, s);
+  }
   if constexpr (EPI == EPI_PG) {
     // 4 waves when every group fits one phase of theirs, else 8
     const int G = a.K / GS;
