@@ -377,8 +377,8 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
   const bool off32 = (int64_t)a.K * 256 < ((int64_t)1 << 32);
   const bool dma = epi != EPI_PG && (wf == W_I8 || epi == EPI_PC) && vec && a.K % 128 == 0 &&
                    a.N % 8 == 0 && off32;
-  const bool dma_pg = epi == EPI_PG && (gs == 64 || gs == 128) && vec && a.K % 128 == 0 &&
-                      a.N % 8 == 0 && off32;
+  const bool dma_pg = epi == EPI_PG && (gs == 64 || gs == 128 || (gs == 256 && wf == W_I8)) &&
+                      vec && a.K % 128 == 0 && a.K % gs == 0 && a.N % 8 == 0 && off32;
   if (a.M <= 64) {
     // The LDS-DMA kernel's 64 x 64 tiles load whole weight rows (one 16-byte
     // lane after another) and beat the skinny kernel, whose MFMA operand loads
@@ -401,13 +401,14 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
       return launch_skinny_stream(a, wf, epi, gs, s);
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
-    if (dma_pg && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
+    if (dma_pg && gs != 256 && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
       return launch_gemm_dma_pg(a, gs, sw_half, wf, s);
     return launch_skinny(a, wf, epi, sw_half, gs, s);
   }
   if (dma) return launch_gemm_dma(a, epi, wf, s);  // LDS-DMA pipeline (gemm_dma.hip)
-  // per-group gs 64 / 128 on the LDS-DMA per-group kernel (gs 256 and other
-  // shapes on the register-staged kernel)
+  // per-group on the LDS-DMA per-group kernel (int4 weights at gs 256 --
+  // which the W4A8 formats do not define -- and other shapes on the
+  // register-staged kernel)
   if (dma_pg) return launch_gemm_dma_pg(a, gs, sw_half, wf, s);  // gemm_dma_pg.hip
   if (epi == EPI_I32) return run_tiled<256, 256, W_I8, EPI_I32, false, 0>(a, vec, s);
   if (epi == EPI_PC) {

@@ -1,5 +1,5 @@
 // Per-group int8 GEMM on the LDS-DMA pipeline (int8 or packed int4 weights,
-// gs 64 / 128, K % 128 == 0, N % 8 == 0).
+// gs 64 / 128, and gs 256 for int8 weights; K % 128 == 0, N % 8 == 0).
 //
 // Reference semantics (cider/kernels/pergroup_int8_gemm.metal:90-191), kept
 // operation for operation, so results are bit-identical to the restatement:
@@ -13,8 +13,8 @@
 //     through a ring of 128-byte k-stages, with the constant-count waits,
 //     swizzle and fixed-order sub-steps of the per-channel kernel
 //     (gemm_dma.hip).  Two launch shapes: 128 x 128 tiles of 8 waves (two
-//     per SIMD, 4 ring slots; gs 64 at M > 64) and 128 x 64 tiles of 4 waves
-//     (gs 128 at two workgroups per CU, gs 64 at M <= 64).
+//     per SIMD, 4 ring slots; gs 64 and 256 at M > 64) and 128 x 64 tiles of
+//     4 waves (gs 128 at two workgroups per CU, gs 64 at M <= 64).
 //   * Group accumulators: two int32 sets alternate by group.  A group's first
 //     MFMA takes C = 0 (an inline constant), so starting a group costs
 //     nothing.  While group g accumulates, group g-1 is flushed into the fp32
@@ -23,7 +23,8 @@
 //     the scale, add: the reference's two roundings rule out a fused
 //     multiply-add).  That flush is the kernel's bound: 12 VALU ops per MFMA
 //     at gs = 128, 24 at gs = 64, against the MFMA's 32 cycles and 4 per
-//     wave64 VALU op.  Before the first group the other set is zero and its
+//     wave64 VALU op (6 at gs = 256).  A gs 256 group spans two k-stages, so
+//     the sets alternate over a period of 4 stages instead of 2.  Before the first group the other set is zero and its
 //     "scales" are group 0's, so the first flush adds +0.0; the last stage
 //     flushes the last group after its MFMAs.  Every register is
 //     architectural (no AGPR reads in the flush) and nothing spills: a spill
@@ -95,7 +96,7 @@ constexpr int PG_LAUNCH_BN = 64;
 
 template <int BM, int BN, int GS, bool SWH, int WF, int OCC, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const GemmArgs p) {
-  static_assert(GS == 64 || GS == 128, "group size");
+  static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
   using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
   constexpr int NW = C::NW;
   constexpr bool W4 = (WF == W_I4);
@@ -105,18 +106,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   constexpr int PG_WI = C::WI, PG_XI = C::XI, PG_PS = C::PS, PG_W_BYTES = C::W_BYTES;
   constexpr int PG_STAGE = C::STAGE, PG_NS = C::NS, PG_RING = C::RING, PG_SSLOT = C::SSLOT;
   constexpr int PG_SNS = C::SNS, PG_SMEM = C::SMEM, PG_OUT_LD = C::OUT_LD, PG_OUT = C::OUT;
-  constexpr int SUBG = GS / 32;              // k sub-steps per group
-  constexpr int GPS = PG_BK / GS;            // groups per stage
+  constexpr int SUBG = GS / 32;              // k sub-steps per group (a stage has 4)
+  constexpr int SRPS = SUBG < 4 ? 4 / SUBG : 1;  // scale rows a stage brings: its groups
+  // stages per period of the set alternation (group parities compile-time):
+  // 2, or 4 when a group spans two stages (gs 256)
+  constexpr int PER = SUBG < 8 ? 2 : 4;
   constexpr int ESZ = SWH ? 2 : 4;           // scale element bytes
   constexpr int CPR = PG_BN * ESZ / 16;      // 16-byte chunks per scale row
   constexpr int ROWB = PG_BN * ESZ;          // bytes per scale row in LDS
   constexpr int NMF = PG_TN * PG_TM;         // MFMAs per sub-step
   constexpr int NR = PG_TN + PG_TM;          // fragment reads per sub-step
   constexpr int NCOMBO = PG_TN * 4;          // (block a, quad q) scale combos
-  constexpr int CPS = NCOMBO / SUBG;         // combos flushed per sub-step
-  constexpr int EPS = CPS * PG_TM * 4;       // accumulators flushed per sub-step
+  constexpr int NE = PG_TN * PG_TM * 16;     // accumulators of a set, per lane
+  constexpr int EPS = NE / SUBG;             // accumulators flushed per sub-step
   static_assert(EPS % NMF == 0, "flush split");
-  static_assert(CPR * 16 * GPS <= PG_SSLOT && 64 / CPR >= GPS, "scale rows per stage");
+  static_assert(CPR * 16 * SRPS <= PG_SSLOT && 64 / CPR >= SRPS, "scale rows per stage");
   static_assert(NCOMBO % 4 == 0, "whole combos per sub-step");
   __shared__ __attribute__((aligned(1024))) int8_t smem[PG_SMEM];
 
@@ -174,8 +178,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       dma16s(xbase + (int64_t)st * PG_BK, xoff[d >= PG_WI ? d - PG_WI : 0],
              sb + PG_W_BYTES + (wave * PG_XI + d - PG_WI) * 1024);
   };
+  // scale row(s) of stage st: the SRPS groups starting in it (gs 256: the
+  // group it belongs to, also on its second stage, whose slot is not read)
   auto dma_scales = [&](int st) __attribute__((always_inline)) {
-    const int g = min(st * GPS + srow, G - 1);
+    const int g = min(st * 4 / SUBG + srow, G - 1);
     dma16(ssrc + (int64_t)g * N * ESZ, lds0 + PG_RING + (uint32_t)((st % PG_SNS) * PG_SSLOT));
   };
 
@@ -204,13 +210,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   };
 
   // Two int32 group sets alternate by group (set = group parity); while
-  // group g accumulates, group g-1 is flushed, CPF of its scale combos per
-  // sub-step over the SUBG sub-steps of group g.  Before the first group the
-  // other set is zero and its "scales" are group 0's, so that flush adds +0.0.
+  // group g accumulates, group g-1 is flushed, EPS of its accumulators per
+  // sub-step over the SUBG sub-steps of group g (accumulator e of a set:
+  // combo e / EPC, block (e / 4) % TM, element e % 4 of the combo's quad).
+  // Before the first group the other set is zero and its "scales" are group
+  // 0's, so that flush adds +0.0.
   constexpr int EPC = PG_TM * 4;          // accumulators per (a, q) combo
-  constexpr int CPF = NCOMBO / SUBG;      // combos flushed per sub-step
-  constexpr int EPM = CPF * EPC / NMF;    // accumulators flushed after each MFMA
-  static_assert(CPF * SUBG == NCOMBO && (CPF * EPC) % NMF == 0, "flush split");
+  constexpr int CPF = EPS >= EPC ? EPS / EPC : 1;  // combos of one sub-step's flush
+  constexpr int EPM = EPS / NMF;          // accumulators flushed after each MFMA
+  static_assert(EPS % EPC == 0 || EPC % EPS == 0, "flush split");
   i32x16 D[2][PG_TN][PG_TM];
   float facc[PG_TN][PG_TM][16];
 #pragma unroll
@@ -228,7 +236,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   // n = wn*WN + 32a + 8q + 4h + [0..3]
   auto read_scales = [&](int g, int combo, float (&sv)[4]) __attribute__((always_inline)) {
     g = max(g, 0);
-    const int8_t* base = smem + PG_RING + ((g / GPS) % PG_SNS) * PG_SSLOT + (g % GPS) * ROWB;
+    // the row sits in the slot of the stage the group starts in
+    const int8_t* base = smem + PG_RING + ((g * SUBG / 4) % PG_SNS) * PG_SSLOT + (g % SRPS) * ROWB;
     const int nl = wn * PG_WN + (combo / 4) * 32 + 8 * (combo % 4) + 4 * h;
     if constexpr (SWH) {
       const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
@@ -253,7 +262,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   auto read_sub_scales = [&](int g, int slice, float (&dst)[CPF][4])
                              __attribute__((always_inline)) {
 #pragma unroll
-    for (int c = 0; c < CPF; ++c) read_scales(g, slice * CPF + c, dst[c]);
+    for (int c = 0; c < CPF; ++c) read_scales(g, slice * EPS / EPC + c, dst[c]);
   };
 
   // One k sub-step J of the stage in a fixed order (sched_barrier): the
@@ -323,8 +332,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       }
 #pragma unroll
       for (int e = idx * EPM; e < (idx + 1) * EPM; ++e) {
-        const int c = e / EPC, bb = (e / 4) % PG_TM, rr = e % 4;
-        const int combo = SL * CPF + c;
+        const int eg = SL * EPS + e;  // accumulator of the set
+        const int combo = eg / EPC, bb = (eg / 4) % PG_TM, rr = eg % 4;
+        const int c = combo - SL * EPS / EPC;  // combo within the sub-step's scales
         const int aa = combo / 4, r = 4 * (combo % 4) + rr;
         const float t = (float)D[1 - CS][aa][bb][r] * sv[SVDB ? (J & 1) : 0][c][rr];
         facc[aa][bb][r] = facc[aa][bb][r] + t;
@@ -375,11 +385,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   float sa_t = 0.0f;
   uint16_t b_t = 0;
 
-  // Stage kt at position HALF (0 or 1) of a 2-stage period that starts at an
-  // even kt, so group parities are compile-time.  Sub-step J belongs to
-  // group kt*GPS + J/SUBG and flushes slice J % SUBG of the group before it.
-  // LAST: the final stage (no barrier or DMA; requests sa and bias; then
-  // flushes its own last group).
+  // Stage kt at position HALF (0 .. PER-1) of a PER-stage period that starts
+  // at a multiple of PER, so group parities are compile-time.  Sub-step J
+  // belongs to group (4 kt + J) / SUBG and flushes slice (4 HALF + J) % SUBG
+  // of the group before it.  LAST: the final stage (no barrier or DMA;
+  // requests sa and bias; then flushes its own last group).
   auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
     constexpr int HALF = decltype(halfc)::value;
     constexpr bool LAST = decltype(lastc)::value != 0;
@@ -388,26 +398,28 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       sa_t = p.sa[min(m0 + tid % PG_BM, M - 1)];
       if (p.bias) b_t = p.bias[min(n0 + tid % PG_BN, N - 1)];
     }
-    // flushed group of sub-step J of stage k: k*GPS + J/SUBG - 1
+    // group of sub-step J of stage k: (4 k + J) / SUBG; it flushes the one before
 #define PG_SUB(J)                                                                            \
   {                                                                                          \
     constexpr int S = 4 * HALF + (J);                                                        \
     constexpr int CS = (S / SUBG) & 1;                                                       \
     constexpr bool FIRST = (S % SUBG) == 0;                                                  \
     constexpr int SL = S % SUBG;                                                             \
+    const int cg = (4 * kt + (J)) / SUBG - 1;                                                \
+    const int ng = (4 * kt + (J) + 1) / SUBG - 1;                                            \
     if constexpr ((J) < 3) {                                                                 \
       step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[(J) & 1],       \
-           xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0,                      \
-           kt * GPS + ((J) + 1) / SUBG - 1, ((J) + 1) % SUBG, kt * GPS + (J) / SUBG - 1);    \
+           xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, ng, (S + 1) % SUBG,  \
+           cg);                                                                              \
     } else if constexpr (!LAST) {                                                            \
       wait_stage();                                                                          \
       __syncthreads();                                                                       \
       step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1],      \
-           (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, (kt + 1) * GPS - 1,  \
-           0, kt * GPS + (J) / SUBG - 1);                                                    \
+           (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, ng, (S + 1) % SUBG,  \
+           cg);                                                                              \
     } else {                                                                                 \
       step(ic<CS>{}, ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1], 0,    \
-           wf[0], xf[0], 0, 0, 0, 0, kt * GPS + (J) / SUBG - 1);                             \
+           wf[0], xf[0], 0, 0, 0, 0, cg);                                                    \
     }                                                                                        \
   }
     PG_SUB(0)
@@ -436,15 +448,34 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   };
 
   int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    stage(kt, ic<0>{}, ic<0>{});
-    stage(kt + 1, ic<1>{}, ic<0>{});
-  }
-  if (kt + 1 < nk) {
-    stage(kt, ic<0>{}, ic<0>{});
-    stage(kt + 1, ic<1>{}, ic<1>{});
+  if constexpr (PER == 2) {
+    for (; kt + 2 < nk; kt += 2) {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<0>{});
+    }
+    if (kt + 1 < nk) {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<1>{});
+    } else {
+      stage(kt, ic<0>{}, ic<1>{});
+    }
   } else {
-    stage(kt, ic<0>{}, ic<1>{});
+    // gs 256: K % 256 == 0, so nk is even and 2 or 4 stages remain
+    for (; kt + 4 < nk; kt += 4) {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<0>{});
+      stage(kt + 2, ic<2>{}, ic<0>{});
+      stage(kt + 3, ic<3>{}, ic<0>{});
+    }
+    if (kt + 2 < nk) {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<0>{});
+      stage(kt + 2, ic<2>{}, ic<0>{});
+      stage(kt + 3, ic<3>{}, ic<1>{});
+    } else {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<1>{});
+    }
   }
   wait_vmcnt<0>();  // reloads past the end land before LDS is reused
 
@@ -494,9 +525,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   }
 }
 
-// Eligible: int8 or int4 weights, per-group gs 64 / 128, K % 128 == 0,
-// N % 8 == 0, 16-byte aligned operands (launch_gemm checks).
+// Eligible: int8 or int4 weights, per-group gs 64 / 128 (gs 256: int8 and
+// K % 256 == 0), K % 128 == 0, N % 8 == 0, 16-byte aligned operands
+// (launch_gemm checks).
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
+  if (gs == 256) {
+    // int8 weights only (the W4A8 formats define gs 64 / 128); the 8-wave
+    // 128 x 128 tile: 205.6 us at M=4096 N=10240 K=2560 against 225.8 us for
+    // two 128 x 64 workgroups per CU (and 280.1 us on the register-staged
+    // kernel that ran gs 256 before)
+    constexpr int BM = 128, BN = 128;
+    const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    if (sw_half)
+      gemm_dma_pg_kernel<BM, BN, 256, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+    else
+      gemm_dma_pg_kernel<BM, BN, 256, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+    return hipGetLastError();
+  }
   if (gs == 64 && a.M > 64) {
     // 128 x 128 tiles, 8 waves of 64 x 32 (two per SIMD), all registers
     // architectural: 1.65x the rate of the one-wave-per-SIMD 128 x 64 tile

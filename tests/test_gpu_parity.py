@@ -282,13 +282,15 @@ def test_full_size_down_proj_rows():
 
 
 # M > 64 with K % 128 == 0 and N % 8 == 0 runs the LDS-DMA per-group kernel
-# at gs 64 / 128 (one k-stage (K=128), two (K=256), an odd count (K=384),
-# ragged M and N); gs 256 and K=320 run the register-staged kernel.
+# (one k-stage (K=128), two (K=256), an odd count (K=384), ragged M and N;
+# gs 256 groups span two stages and their sets alternate over a 4-stage
+# period: K=256 / 768 / 1280 end it after 2 stages, K=512 / 1024 after 4);
+# K=320 runs the register-staged kernel.
 @pytest.mark.parametrize("gs", [64, 128, 256])
 @pytest.mark.parametrize("M,N,K", [(1, 72, 512), (1, 10240, 2560), (5, 48, 256), (16, 130, 512),
                                    (64, 100, 1024), (65, 96, 512), (300, 520, 1024),
                                    (130, 64, 320), (128, 256, 128), (200, 1024, 256),
-                                   (257, 136, 384)])
+                                   (257, 136, 384), (129, 264, 768), (96, 1032, 1280)])
 def test_pergroup_linear(gs, M, N, K):
     if K % gs:
         pytest.skip("K not a multiple of gs")
@@ -317,7 +319,7 @@ def test_pergroup_mv_shapes(gs, N, K):
     assert_mv_close(y, x, w, sw, b, gs, f"pg mv gs{gs} {N}x{K}")
 
 
-@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("gs", [64, 128, 256])
 @pytest.mark.parametrize("M,N,K", [(1024, 10240, 2560), (512, 2560, 10240)])
 def test_pergroup_full_size_rows(gs, M, N, K):
     x = O.synth_activations(M, K, 50 + gs)
