@@ -414,7 +414,8 @@ def compact_sweep(torch, lib, _lib, args, dev, stream):
 
 def sweep(torch, args, dev):
     """per-channel / per-group gs 128 and 64, M in {1,128,1024,4096,8192},
-    (N,K) in {(10240,2560),(2560,10240)}; configs[2]: W4A8 per-group gs 64 / 128,
+    (N,K) in {(10240,2560),(2560,10240)}, plus per-group gs 256 (a group size
+    the reference's per-group op also takes); configs[2]: W4A8 per-group gs 64 / 128,
     (N,K) in {(12288,4096),(4096,12288)}, M in {1,16,512,4096}.
 
     Each case is the whole linear (per-token quantize + GEMM, or the MV at
@@ -450,7 +451,8 @@ def sweep(torch, args, dev):
         ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev)
               for _ in range(nw)]
         bias = torch.zeros(N, dtype=torch.float16, device=dev)
-        for mode, gs in [("per-channel", 0), ("per-group-128", 128), ("per-group-64", 64)]:
+        for mode, gs in [("per-channel", 0), ("per-group-128", 128), ("per-group-64", 64),
+                         ("per-group-256", 256)]:
             sw = ((torch.rand(N, generator=g) * 9e-3 + 1e-3) if gs == 0 else
                   (torch.rand(K // gs, N, generator=g) * 9e-3 + 1e-3)).to(dev)
             sbytes = 4 * N if gs == 0 else 4 * N * (K // gs)
