@@ -400,6 +400,7 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // (N=12288 K=4096 M=16: 13.3 us DMA vs 16.0 us stream).
     if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
       return launch_skinny_stream(a, wf, epi, gs, s);
+    if (a.M <= 16 && skinny_dma_supported(a, wf, epi)) return launch_skinny_dma(a, epi, s);
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
     if (dma_pg && gs != 256 && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
       return launch_gemm_dma_pg(a, gs, sw_half, wf, s);

@@ -434,6 +434,29 @@ def test_gemv_q_exact(M, N, K):
                           O.w4a8_pergroup_linear(x, pk, sc, gs, b), f"gemv w4g{gs} {M}x{N}x{K}")
 
 
+# M <= 16 with int8 weights, per-channel or int32, K % 512 == 0 and K >= 1536:
+# the weight stream through LDS (skinny_dma.hip).  Covered: 8 and 16
+# activation slots (M <= 8 re-reads rows for the MFMA's columns past 8), one to
+# four blocks of 16 rows per workgroup, N past the last block (1000, 8196,
+# 4100), the fewest stages the ring takes (K = 1536: 3 stages of 512), long K
+# (12288: 24 stages), and a grid of more than one round (N = 20480, 4 blocks
+# per workgroup: 320 workgroups).
+@pytest.mark.parametrize("M,N,K", [(5, 1000, 1536), (8, 2560, 10240), (9, 8196, 2048),
+                                   (12, 4100, 12288), (16, 20480, 2560), (16, 10240, 2560),
+                                   (13, 12288, 4096), (6, 4096, 2048), (16, 64, 1536)])
+def test_skinny_dma_exact(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 140 + M)
+    for bias in (b, None):
+        y = H(C.perchannel_linear(T(x), T(w), T(sw), None if bias is None else T(bias)))
+        assert_bits_equal(y, O.perchannel_linear(x, w, sw, bias), f"skinny dma pc {M}x{N}x{K}")
+    q = np.random.default_rng(141).integers(-128, 128, (M, K), dtype=np.int8)
+    q[0, :] = -128  # the extremes: -128 * -127 summed over K
+    w2 = w.copy()
+    w2[: min(N, 5), :] = -127
+    c = C.int8_matmul_int32(T(q), T(w2)).cpu().numpy()
+    assert np.array_equal(c, O.int8_matmul_int32(q, w2)), f"skinny dma i32 {M}x{N}x{K}"
+
+
 # Skinny kernel (M <= 64) at shapes where N alone gives few workgroups, so the
 # K range is split over 8 or 16 waves per workgroup (int32 sums exact in any
 # order); per-group deals the groups to the waves round-robin and keeps the
@@ -455,9 +478,9 @@ def test_skinny_wave_splits_exact(M, N, K):
 
 
 # 5 <= M <= 64 with at least 128 column tiles of 64 (or M > 48) runs the
-# LDS-DMA kernel's 64 x 64 tiles (per-channel, int32, int4 weights) instead of
-# the skinny kernel: rows past M are loaded from the last valid row and never
-# stored.  Per-group at >= 128 column tiles runs the 128-row per-group DMA
+# LDS-DMA kernel's 64 x 64 tiles (int4 weights; per-channel and int32 at
+# M > 16 or K not a multiple of 512) instead of the skinny kernel: rows past M
+# are loaded from the last valid row and never stored.  Per-group at >= 128 column tiles runs the 128-row per-group DMA
 # tiles for M > 32, and for int8 weights at gs 128 at every M: (16, 10240,
 # 2560) and (5, 12288, 512) int8 gs 128; (33, 8192, 1024) and (64, 8192, 512)
 # every per-group variant; the others stay on the skinny kernel ((64, 512, 4096)
