@@ -392,15 +392,24 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // and for int8 weights at gs 128 from the smallest M (N=10240 K=2560 M=8:
     // 16.8 vs 14.2 us).  Below that the skinny kernel keeps int4 and gs 64
     // (N=12288 K=4096 M=16, int4 gs 128: 16.2 vs 25.7 us).
-    // M <= 16, per-group or int4 weights: the weight-stream kernel
-    // (skinny_stream.hip), which beat the skinny and per-group DMA kernels
-    // at every such shape measured (N=12288 K=4096 M=16, int4 gs 128: 13.4
-    // vs 17.2 us; int4 per-channel: 11.5 vs 16.4 us; int8 gs 64: 18.3 vs
-    // 20.5 us).  int8 per-channel keeps the DMA tiles and the skinny kernel
-    // (N=12288 K=4096 M=16: 13.3 us DMA vs 16.0 us stream).
+    // M <= 16 with K % 512 == 0 (K >= 1536): the weight stream through LDS
+    // (skinny_dma.hip), whole linears against the kernels below: int8
+    // per-channel M=16 N=2560 K=10240 13.1 vs 19.0 us (64 x 64 DMA tiles);
+    // int8 gs 128 N=10240 K=2560 11.3 vs 18.1 us and int4 gs 64 N=12288
+    // K=4096 16.4 vs 20.6 us (register weight stream).  int4 weights that the
+    // register stream loads in pairs of k-steps (per-channel, gs >= 128) stay
+    // there at 3 blocks of 16 rows per workgroup (N >= 11520), where its
+    // 16-byte loads and the LDS stream's short int4 rows per stage trade the
+    // other way (gs 128 M=16 N=12288 K=4096: 12.7 vs 13.9 us).
+    // Other M <= 16 per-group or int4 shapes: the register weight stream
+    // (skinny_stream.hip), ahead of the skinny and per-group DMA kernels
+    // (N=12288 K=4096 M=16, int4 gs 128: 13.4 vs 17.2 us; int4 per-channel:
+    // 11.5 vs 16.4 us; int8 gs 64: 18.3 vs 20.5 us).
+    const bool w4_pairs = wf == W_I4 && (epi != EPI_PG || gs >= 128) && a.N >= 48 * 240;
+    if (a.M <= 16 && !w4_pairs && skinny_dma_supported(a, wf, epi, sw_half, gs))
+      return launch_skinny_dma(a, wf, epi, gs, s);
     if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
       return launch_skinny_stream(a, wf, epi, gs, s);
-    if (a.M <= 16 && skinny_dma_supported(a, wf, epi)) return launch_skinny_dma(a, epi, s);
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
     if (dma_pg && gs != 256 && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
       return launch_gemm_dma_pg(a, gs, sw_half, wf, s);

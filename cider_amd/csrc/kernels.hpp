@@ -33,10 +33,10 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
 // K % 64 == 0, K <= 16384, N % 4 == 0, aligned operands.
 bool skinny_stream_supported(const GemmArgs& a, int wf, int epi, int gs);
 hipError_t launch_skinny_stream(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s);
-// Small-M int8-weight GEMM through LDS (skinny_dma.hip): 1 <= M <= 16,
-// per-channel or int32, K % 512 == 0 and K >= 1536, N % 4 == 0, aligned.
-bool skinny_dma_supported(const GemmArgs& a, int wf, int epi);
-hipError_t launch_skinny_dma(const GemmArgs& a, int epi, hipStream_t s);
+// Small-M GEMM as a weight stream through LDS (skinny_dma.hip): 1 <= M <= 16,
+// K % 512 == 0 and K >= 1536, N % 4 == 0 (per-group N % 8 == 0), aligned.
+bool skinny_dma_supported(const GemmArgs& a, int wf, int epi, bool sw_half, int gs);
+hipError_t launch_skinny_dma(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s);
 // The earlier small-M kernel (skinny.hip), for shapes the stream kernel does
 // not take.
 hipError_t launch_skinny(const GemmArgs& a, int wf, int epi, bool sw_half, int gs,

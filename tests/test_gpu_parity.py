@@ -434,13 +434,15 @@ def test_gemv_q_exact(M, N, K):
                           O.w4a8_pergroup_linear(x, pk, sc, gs, b), f"gemv w4g{gs} {M}x{N}x{K}")
 
 
-# M <= 16 with int8 weights, per-channel or int32, K % 512 == 0 and K >= 1536:
-# the weight stream through LDS (skinny_dma.hip).  Covered: 8 and 16
-# activation slots (M <= 8 re-reads rows for the MFMA's columns past 8), one to
-# four blocks of 16 rows per workgroup, N past the last block (1000, 8196,
-# 4100), the fewest stages the ring takes (K = 1536: 3 stages of 512), long K
-# (12288: 24 stages), and a grid of more than one round (N = 20480, 4 blocks
-# per workgroup: 320 workgroups).
+# M <= 16 with K % 512 == 0 and K >= 1536: the weight stream through LDS
+# (skinny_dma.hip) for every format.  Covered: 8 and 16 activation slots
+# (M <= 8 re-reads rows for the MFMA's columns past 8), one to four blocks of
+# 16 rows per workgroup, N past the last block (1000, 8196, 4100; per-group
+# needs N % 8 == 0, so 8196 and 4100 take the other kernels there), the fewest
+# stages the ring takes (K = 1536: 3 stages of 512), long K (12288: 24
+# stages), a grid of more than one round (N = 20480, 4 blocks per workgroup:
+# 320 workgroups), and per-group chains over 8 / 4 / 2 groups per stage (gs
+# 64 / 128 / 256, the last summing two waves' halves of a group).
 @pytest.mark.parametrize("M,N,K", [(5, 1000, 1536), (8, 2560, 10240), (9, 8196, 2048),
                                    (12, 4100, 12288), (16, 20480, 2560), (16, 10240, 2560),
                                    (13, 12288, 4096), (6, 4096, 2048), (16, 64, 1536)])
@@ -455,6 +457,23 @@ def test_skinny_dma_exact(M, N, K):
     w2[: min(N, 5), :] = -127
     c = C.int8_matmul_int32(T(q), T(w2)).cpu().numpy()
     assert np.array_equal(c, O.int8_matmul_int32(q, w2)), f"skinny dma i32 {M}x{N}x{K}"
+    for gs in (64, 128, 256):
+        swg = O.synth_scales((K // gs, N), 142 + gs)
+        y = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
+        assert_bits_equal(y, O.pergroup_linear(x, w, swg, gs, b), f"skinny dma pg{gs} {M}x{N}x{K}")
+    w4 = np.random.default_rng(143).integers(-8, 8, (N, K), dtype=np.int8)
+    w4[0, :] = -8
+    pk = O.pack_w4_lo_first(w4)
+    for gs in (64, 128):
+        sc = O.synth_scales((K // gs, N), 144 + gs).astype(np.float16)
+        for bias in (b, None):
+            y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, None if bias is None else T(bias)))
+            assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, bias),
+                              f"skinny dma w4g{gs} {M}x{N}x{K}")
+    wf = np.random.default_rng(145).standard_normal((K, N)).astype(np.float32)
+    packed, sw4 = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"skinny dma w4 {M}x{N}x{K}")
 
 
 # Skinny kernel (M <= 64) at shapes where N alone gives few workgroups, so the
