@@ -21,10 +21,26 @@ __device__ __forceinline__ float row_scale(float amax) {
   return s == 0.0f ? 1.0f : s;
 }
 
+// q of one element x (an fp16 value widened to binary32):
+//   * r = x * inv rounded to binary32, as a fused multiply-add with +0: the
+//     exact product rounded once, as the multiply rounds it (the two differ
+//     only in the sign of a zero product, which q does not see), and the
+//     fp16 -> fp32 widening folds into v_fma_mix_f32;
+//   * clamped to [-128, 127] first (fmax(NaN, -128) = -128): rounding and
+//     clamping commute here, since the bounds are integers;
+//   * rounded half away from zero as the truncation of r + copysign(0.5 -
+//     2^-25, r): adding the largest float below 0.5 carries r past the next
+//     integer exactly when its fraction is >= 0.5 (checked against roundf for
+//     every binary32 value), and the conversion to int truncates.
+__device__ __forceinline__ int32_t quant1i(float xv, float inv) {
+  float r = __builtin_fmaf(xv, inv, 0.0f);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  r = r + __builtin_copysignf(0x1.fffffep-2f, r);
+  return (int32_t)r;
+}
+
 __device__ __forceinline__ int8_t quant1(float xv, float inv) {
-  float r = __builtin_roundf(xv * inv);  // half away from zero
-  r = fminf(fmaxf(r, -128.0f), 127.0f);  // fmax(NaN, -128) = -128
-  return (int8_t)(int)r;
+  return (int8_t)quant1i(xv, inv);
 }
 
 __device__ __forceinline__ float absmax8(i32x4 v, float m) {
@@ -42,8 +58,8 @@ __device__ __forceinline__ i32x2 quant8(i32x4 v, float inv) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t w = (uint32_t)v[j];
-    const uint32_t a = (uint8_t)quant1(h2f((uint16_t)(w & 0xffffu)), inv);
-    const uint32_t b = (uint8_t)quant1(h2f((uint16_t)(w >> 16)), inv);
+    const uint32_t a = (uint32_t)quant1i(h2f((uint16_t)(w & 0xffffu)), inv) & 0xffu;
+    const uint32_t b = (uint32_t)quant1i(h2f((uint16_t)(w >> 16)), inv) & 0xffu;
     const uint32_t pair = a | (b << 8);
     if (j & 1)
       out[j >> 1] |= pair << 16;
