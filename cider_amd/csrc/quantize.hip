@@ -9,9 +9,10 @@
 // MI355X design: one 64-lane wavefront owns one row, so the absmax is a pure
 // cross-lane reduction (no LDS, no barrier); a workgroup of 4 waves handles 4
 // rows.  Up to 64 rows (decode-sized batches) get a 1024-thread workgroup per
-// row instead.  Rows of up to 64*8*32 = 16384 elements stay in registers between the
-// absmax and the quantize pass (each element is read from HBM once); longer
-// rows are re-read, which hits in L2.
+// row instead, and rows longer than 4096 (up to 16384) a 256-thread one at
+// any M.  A row stays in registers between the absmax and the quantize pass
+// (each element is read from HBM once); rows past 16384 elements are re-read,
+// which hits in L2.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "quant_common.hpp"
@@ -59,15 +60,17 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(
   }
 }
 
-// Few rows (M <= 64): one 1024-thread workgroup per row, so sixteen waves
-// share a row's loads and conversions (a single wave per row leaves the
-// row's VALU work serial: about 8 us at K = 12288); the absmax goes through
-// LDS in wave order.  Vectorized rows only; NV 16-byte vectors per thread.
-template <int NV>
-__global__ __launch_bounds__(1024) void quantize_row_kernel(
+// A workgroup of NT threads per row: few rows (M <= 64, NT = 1024: sixteen
+// waves share a row's loads and conversions, where a single wave per row
+// leaves the row's VALU work serial: about 8 us at K = 12288) and long rows
+// (NT = 256); the absmax goes through LDS in wave order.  Vectorized rows
+// only; NV 16-byte vectors per thread.
+template <int NV, int NT = 1024>
+__global__ __launch_bounds__(NT) void quantize_row_kernel(
     const uint16_t* __restrict__ x, int8_t* __restrict__ q,
     float* __restrict__ sa, int K) {
-  __shared__ float red[16];
+  constexpr int NWV = NT / 64;
+  __shared__ float red[NWV];
   const int tid = threadIdx.x;
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * K;
@@ -77,7 +80,7 @@ __global__ __launch_bounds__(1024) void quantize_row_kernel(
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int e = tid + i * 1024;
+    const int e = tid + i * NT;
     v[i] = e < nvec ? ld16(xr + 8 * e) : i32x4{0, 0, 0, 0};
     amax = absmax8(v[i], amax);
   }
@@ -86,13 +89,13 @@ __global__ __launch_bounds__(1024) void quantize_row_kernel(
   __syncthreads();
   amax = red[0];
 #pragma unroll
-  for (int w = 1; w < 16; ++w) amax = fmaxf(amax, red[w]);
+  for (int w = 1; w < NWV; ++w) amax = fmaxf(amax, red[w]);
   const float s = row_scale(amax);
   const float inv = 1.0f / s;
   if (tid == 0) sa[row] = s;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int e = tid + i * 1024;
+    const int e = tid + i * NT;
     if (e < nvec) *reinterpret_cast<i32x2*>(qr + 8 * e) = quant8(v[i], inv);
   }
 }
@@ -139,6 +142,19 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
     return hipGetLastError();
   }
   const int per_lane = (nvec + kWave - 1) / kWave;
+  if (nvec > 512 && nvec <= 8 * 256) {
+    // Long rows (K > 4096) at any M: a 256-thread workgroup per row, its
+    // four waves' maxima meeting in LDS.  One wave per row held up to 32
+    // 16-byte vectors per lane and ran at few waves per SIMD (4096 x 10240:
+    // 35.0 us; here 21.2 us).
+    const int nv = (nvec + 255) / 256;
+    if (nv <= 3) quantize_row_kernel<3, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    else if (nv <= 4) quantize_row_kernel<4, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    else if (nv <= 5) quantize_row_kernel<5, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    else if (nv <= 6) quantize_row_kernel<6, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    else quantize_row_kernel<8, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    return hipGetLastError();
+  }
   if (per_lane <= 1)
     quantize_vec_kernel<1><<<grid, block, 0, s>>>(x, q, sa, M, K);
   else if (per_lane <= 2)
