@@ -9,8 +9,8 @@
 // MI355X design: one 64-lane wavefront owns one row, so the absmax is a pure
 // cross-lane reduction (no LDS, no barrier); a workgroup of 4 waves handles 4
 // rows.  Up to 64 rows (decode-sized batches) get a 1024-thread workgroup per
-// row instead, and rows longer than 4096 (up to 16384) a 256-thread one at
-// any M.  A row stays in registers between the absmax and the quantize pass
+// row instead, and rows of 2048 to 16384 elements a 256-thread one at any
+// M.  A row stays in registers between the absmax and the quantize pass
 // (each element is read from HBM once); rows past 16384 elements are re-read,
 // which hits in L2.
 #include "common.hpp"
@@ -142,13 +142,14 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
     return hipGetLastError();
   }
   const int per_lane = (nvec + kWave - 1) / kWave;
-  if (nvec > 512 && nvec <= 8 * 256) {
-    // Long rows (K > 4096) at any M: a 256-thread workgroup per row, its
-    // four waves' maxima meeting in LDS.  One wave per row held up to 32
-    // 16-byte vectors per lane and ran at few waves per SIMD (4096 x 10240:
-    // 35.0 us; here 21.2 us).
+  if (nvec >= 256 && nvec <= 8 * 256) {
+    // Rows of 2048 .. 16384 elements at any M: a 256-thread workgroup per
+    // row, its four waves' maxima meeting in LDS.  One wave per row held up
+    // to 32 16-byte vectors per lane and ran at few waves per SIMD (4096 x
+    // 10240: 36.3 -> 21.7 us; 4096 x 4096: 10.8 -> 9.7 us).
     const int nv = (nvec + 255) / 256;
-    if (nv <= 3) quantize_row_kernel<3, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    if (nv <= 2) quantize_row_kernel<2, 256><<<M, 256, 0, s>>>(x, q, sa, K);
+    else if (nv <= 3) quantize_row_kernel<3, 256><<<M, 256, 0, s>>>(x, q, sa, K);
     else if (nv <= 4) quantize_row_kernel<4, 256><<<M, 256, 0, s>>>(x, q, sa, K);
     else if (nv <= 5) quantize_row_kernel<5, 256><<<M, 256, 0, s>>>(x, q, sa, K);
     else if (nv <= 6) quantize_row_kernel<6, 256><<<M, 256, 0, s>>>(x, q, sa, K);
