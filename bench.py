@@ -335,7 +335,8 @@ def compact_sweep(torch, lib, _lib, args, dev, stream):
     """The cases of the configs[1] / configs[2] sweep that the headline line
     does not cover, timed as in sweep(): per-group gs 128 / 64 at M=4096, the
     M=1 MV on the down-projection shape, W4A8 per-group gs 128 at M=4096 and
-    M=16 (the decode-batch path), per-channel at M=16 and M=8192."""
+    M=16 (the decode-batch path), per-channel at M=16 and M=8192, and the
+    M=16 per-group cases of the LDS weight stream (int8 gs 128, W4A8 gs 64)."""
     vp = ctypes.c_void_p
 
     def cur():
@@ -408,6 +409,8 @@ def compact_sweep(torch, lib, _lib, args, dev, stream):
     w8_case(8192, 10240, 2560, 0)
     w4_case(4096, 12288, 4096, 128)
     w4_case(16, 12288, 4096, 128)
+    w8_case(16, 10240, 2560, 128)
+    w4_case(16, 12288, 4096, 64)
     torch.cuda.synchronize()
     return recs
 
