@@ -395,18 +395,13 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // M <= 16 with K % 512 == 0 (K >= 1536): the weight stream through LDS
     // (skinny_dma.hip), whole linears against the kernels below: int8
     // per-channel M=16 N=2560 K=10240 13.1 vs 19.0 us (64 x 64 DMA tiles);
-    // int8 gs 128 N=10240 K=2560 11.3 vs 18.1 us and int4 gs 64 N=12288
-    // K=4096 16.4 vs 20.6 us (register weight stream).  int4 weights that the
-    // register stream loads in pairs of k-steps (per-channel, gs >= 128) stay
-    // there at 3 blocks of 16 rows per workgroup (N >= 11520), where its
-    // 16-byte loads and the LDS stream's short int4 rows per stage trade the
-    // other way (gs 128 M=16 N=12288 K=4096: 12.7 vs 13.9 us).
+    // int8 gs 64 N=10240 K=2560 11.2 vs 20.0 us, int4 gs 64 N=12288 K=4096
+    // 14.2 vs 20.6 us and int4 gs 128 12.2 vs 12.5 us (register stream).
     // Other M <= 16 per-group or int4 shapes: the register weight stream
     // (skinny_stream.hip), ahead of the skinny and per-group DMA kernels
     // (N=12288 K=4096 M=16, int4 gs 128: 13.4 vs 17.2 us; int4 per-channel:
     // 11.5 vs 16.4 us; int8 gs 64: 18.3 vs 20.5 us).
-    const bool w4_pairs = wf == W_I4 && (epi != EPI_PG || gs >= 128) && a.N >= 48 * 240;
-    if (a.M <= 16 && !w4_pairs && skinny_dma_supported(a, wf, epi, sw_half, gs))
+    if (a.M <= 16 && skinny_dma_supported(a, wf, epi, sw_half, gs))
       return launch_skinny_dma(a, wf, epi, gs, s);
     if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
       return launch_skinny_stream(a, wf, epi, gs, s);

@@ -35,6 +35,11 @@
 //     at gs 128, and half a group at gs 256) to LDS; after a barrier the owner
 //     of each output adds the halves (int32, exact), and chains
 //     acc = acc + f32(f32(D_g) * sw[g, n]) over the stage's groups in order.
+//     The owners are four more waves that only chain: while the MFMA waves
+//     compute stage st into one parts buffer (and copy its scale block
+//     beside it), the chain waves add up stage st - 1 from the other, so the
+//     chain (1-4.4 us per call when the MFMA waves ran it between stages)
+//     overlaps the stream; one barrier per stage orders both buffers.
 #include "common.hpp"
 #include "dma_common.hpp"
 #include "kernels.hpp"
@@ -63,8 +68,10 @@ struct SdCfg {
   static constexpr int RING = NS * STAGE;
   static constexpr int PARTS = PG ? (GS == 64 ? 8 : 4) : 0;    // int32 sums per stage
   static constexpr int TERMS = PARTS * ROWS * 16 * 4;
+  // per-group: two buffers of a stage's parts and of its scale block
+  static constexpr int CHAIN = PG ? 2 * (TERMS + NSI * 1024) : 0;
   static constexpr int RED = kSdKW * RB * 64 * 16;             // partial tiles (PC / I32)
-  static constexpr int SMEM = (RING + TERMS) > RED ? (RING + TERMS) : RED;
+  static constexpr int SMEM = (RING + CHAIN) > RED ? (RING + CHAIN) : RED;
   static_assert(NWI % kSdKW == 0 && NXI % kSdKW == 0, "whole DMA instructions per wave");
   static_assert(CPRW >= 16 && NSI <= kSdKW, "swizzle range; one scale instruction per wave");
   static_assert(RB <= kSdKW, "one wave per block in the epilogue");
@@ -90,7 +97,8 @@ __device__ __forceinline__ void wait_stage(int rem) {
 }  // namespace
 
 template <int RB, int MB, int NS, int WF, int EPI, int GS, bool SWH>
-__global__ __launch_bounds__(kSdKW * 64) void skinny_dma_kernel(const GemmArgs p) {
+__global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_dma_kernel(
+    const GemmArgs p) {
   using C = SdCfg<RB, MB, NS, WF, EPI, GS, SWH>;
   constexpr bool PG = C::PG;
   constexpr int PW = C::PW, CPRW = C::CPRW, CPRX = C::CPRX, WB = C::WB;
@@ -181,9 +189,11 @@ __global__ __launch_bounds__(kSdKW * 64) void skinny_dma_kernel(const GemmArgs p
     return *reinterpret_cast<const i32x4*>(slot + C::WS + xr * kSdBK + 16 * ((4 * t + lq) ^ xr));
   };
 
+  // per-group workgroups have four more waves, which only run the chain
+  const bool mma = wave < kSdKW;
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
-    if (st < nst) issue(st);
+    if (mma && st < nst) issue(st);
 
   if constexpr (!PG) {
     i32x4 acc[RB];
@@ -239,50 +249,29 @@ __global__ __launch_bounds__(kSdKW * 64) void skinny_dma_kernel(const GemmArgs p
     //   gs 64: part 2 w + j = k-step 2 w + j = group 2 w + j
     //   gs 128: part w = group w;  gs 256: parts 2 g and 2 g + 1 = group g
     constexpr int NOUT = C::ROWS * 16;
-    constexpr int OWN = NOUT / (kSdKW * 64);  // outputs per thread (RB)
-    int32_t* parts = reinterpret_cast<int32_t*>(smem + C::RING);
+    constexpr int NCH = kSdKW * 64;                 // chain threads (waves 4 .. 7)
+    constexpr int OWN = NOUT / NCH;                 // outputs per chain thread (RB)
+    constexpr int SB = C::NSI * 1024;               // scale block bytes
+    auto parts = [&](int b) { return reinterpret_cast<int32_t*>(smem + C::RING + b * C::TERMS); };
+    auto sbuf = [&](int b) { return smem + C::RING + 2 * C::TERMS + b * SB; };
+    const int ct = tid - NCH;                       // chain thread index (chain waves)
     float facc[OWN];
 #pragma unroll
     for (int o = 0; o < OWN; ++o) facc[o] = 0.0f;
-    for (int st = 0; st < nst; ++st) {
-      wait(min(NS - 2, nst - 1 - st));
-      __syncthreads();  // stage st landed; slot st-1 and the parts are free
-      if (st + NS - 1 < nst) issue(st + NS - 1);
-      const int8_t* slot = smem + (st % NS) * C::STAGE;
-      i32x4 d[2][RB];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int t = 2 * wave + j;
-        const i32x4 b = operand_x(slot, t);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-          d[j][rb] = mfma_i8(operand_w(slot, rb, t), b,
-                             (GS == 64 || j == 0) ? i32x4{0, 0, 0, 0} : d[0][rb]);
-      }
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        if constexpr (GS == 64) {
-          *reinterpret_cast<i32x4*>(parts + ((2 * wave) * NOUT) + (rb * 64 + lane) * 4) = d[0][rb];
-          *reinterpret_cast<i32x4*>(parts + ((2 * wave + 1) * NOUT) + (rb * 64 + lane) * 4) = d[1][rb];
-        } else {
-          *reinterpret_cast<i32x4*>(parts + (wave * NOUT) + (rb * 64 + lane) * 4) = d[1][rb];
-        }
-      }
-      __syncthreads();
-      // the chain: output o adds the stage's groups in order
-      const int8_t* sc = slot + C::WS + C::XS;
+    // chain of one stage: output idx adds the stage's groups in order
+    auto chain = [&](const int32_t* pt, const int8_t* sc) {
 #pragma unroll
       for (int o = 0; o < OWN; ++o) {
-        const int idx = tid + o * kSdKW * 64;
+        const int idx = ct + o * NCH;
         const int l = (idx >> 2) & 63;
         const int nl = 16 * (idx >> 8) + 4 * (l >> 4) + (idx & 3);  // column - n0
 #pragma unroll
         for (int g = 0; g < C::GPS; ++g) {
           int32_t dg;
           if constexpr (GS == 256)
-            dg = parts[(2 * g) * NOUT + idx] + parts[(2 * g + 1) * NOUT + idx];
+            dg = pt[(2 * g) * NOUT + idx] + pt[(2 * g + 1) * NOUT + idx];
           else
-            dg = parts[g * NOUT + idx];
+            dg = pt[g * NOUT + idx];
           float s;
           if constexpr (SWH)
             s = h2f(reinterpret_cast<const uint16_t*>(sc)[g * C::ROWS + nl]);
@@ -291,12 +280,53 @@ __global__ __launch_bounds__(kSdKW * 64) void skinny_dma_kernel(const GemmArgs p
           facc[o] = facc[o] + (float)dg * s;
         }
       }
+    };
+    for (int st = 0; st < nst; ++st) {
+      if (mma) wait(min(NS - 2, nst - 1 - st));
+      // stage st landed; slot st-1 is free; the parts and scales of stage st-1
+      // are written, and the chain of stage st-2 has read its buffers
+      __syncthreads();
+      if (mma) {
+        if (st + NS - 1 < nst) issue(st + NS - 1);
+        const int8_t* slot = smem + (st % NS) * C::STAGE;
+        int32_t* pt = parts(st & 1);
+        i32x4 d[2][RB];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int t = 2 * wave + j;
+          const i32x4 b = operand_x(slot, t);
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+            d[j][rb] = mfma_i8(operand_w(slot, rb, t), b,
+                               (GS == 64 || j == 0) ? i32x4{0, 0, 0, 0} : d[0][rb]);
+        }
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          if constexpr (GS == 64) {
+            *reinterpret_cast<i32x4*>(pt + ((2 * wave) * NOUT) + (rb * 64 + lane) * 4) = d[0][rb];
+            *reinterpret_cast<i32x4*>(pt + ((2 * wave + 1) * NOUT) + (rb * 64 + lane) * 4) =
+                d[1][rb];
+          } else {
+            *reinterpret_cast<i32x4*>(pt + (wave * NOUT) + (rb * 64 + lane) * 4) = d[1][rb];
+          }
+        }
+        // the scale block of the stage, for the chain of the next iteration
+        // (the slot is reloaded before then); wave w copied-in kilobyte w
+        if (sdma)
+          *reinterpret_cast<i32x4*>(sbuf(st & 1) + wave * 1024 + lane * 16) =
+              *reinterpret_cast<const i32x4*>(slot + C::WS + C::XS + wave * 1024 + lane * 16);
+      } else if (st > 0) {
+        chain(parts((st - 1) & 1), sbuf((st - 1) & 1));
+      }
     }
+    __syncthreads();
+    if (mma) return;
+    chain(parts((nst - 1) & 1), sbuf((nst - 1) & 1));
     // output idx = (rb, lane, r): weight row n0 + 16 rb + 4 (lane / 16) + r,
     // activation row lane % 16
 #pragma unroll
     for (int o = 0; o < OWN; ++o) {
-      const int idx = tid + o * kSdKW * 64;
+      const int idx = ct + o * NCH;
       const int l = (idx >> 2) & 63;
       const int n = n0 + 16 * (idx >> 8) + 4 * (l >> 4) + (idx & 3), m = l & 15;
       if (m >= M || n >= N) continue;
@@ -313,18 +343,18 @@ template <int RB, int MB, int WF, int EPI, int GS, bool SWH, int NS>
 hipError_t run_sd_ns(const GemmArgs& a, hipStream_t s) {
   const int rows = 16 * RB;
   skinny_dma_kernel<RB, MB, NS, WF, EPI, GS, SWH>
-      <<<(a.N + rows - 1) / rows, kSdKW * 64, 0, s>>>(a);
+      <<<(a.N + rows - 1) / rows, (EPI == EPI_PG ? 2 : 1) * kSdKW * 64, 0, s>>>(a);
   return hipGetLastError();
 }
 
-// Ring slots: 4, or as many as the LDS holds beside the per-group parts.
+// Ring slots: 4, or as many as the LDS holds beside the per-group buffers.
 // Deeper rings measured slower (int4 gs 128 M=16 N=12288 K=4096: 7 slots
 // 15.2 us against 13.9 us with 4; N=2560 K=10240 gs 128: 8 slots 15.3 us
 // against 13.8 us).
 template <int RB, int MB, int WF, int EPI, int GS, bool SWH>
 constexpr int sd_slots() {
   using C2 = SdCfg<RB, MB, 2, WF, EPI, GS, SWH>;
-  const int ns = (kLdsBytes - C2::TERMS) / C2::STAGE;
+  const int ns = (kLdsBytes - C2::CHAIN) / C2::STAGE;
   return ns > 4 ? 4 : ns;
 }
 
