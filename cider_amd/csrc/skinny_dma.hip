@@ -35,7 +35,7 @@
 //     at gs 128, and half a group at gs 256) to LDS; after a barrier the owner
 //     of each output adds the halves (int32, exact), and chains
 //     acc = acc + f32(f32(D_g) * sw[g, n]) over the stage's groups in order.
-//     The owners are four more waves that only chain: while the MFMA waves
+//     The owners are eight more waves that only chain: while the MFMA waves
 //     compute stage st into one parts buffer (and copy its scale block
 //     beside it), the chain waves add up stage st - 1 from the other, so the
 //     chain (1-4.4 us per call when the MFMA waves ran it between stages)
@@ -49,7 +49,8 @@ namespace cider {
 namespace {
 
 constexpr int kSdBK = 512;  // k per stage
-constexpr int kSdKW = 4;    // waves per workgroup (two 64-wide k-steps each per stage)
+constexpr int kSdKW = 4;    // MFMA waves per workgroup (two 64-wide k-steps each per stage)
+constexpr int kSdCW = 8;    // per-group: chain waves beside them
 
 template <int RB, int MB, int NS, int WF, int EPI, int GS, bool SWH>
 struct SdCfg {
@@ -97,7 +98,7 @@ __device__ __forceinline__ void wait_stage(int rem) {
 }  // namespace
 
 template <int RB, int MB, int NS, int WF, int EPI, int GS, bool SWH>
-__global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_dma_kernel(
+__global__ __launch_bounds__((EPI == EPI_PG ? kSdKW + kSdCW : kSdKW) * 64) void skinny_dma_kernel(
     const GemmArgs p) {
   using C = SdCfg<RB, MB, NS, WF, EPI, GS, SWH>;
   constexpr bool PG = C::PG;
@@ -189,7 +190,7 @@ __global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_d
     return *reinterpret_cast<const i32x4*>(slot + C::WS + xr * kSdBK + 16 * ((4 * t + lq) ^ xr));
   };
 
-  // per-group workgroups have four more waves, which only run the chain
+  // per-group workgroups have eight more waves, which only run the chain
   const bool mma = wave < kSdKW;
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
@@ -249,12 +250,12 @@ __global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_d
     //   gs 64: part 2 w + j = k-step 2 w + j = group 2 w + j
     //   gs 128: part w = group w;  gs 256: parts 2 g and 2 g + 1 = group g
     constexpr int NOUT = C::ROWS * 16;
-    constexpr int NCH = kSdKW * 64;                 // chain threads (waves 4 .. 7)
-    constexpr int OWN = NOUT / NCH;                 // outputs per chain thread (RB)
+    constexpr int NCH = kSdCW * 64;                 // chain threads (waves 4 .. 11)
+    constexpr int OWN = (NOUT + NCH - 1) / NCH;     // outputs per chain thread (RB)
     constexpr int SB = C::NSI * 1024;               // scale block bytes
     auto parts = [&](int b) { return reinterpret_cast<int32_t*>(smem + C::RING + b * C::TERMS); };
     auto sbuf = [&](int b) { return smem + C::RING + 2 * C::TERMS + b * SB; };
-    const int ct = tid - NCH;                       // chain thread index (chain waves)
+    const int ct = tid - kSdKW * 64;                // chain thread index (chain waves)
     float facc[OWN];
 #pragma unroll
     for (int o = 0; o < OWN; ++o) facc[o] = 0.0f;
@@ -263,6 +264,7 @@ __global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_d
 #pragma unroll
       for (int o = 0; o < OWN; ++o) {
         const int idx = ct + o * NCH;
+        if (NOUT % NCH != 0 && idx >= NOUT) continue;
         const int l = (idx >> 2) & 63;
         const int nl = 16 * (idx >> 8) + 4 * (l >> 4) + (idx & 3);  // column - n0
 #pragma unroll
@@ -327,6 +329,7 @@ __global__ __launch_bounds__((EPI == EPI_PG ? 2 : 1) * kSdKW * 64) void skinny_d
 #pragma unroll
     for (int o = 0; o < OWN; ++o) {
       const int idx = ct + o * NCH;
+      if (NOUT % NCH != 0 && idx >= NOUT) continue;
       const int l = (idx >> 2) & 63;
       const int n = n0 + 16 * (idx >> 8) + 4 * (l >> 4) + (idx & 3), m = l & 15;
       if (m >= M || n >= N) continue;
@@ -343,7 +346,7 @@ template <int RB, int MB, int WF, int EPI, int GS, bool SWH, int NS>
 hipError_t run_sd_ns(const GemmArgs& a, hipStream_t s) {
   const int rows = 16 * RB;
   skinny_dma_kernel<RB, MB, NS, WF, EPI, GS, SWH>
-      <<<(a.N + rows - 1) / rows, (EPI == EPI_PG ? 2 : 1) * kSdKW * 64, 0, s>>>(a);
+      <<<(a.N + rows - 1) / rows, (EPI == EPI_PG ? kSdKW + kSdCW : kSdKW) * 64, 0, s>>>(a);
   return hipGetLastError();
 }
 
