@@ -52,6 +52,8 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
 size_t quant_ws_bytes(int64_t M, int64_t K) {
   return align256((size_t)M * (size_t)K) + align256((size_t)M * sizeof(float));
 }
@@ -160,11 +162,15 @@ int cider_version(void) { return 100; }  // 0.1.0
 const char* cider_last_error(void) { return g_last_error.c_str(); }
 
 size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K, int group_size) {
-  (void)N;
   (void)group_size;
   if (M <= 0 || K < 0) return 0;
   switch (op) {
     case CIDER_OP_PERCHANNEL:
+      // quantized activations and scales, plus the int32 partial sums of the
+      // split-K GEMM where that shape takes it
+      if (M <= 1) return 0;
+      if (N <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return quant_ws_bytes(M, K);
+      return quant_ws_bytes(M, K) + align256(cider::splitk_bytes((int)M, (int)N, (int)K));
     case CIDER_OP_PERGROUP:
       return M <= 1 ? 0 : quant_ws_bytes(M, K);
     case CIDER_OP_W4A8:
@@ -248,6 +254,15 @@ int cider_perchannel_linear(const void* x_f16, const int8_t* w_nk, const float* 
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
   cider::GemmArgs g{q, w_nk, sa, sw, bias, y_f16, (int)M, (int)N, (int)K};
+  // Split-K where the shape takes it and the workspace holds the partial sums
+  // (a workspace sized for the quantized activations alone runs one pass)
+  const int S = cider::splitk_ways((int)M, (int)N, (int)K);
+  const size_t qbytes = quant_ws_bytes(M, K);
+  if (S > 1 && ws_bytes >= qbytes + cider::splitk_bytes((int)M, (int)N, (int)K) &&
+      aligned16(w_nk) && aligned16(y_f16) && aligned16(sw) && aligned16(q)) {
+    int32_t* part = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(ws) + qbytes);
+    return hip_status(cider::launch_gemm_splitk(g, S, part, s), fn);
+  }
   return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PC, false, 0, s), fn);
 }
 
@@ -257,7 +272,8 @@ int cider_perchannel_linear_noalloc(const void* x_f16, const int8_t* w_nk, const
   static const char* fn = "cider_perchannel_linear_noalloc";
   CIDER_TRY(check_dims(fn, M, N, K));
   if (M == 0 || N == 0) return ok();
-  const size_t need = cider_workspace_bytes(CIDER_OP_PERCHANNEL, M, N, K, 0);
+  // the quantized activations and scales only (no split-K partial sums)
+  const size_t need = M <= 1 ? 0 : quant_ws_bytes(M, K);
   if (need > (size_t)CIDER_NOALLOC_SCRATCH_BYTES)
     return fail(CIDER_E_INVALID,
                 "%s: M=%lld K=%lld needs %zu bytes of scratch, above the library's %zu "
@@ -398,8 +414,6 @@ int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
 // ---- producers of the linear's input and the decode attention -------------
 
 namespace {
-
-bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 int check_rows(const char* fn, int64_t M, int64_t K, const char* kname) {
   CIDER_TRY(check_dims(fn, M, 1, K));

@@ -131,7 +131,7 @@ using icst = std::integral_constant<int, V>;
 // byte k/2, low nibble first, two's complement), unpacked in registers.
 template <int BM, int BN, int BK, int EPI, int WF = W_I8>
 __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const int n0,
-                                         int8_t* __restrict__ smem) {
+                                         int8_t* __restrict__ smem, const int kloop = 0) {
   static_assert((BM == 64 || BM == 128 || BM == 192 || BM == 256) &&
                     (BN == 64 || BN == 128 || BN == 256),
                 "tile shape");
@@ -293,7 +293,7 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     }
   };
 
-  const int nk = K / BK;
+  const int nk = (kloop > 0 ? kloop : K) / BK;  // k-stages (a split-K slice: kloop of K)
   i32x4 wf[2][TN], xf[2][TM];
   // Prologue: stages 0 .. NS-2 into slots 0 .. NS-2, and part 0 of stage
   // NS-1 into slot NS-1; stage 0's first sub-steps issue its other parts as
@@ -591,6 +591,95 @@ int num_cus() {
     cache[dev] = n;
   }
   return cache[dev];
+}
+
+// ---- Split-K for per-channel shapes whose tiles leave most CUs idle (M up
+// to a few hundred rows on small N, e.g. M=128 N=2560 K=10240: 20 tiles of
+// 128 x 128).  Workgroup (t, s) runs tile t over the k range [s ks, (s+1) ks)
+// with the int32 epilogue into partial slice s; the dequant kernel sums the
+// slices (int32: exact in any order) and applies the per-channel epilogue
+// with the operation order of the tile epilogue, so the result is the same
+// bits as one pass over K.
+template <int BM>
+__global__ __launch_bounds__(256, 1) void gemm_dma_splitk_kernel(const GemmArgs p, int ks,
+                                                                 int32_t* __restrict__ part) {
+  constexpr int BN = 128, BK = 128;
+  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK, W_I8>::SMEM];
+  const int sl = blockIdx.y;
+  GemmArgs q = p;
+  q.x = p.x + (int64_t)sl * ks;
+  q.w = reinterpret_cast<const int8_t*>(p.w) + (int64_t)sl * ks;
+  q.y = part + (int64_t)sl * p.M * p.N;
+  int m0, n0;
+  tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), p.M, 0, p.N, m0, n0);
+  dma_tile<BM, BN, BK, EPI_I32, W_I8>(q, m0, n0, smem, ks);
+}
+
+// y[m, n..n+3] = h(f32(f32(sum_s part[s][m][n]) * sa[m]) * sw[n] [+ bias[n]]);
+// N % 4 == 0, so a thread's four columns share a row.
+__global__ __launch_bounds__(256) void splitk_dequant_kernel(const GemmArgs p,
+                                                             const int32_t* __restrict__ part,
+                                                             int S) {
+  const int64_t MN = (int64_t)p.M * p.N;
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= MN) return;
+  const int m = (int)(e / p.N), n = (int)(e % p.N);
+  i32x4 acc = *reinterpret_cast<const i32x4*>(part + e);
+  for (int sl = 1; sl < S; ++sl) acc += *reinterpret_cast<const i32x4*>(part + sl * MN + e);
+  const float sam = p.sa[m];
+  const f32x4 swv = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.sw) + n);
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = (float)acc[r] * sam;
+    v = v * swv[r];
+    if (p.bias) v = v + h2f(p.bias[n + r]);
+    o[r] = v;
+  }
+  *reinterpret_cast<i32x2*>(reinterpret_cast<uint16_t*>(p.y) + e) =
+      i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+}
+
+// K slices for a per-channel int8 shape (1 = no split): only where the
+// 128-column tiles (64-row for M <= 64) fill at most a quarter of the CUs,
+// then the most slices, in powers of two, that keep the grid within one
+// workgroup per CU and each slice at 8 k-stages or more.  Measured with the
+// weights streaming from HBM (whole linears): N=2560 K=10240 M=32 / 128 /
+// 256: 25.6 -> 17.9 us (8 slices), 32.3 -> 23.8 us (8), 32.6 -> 28.8 us (4);
+// N=4096 K=12288 M=64: 37.1 -> 23.7 us (8).  Grids of more tiles gained
+// little or lost (N=10240 K=2560 M=32, 80 tiles: 12.4 us whole, 16.2 us in
+// two slices).  The caller also checks the DMA conditions (K % 128 == 0,
+// N % 8 == 0, aligned operands).
+int splitk_ways(int M, int N, int K) {
+  if (M <= 16 || M > 512 || N % 8 != 0 || K % 128 != 0) return 1;
+  const int bm = M <= 64 ? 64 : 128;
+  const int tiles = ((M + bm - 1) / bm) * ((N + 127) / 128);
+  const int cus = num_cus();
+  if (4 * tiles > cus) return 1;
+  int S = 1;
+  while (S < 16 && tiles * 2 * S <= cus && K % (128 * 2 * S) == 0 && K / (2 * S) >= 1024) S *= 2;
+  return S;
+}
+
+size_t splitk_bytes(int M, int N, int K) {
+  const int S = splitk_ways(M, N, K);
+  return S > 1 ? (size_t)S * M * N * 4 : 0;
+}
+
+hipError_t launch_gemm_splitk(const GemmArgs& a, int S, int32_t* part, hipStream_t s) {
+  const int ks = a.K / S;
+  if (a.M <= 64) {
+    const dim3 grid(((a.M + 63) / 64) * ((a.N + 127) / 128), S);
+    gemm_dma_splitk_kernel<64><<<grid, 256, 0, s>>>(a, ks, part);
+  } else {
+    const dim3 grid(((a.M + 127) / 128) * ((a.N + 127) / 128), S);
+    gemm_dma_splitk_kernel<128><<<grid, 256, 0, s>>>(a, ks, part);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t quads = ((int64_t)a.M * a.N) / 4;
+  splitk_dequant_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>(a, part, S);
+  return hipGetLastError();
 }
 
 // Eligible: EPI_I32 or EPI_PC with int8 weights, EPI_PC with int4 weights;

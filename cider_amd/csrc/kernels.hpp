@@ -42,6 +42,12 @@ hipError_t launch_skinny_dma(const GemmArgs& a, int wf, int epi, int gs, hipStre
 hipError_t launch_skinny(const GemmArgs& a, int wf, int epi, bool sw_half, int gs,
                          hipStream_t s);
 hipError_t launch_gemm_dma(const GemmArgs& a, int epi, int wf, hipStream_t s);
+// Split-K per-channel GEMM for shapes with few tiles (gemm_dma.hip): K slices
+// (1 = no split), the int32 partial bytes they need, and the launch (split
+// tiles into `part`, then the summing dequant into a.y).
+int splitk_ways(int M, int N, int K);
+size_t splitk_bytes(int M, int N, int K);
+hipError_t launch_gemm_splitk(const GemmArgs& a, int S, int32_t* part, hipStream_t s);
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s);
 
 // Decode-sized GEMV on quantized activations (1 <= M <= 4), gemv_q.hip.

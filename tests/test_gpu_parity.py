@@ -476,6 +476,30 @@ def test_skinny_dma_exact(M, N, K):
     assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"skinny dma w4 {M}x{N}x{K}")
 
 
+# Split-K per-channel GEMM (M from 17 to 512 where the tiles fill at most a
+# quarter of the CUs): int32 partial sums of K slices, summed (exact) by the
+# dequant kernel in the tile epilogue's operation order.  Slices:
+# (128, 2560, 10240) and (64, 2560, 10240) eight, (17, 4096, 12288) eight,
+# (130, 2560, 4096) four with a ragged row tile, (256, 2560, 10240) four,
+# (200, 1000, 4096) four with N past the last 128-column tile; (512, 2560,
+# 2560) has 80 tiles and runs one pass.  The extremes (-127 everywhere) are
+# summed over the longest slices.
+@pytest.mark.parametrize("M,N,K", [(128, 2560, 10240), (64, 2560, 10240), (17, 4096, 12288),
+                                   (130, 2560, 4096), (256, 2560, 10240), (200, 1000, 4096),
+                                   (512, 2560, 2560)])
+def test_splitk_perchannel_exact(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 150 + M)
+    x[0, :] = 0                                  # s = 1, q = 0
+    x[1, :3] = [65504.0, -65504.0, 1.0]
+    for bias in (b, None):
+        y = H(C.perchannel_linear(T(x), T(w), T(sw), None if bias is None else T(bias)))
+        assert_bits_equal(y, O.perchannel_linear(x, w, sw, bias), f"split-K pc {M}x{N}x{K}")
+    xe = np.full((M, K), -60000.0, dtype=np.float16)   # quantizes to -127 everywhere
+    we = np.full((N, K), -127, dtype=np.int8)
+    y = H(C.perchannel_linear(T(xe), T(we), T(sw), T(b)))
+    assert_bits_equal(y, O.perchannel_linear(xe, we, sw, b), f"split-K extremes {M}x{N}x{K}")
+
+
 # Skinny kernel (M <= 64) at shapes where N alone gives few workgroups, so the
 # K range is split over 8 or 16 waves per workgroup (int32 sums exact in any
 # order); per-group deals the groups to the waves round-robin and keeps the

@@ -43,8 +43,10 @@ def _call_both(lib, _lib, x, w, sw, b):
 def test_noalloc_matches_workspace_entry_twice_then_smaller():
     from cider_amd import _lib
     lib = _lib.load()
+    # (128, 2560, 10240): the workspace entry runs the split-K GEMM (eight K
+    # slices), the scratch entry one pass over K: the same bits either way
     cases = [(4096, 2560, 2560, True), (300, 1000, 1024, False), (1, 512, 1024, True),
-             (3, 256, 512, True)]
+             (3, 256, 512, True), (128, 2560, 10240, True)]
     for M, N, K, bias in cases:
         print(f"noalloc M={M} N={N} K={K}", flush=True)
         x = O.synth_activations(M, K, 7000 + M)
