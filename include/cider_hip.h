@@ -51,7 +51,11 @@ const char* cider_last_error(void);
 
 /* Bytes of scratch the linear entry points need for the given problem
  * (quantized activations int8 [M,K] and per-token scales fp32 [M], each
- * 256-byte aligned). 0 when the call needs none (M <= 1 on the W8 paths).
+ * 256-byte aligned; for CIDER_OP_PERCHANNEL also the int32 partial sums of
+ * the split-K GEMM, S*M*N*4 bytes, on shapes with few output tiles, which
+ * a smaller workspace of at least the first two parts runs in one pass over
+ * K instead, with the same results). 0 when the call needs none (M <= 1 on
+ * the W8 paths).
  * Replaces the per-call temporaries of csrc/src/w8a8_primitive.mm:184-188
  * and the global ScratchPool of csrc/src/w4a8_primitive.mm:40-76. */
 size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K,
