@@ -12,9 +12,10 @@
 //     v_mfma_i32_32x32x32_i8; operands reach LDS by global_load_lds_dwordx4
 //     through a ring of 128-byte k-stages, with the constant-count waits,
 //     swizzle and fixed-order sub-steps of the per-channel kernel
-//     (gemm_dma.hip).  Two launch shapes: 128 x 128 tiles of 8 waves (two
-//     per SIMD, 4 ring slots; gs 64 and 256 at M > 64) and 128 x 64 tiles of
-//     4 waves (gs 128 at two workgroups per CU, gs 64 at M <= 64).
+//     (gemm_dma.hip).  Three launch shapes: 128 x 128 tiles of 8 waves (two
+//     per SIMD, 4 ring slots; gs 64 and 256 at M > 64), 128 x 64 tiles of
+//     4 waves (gs 128 at two workgroups per CU, gs 64 at M <= 64), and 64 x 64
+//     tiles of four 32 x 32 waves where those would leave most CUs idle.
 //   * Group accumulators: two int32 sets alternate by group.  A group's first
 //     MFMA takes C = 0 (an inline constant), so starting a group costs
 //     nothing.  While group g accumulates, group g-1 is flushed into the fp32
@@ -528,7 +529,40 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 // Eligible: int8 or int4 weights, per-group gs 64 / 128 (gs 256: int8 and
 // K % 256 == 0), K % 128 == 0, N % 8 == 0, 16-byte aligned operands
 // (launch_gemm checks).
+namespace {
+
+// 64 x 64 tiles of four 32 x 32 waves, for grids the larger tiles leave
+// mostly idle.
+template <int GS, bool SWH, int WF>
+hipError_t run_pg64(const GemmArgs& a, hipStream_t s) {
+  const int tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+  gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
+  {
+    // Mid M on small N: when the tiles below would fill at most half the
+    // CUs, 64 x 64 tiles give four times as many workgroups (the group chain
+    // rules out splitting K across workgroups).  Weights from HBM: gs 128
+    // M=128 N=2560 K=10240 48.9 -> 35.3 us, gs 64 M=512 N=4096 K=12288 99.0
+    // -> 77.4 us; at twice that many large tiles the 64 x 64 grid was slower.
+    const int big = gs == 128 ? ((a.M + 127) / 128) * ((a.N + 63) / 64)
+                              : ((a.M + 127) / 128) * ((a.N + 127) / 128);
+    if (2 * big <= num_cus()) {
+      if (wf == W_I4) return gs == 64 ? run_pg64<64, true, W_I4>(a, s) : run_pg64<128, true, W_I4>(a, s);
+      if (sw_half) {
+        if (gs == 64) return run_pg64<64, true, W_I8>(a, s);
+        if (gs == 128) return run_pg64<128, true, W_I8>(a, s);
+        return run_pg64<256, true, W_I8>(a, s);
+      }
+      if (gs == 64) return run_pg64<64, false, W_I8>(a, s);
+      if (gs == 128) return run_pg64<128, false, W_I8>(a, s);
+      return run_pg64<256, false, W_I8>(a, s);
+    }
+  }
   if (gs == 256) {
     // int8 weights only (the W4A8 formats define gs 64 / 128); the 8-wave
     // 128 x 128 tile: 205.6 us at M=4096 N=10240 K=2560 against 225.8 us for

@@ -476,6 +476,28 @@ def test_skinny_dma_exact(M, N, K):
     assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"skinny dma w4 {M}x{N}x{K}")
 
 
+# Per-group at mid M on small N: 64 x 64 tiles of four 32 x 32 waves, where the
+# 128-row tiles would fill at most half the CUs.  (65, 2560, 10240) leaves a
+# one-row tile, (200, 1032, 2048) a ragged row tile and N past the last
+# 64-column tile; every group size and both weight formats, bit-exact
+# against the oracle's sequential group chain.
+@pytest.mark.parametrize("M,N,K", [(65, 2560, 10240), (128, 2560, 10240), (200, 1032, 2048),
+                                   (512, 4096, 4096)])
+def test_pergroup_small_tiles_exact(M, N, K):
+    x, w, _, b = synth_pc(M, N, K, 160 + M)
+    for gs in (64, 128, 256):
+        swg = O.synth_scales((K // gs, N), 161 + gs)
+        y = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
+        assert_bits_equal(y, O.pergroup_linear(x, w, swg, gs, b), f"pg64 tiles gs{gs} {M}x{N}x{K}")
+    w4 = np.random.default_rng(162).integers(-8, 8, (N, K), dtype=np.int8)
+    pk = O.pack_w4_lo_first(w4)
+    for gs in (64, 128):
+        sc = O.synth_scales((K // gs, N), 163 + gs).astype(np.float16)
+        y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b)))
+        assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, b),
+                          f"pg64 tiles w4g{gs} {M}x{N}x{K}")
+
+
 # Split-K per-channel GEMM (M from 17 to 512 where the tiles fill at most a
 # quarter of the CUs): int32 partial sums of K slices, summed (exact) by the
 # dequant kernel in the tile epilogue's operation order.  Slices:
