@@ -77,7 +77,12 @@ __device__ __forceinline__ float dot16(i32x4 wv, i32x4 xa, i32x4 xb, float acc) 
 
 }  // namespace
 
-template <int R, int C, bool PG, int XM>
+// SS (per-group, N % (4 R) == 0, 16-byte aligned scales): the workgroup's
+// group scales, 4 R consecutive floats of each group row, are loaded as
+// 16-byte vectors with x and staged in LDS, instead of one scalar load per
+// weight chunk and lane (a group row per lane group, many cache lines per
+// instruction).
+template <int R, int C, bool PG, int XM, bool SS = false>
 __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w,
     const float* __restrict__ sw, const uint16_t* __restrict__ bias,
@@ -85,7 +90,11 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
   constexpr int K = 1024 * C / R;
   constexpr int CPR = K / 16;  // 16-byte chunks per row
   static_assert(R * K == 1024 * C && CPR >= 64, "one wave covers whole rows");
+  static_assert(!SS || PG, "staged scales are per-group");
   __shared__ __attribute__((aligned(16))) uint16_t xs[K];
+  constexpr int WR = kWpg * R;                     // rows of the workgroup
+  constexpr int SV = SS ? ((K / 64) * R + 255) / 256 : 1;  // scale vectors per thread (gs >= 64)
+  __shared__ __attribute__((aligned(16))) float ssc[SS ? (K / 64) * WR : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -106,6 +115,18 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     if constexpr (kNorm) xn[q] = ld16(pp.nw + 8 * e);
   }
 
+  // per-group, staged: the [G][WR] scale block of the workgroup's rows
+  f32x4 sv[SV];
+  const int nw0 = blockIdx.x * WR;
+  if constexpr (SS) {
+    const int nv = (K / gs) * R;  // 16-byte vectors: R per group row
+#pragma unroll
+    for (int q = 0; q < SV; ++q) {
+      const int e = min(tid + q * 256, nv - 1);
+      sv[q] = *reinterpret_cast<const f32x4*>(sw + (int64_t)(e / R) * N + nw0 + 4 * (e % R));
+    }
+  }
+
   // per-row scale (per-channel) and bias of the row lane l < R writes; the
   // loads are unconditional (clamped row; x stands in for a missing bias), as
   // a load under a lane mask makes the compiler wait for every load before it
@@ -122,7 +143,7 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     const int r = c / CPR, kc = c - r * CPR;
     const int row = min(n0 + r, N - 1);
     wv[j] = ld16(w + (int64_t)row * K + 16 * kc);
-    if constexpr (PG) sj[j] = sw[(int64_t)((16 * kc) / gs) * N + row];
+    if constexpr (PG && !SS) sj[j] = sw[(int64_t)((16 * kc) / gs) * N + row];
   }
   // every load is issued before any arithmetic on x: keeps the scheduler from
   // hoisting the producer math (and its waits) above the weight loads
@@ -160,6 +181,14 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     const int e = min(tid + q * 256, nchunk - 1);
     *reinterpret_cast<i32x4*>(xs + 8 * e) = xr[q];
   }
+  if constexpr (SS) {
+    const int nv = (K / gs) * R;
+#pragma unroll
+    for (int q = 0; q < SV; ++q) {
+      const int e = min(tid + q * 256, nv - 1);  // a copy of the last vector past the end
+      *reinterpret_cast<f32x4*>(ssc + (e / R) * WR + 4 * (e % R)) = sv[q];
+    }
+  }
   __syncthreads();
 
   // ---- products, in chunk order per lane; a chunk's row is r_lo or r_lo + 1
@@ -173,7 +202,9 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     const i32x4 xa = *reinterpret_cast<const i32x4*>(xs + 16 * kc);
     const i32x4 xb = *reinterpret_cast<const i32x4*>(xs + 16 * kc + 8);
     float d;
-    if constexpr (PG) {
+    if constexpr (SS) {
+      d = ssc[((16 * kc) / gs) * WR + wave * R + r] * dot16(wv[j], xa, xb, 0.0f);
+    } else if constexpr (PG) {
       d = sj[j] * dot16(wv[j], xa, xb, 0.0f);
     } else {
       d = dot16(wv[j], xa, xb, 0.0f);
@@ -202,9 +233,21 @@ template <int R, int C, bool PG, int XM>
 hipError_t run_stream(const uint16_t* x, const int8_t* w, const float* sw,
                       const uint16_t* bias, uint16_t* y, int N, int gs, const MvProducer& pp,
                       hipStream_t s) {
+  constexpr int K = 1024 * C / R;
   const int waves = (N + R - 1) / R;
-  mv_stream_kernel<R, C, PG, XM><<<(waves + kWpg - 1) / kWpg, kWpg * 64, 0, s>>>(
-      x, w, sw, bias, y, N, gs, pp);
+  const dim3 grid((waves + kWpg - 1) / kWpg), block(kWpg * 64);
+  if constexpr (PG) {
+    // staged where it measured faster (weights from HBM): every gs 64 shape
+    // (N=2560 K=10240: 11.6 -> 9.5 us), gs 128 at one row per wave (9.4 ->
+    // 8.4 us), gs 256 at one row per wave and K >= 8192 (8.4 -> 7.8 us); at
+    // two rows per wave gs 128 / 256 ran 3-5 % slower staged
+    const bool stage = gs == 64 || (R == 1 && (gs == 128 || K >= 8192));
+    if (stage && N % (kWpg * R) == 0 && ((uintptr_t)sw & 15) == 0) {
+      mv_stream_kernel<R, C, PG, XM, true><<<grid, block, 0, s>>>(x, w, sw, bias, y, N, gs, pp);
+      return hipGetLastError();
+    }
+  }
+  mv_stream_kernel<R, C, PG, XM><<<grid, block, 0, s>>>(x, w, sw, bias, y, N, gs, pp);
   return hipGetLastError();
 }
 
