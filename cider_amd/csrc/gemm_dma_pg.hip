@@ -25,9 +25,12 @@
 //     multiply-add).  That flush is the kernel's bound: 12 VALU ops per MFMA
 //     at gs = 128, 24 at gs = 64, against the MFMA's 32 cycles and 4 per
 //     wave64 VALU op (6 at gs = 256).  A gs 256 group spans two k-stages, so
-//     the sets alternate over a period of 4 stages instead of 2.  Before the first group the other set is zero and its
-//     "scales" are group 0's, so the first flush adds +0.0; the last stage
-//     flushes the last group after its MFMAs.  Every register is
+//     the sets alternate over a period of 4 stages instead of 2.  Before the
+//     first group the other set is zero and its "scales" are a zero row, so
+//     the first flush adds +0.0; the last stage flushes the last group after
+//     its MFMAs.  fp16 scales (W4A8) take the fast flush below: the MFMA
+//     starts each group from a float bias, and one fma per accumulator
+//     replaces the conversion and the multiply (2 VALU ops).  Every register is
 //     architectural (no AGPR reads in the flush) and nothing spills: a spill
 //     reload is a vector-memory load the compiler tracks, and waiting for it
 //     would also wait for every LDS-DMA load in flight.
@@ -89,6 +92,25 @@ __device__ __forceinline__ i32x4 pg_unpack_w4_8(uint32_t w0, uint32_t w1) {
 template <int V>
 using ic = std::integral_constant<int, V>;
 
+// Fast flush (fp16 group scales).  A group's int32 sum D starts from the bit
+// pattern of B = 1.5 * 2^23 instead of 0, so for |D| <= 2^22 (every group
+// size here: |D| <= 128 * 128 * 256 = 2^22) the sum's bits read as the float
+// F = B + D exactly.  For an fp16 scale s (11 significant bits) c = -B * s is
+// exact in fp32, so fma(F, s, c) = round(D * s): the same single rounding as
+// f32(f32(D) * s), since f32(D) is exact.  The conversion disappears from
+// the flush: 2 VALU ops per accumulator instead of 3.  A non-finite s gives
+// NaN where the specified product is +-inf; the kernel then redoes the tile
+// with the exact flush.
+constexpr int32_t kPgBiasBits = 0x4B400000;
+constexpr float kPgBias = 12582912.0f;  // 1.5 * 2^23
+static_assert(__builtin_bit_cast(float, kPgBiasBits) == kPgBias, "bias bits");
+
+// fp16 element i of 4 packed in two words, widened (the fma takes it as an
+// fp16 operand).
+__device__ __forceinline__ float pg_half(const uint32_t (&r)[2], int i) {
+  return (float)__builtin_bit_cast(f16x2, r[i >> 1])[i & 1];
+}
+
 // Width of the 4-wave tile (128 x 64).  gs = 128 runs two of its workgroups
 // per CU: each workgroup's waits hide behind the other's flush.
 constexpr int PG_LAUNCH_BN = 64;
@@ -123,6 +145,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   static_assert(EPS % NMF == 0, "flush split");
   static_assert(CPR * 16 * SRPS <= PG_SSLOT && 64 / CPR >= SRPS, "scale rows per stage");
   static_assert(NCOMBO % 4 == 0, "whole combos per sub-step");
+  // The flush before the first group (zero sums) reads zero "scales": 0 * s
+  // would be NaN for an infinite s.  They sit in the last scale slot, whose
+  // first DMA (stage SNS-1) is issued in stage SNS-1-NS, after every read of
+  // the zero row (stages 0 and 1) has finished; each pass writes them anew.
+  constexpr int kZeroRow = PG_RING + (PG_SNS - 1) * PG_SSLOT;
+  static_assert(PG_SNS - 1 - PG_NS >= 2 && ROWB <= PG_SSLOT, "zero row slot");
   __shared__ __attribute__((aligned(1024))) int8_t smem[PG_SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -210,275 +238,341 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
                        : pg_unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
   };
 
-  // Two int32 group sets alternate by group (set = group parity); while
-  // group g accumulates, group g-1 is flushed, EPS of its accumulators per
-  // sub-step over the SUBG sub-steps of group g (accumulator e of a set:
-  // combo e / EPC, block (e / 4) % TM, element e % 4 of the combo's quad).
-  // Before the first group the other set is zero and its "scales" are group
-  // 0's, so that flush adds +0.0.
-  constexpr int EPC = PG_TM * 4;          // accumulators per (a, q) combo
-  constexpr int CPF = EPS >= EPC ? EPS / EPC : 1;  // combos of one sub-step's flush
-  constexpr int EPM = EPS / NMF;          // accumulators flushed after each MFMA
-  static_assert(EPS % EPC == 0 || EPC % EPS == 0, "flush split");
-  i32x16 D[2][PG_TN][PG_TM];
   float facc[PG_TN][PG_TM][16];
-#pragma unroll
-  for (int a = 0; a < PG_TN; ++a)
-#pragma unroll
-    for (int b = 0; b < PG_TM; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        D[0][a][b][r] = 0;
-        D[1][a][b][r] = 0;
-        facc[a][b][r] = 0.0f;
-      }
-
-  // the 4 scales of combo (a, q) of group g (clamped at 0):
-  // n = wn*WN + 32a + 8q + 4h + [0..3]
-  auto read_scales = [&](int g, int combo, float (&sv)[4]) __attribute__((always_inline)) {
-    g = max(g, 0);
-    // the row sits in the slot of the stage the group starts in
-    const int8_t* base = smem + PG_RING + ((g * SUBG / 4) % PG_SNS) * PG_SSLOT + (g % SRPS) * ROWB;
-    const int nl = wn * PG_WN + (combo / 4) * 32 + 8 * (combo % 4) + 4 * h;
-    if constexpr (SWH) {
-      const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
-      sv[0] = h2f((uint16_t)((uint32_t)v[0] & 0xffffu));
-      sv[1] = h2f((uint16_t)((uint32_t)v[0] >> 16));
-      sv[2] = h2f((uint16_t)((uint32_t)v[1] & 0xffffu));
-      sv[3] = h2f((uint16_t)((uint32_t)v[1] >> 16));
-    } else {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(base + nl * 4);
-      sv[0] = v[0];
-      sv[1] = v[1];
-      sv[2] = v[2];
-      sv[3] = v[3];
-    }
-  };
-  // Scales of the flush.  gs = 128: double-buffered by sub-step (sub-step j
-  // flushes with sv[j & 1] and reads the next sub-step's into sv[(j+1) & 1]).
-  // gs = 64 at two workgroups per CU (twice the combos per sub-step): one
-  // buffer, read at the start of the sub-step, to save registers.
-  constexpr bool SVDB = (GS == 128) || (OCC == 1);
-  float sv[SVDB ? 2 : 1][CPF][4];
-  auto read_sub_scales = [&](int g, int slice, float (&dst)[CPF][4])
-                             __attribute__((always_inline)) {
-#pragma unroll
-    for (int c = 0; c < CPF; ++c) read_scales(g, slice * EPS / EPC + c, dst[c]);
-  };
-
-  // One k sub-step J of the stage in a fixed order (sched_barrier): the
-  // MFMAs into set CS (C = 0 when `first`), the next sub-step's fragment
-  // reads one per MFMA in consumption order (rd) together with its flush
-  // scales (group ng, slice ns), this wave's DMA loads of stage dst into slot
-  // dsl (dma), and the flush of slice SL of the previous group from set
-  // 1 - CS (EPM accumulators after each MFMA).
-  auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto SLc, auto Jc,
-                  const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs,
-                  i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int ng, int ns,
-                  int cg) __attribute__((always_inline)) {
-    constexpr int CS = decltype(CSc)::value, SL = decltype(SLc)::value, J = decltype(Jc)::value;
-    constexpr int JN = (J + 1) % 4;  // the sub-step whose operands are read
-    constexpr bool first = decltype(firstc)::value != 0;
-    constexpr bool rd = decltype(rdc)::value != 0;
-    constexpr bool dma = decltype(dmac)::value != 0;
-    if constexpr (!SVDB) read_sub_scales(cg, SL, sv[0]);
-#pragma unroll
-    for (int idx = 0; idx < NMF; ++idx) {
-      const int a = idx / PG_TM, b = idx % PG_TM;
-      if constexpr (first)
-        D[CS][a][b] = mfma32(wc[a], xc[b], i32x16{});
-      else
-        D[CS][a][b] = mfma32(wc[a], xc[b], D[CS][a][b]);
-      if constexpr (rd && !W4) {
-#pragma unroll
-        for (int q = 0; q < NR; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx) {
-            if (q == 0)
-              read_w(rs, JN, 0, wn_);
-            else if (q <= PG_TM)
-              read_x(rs, JN, q - 1, xn);
-            else
-              read_w(rs, JN, q - PG_TM, wn_);
-          }
-      }
-      if constexpr (rd && W4) {
-        constexpr bool new_pair = (JN % 2) == 0;
-        constexpr int NRD = PG_TM + (new_pair ? PG_TN : 0);
-#pragma unroll
-        for (int q = 0; q < NRD; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx) {
-            if (q < PG_TM)
-              read_x(rs, JN, q, xn);
-            else
-              read_w(rs, JN, q - PG_TM, raw);
-          }
-        // unpack of block a2: in the last PG_TN slots, never before the slot
-        // that reads its new chunk (PG_TM + a2, clamped)
-#pragma unroll
-        for (int a2 = 0; a2 < PG_TN; ++a2) {
-          constexpr int first_slot = new_pair ? (NMF > PG_TN ? NMF - PG_TN : 0) : 0;
-          const int want =
-              first_slot + a2 > PG_TM + a2 || !new_pair ? first_slot + a2 : PG_TM + a2;
-          if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
-        }
-      }
-      if constexpr (rd && SVDB) {
-        if (idx == 0) read_sub_scales(ng, ns, sv[JN & 1]);
-      }
-      if constexpr (dma) {
-#pragma unroll
-        for (int d = 0; d < PG_PS; ++d)
-          if (d * NMF / PG_PS == idx) dma_one(dst, dsl, d);
-        if (idx == 0 && wave == 0) dma_scales(dst);
-      }
-#pragma unroll
-      for (int e = idx * EPM; e < (idx + 1) * EPM; ++e) {
-        const int eg = SL * EPS + e;  // accumulator of the set
-        const int combo = eg / EPC, bb = (eg / 4) % PG_TM, rr = eg % 4;
-        const int c = combo - SL * EPS / EPC;  // combo within the sub-step's scales
-        const int aa = combo / 4, r = 4 * (combo % 4) + rr;
-        const float t = (float)D[1 - CS][aa][bb][r] * sv[SVDB ? (J & 1) : 0][c][rr];
-        facc[aa][bb][r] = facc[aa][bb][r] + t;
-        // Pins this flush element to its slot: without it the compiler sinks
-        // the whole flush of a group below the next group's MFMAs, in one
-        // VALU block that the MFMAs no longer hide (and, at 64 x 64 waves,
-        // with both versions of the set alive at once).
-        asm volatile("" : "+v"(facc[aa][bb][r]));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
-  auto wait_stage = [&]() __attribute__((always_inline)) {
-    if (wave == 0)
-      wait_vmcnt<(PG_NS - 2) * (PG_PS + 1)>();
-    else
-      wait_vmcnt<(PG_NS - 2) * PG_PS>();
-  };
-
-  i32x4 wf[2][PG_TN], xf[2][PG_TM];
-  // Prologue: stages 0 .. NS-1 (a stage past the end reloads stage nk-1 into
-  // a slot nobody reads, so every stage issue moves the same loads).
-#pragma unroll
-  for (int st = 0; st < PG_NS; ++st) {
-    dma_stage(min(st, nk - 1), st);
-    if (wave == 0) dma_scales(min(st, nk - 1));
-  }
-  if (wave == 0)
-    wait_vmcnt<(PG_NS - 1) * (PG_PS + 1)>();
-  else
-    wait_vmcnt<(PG_NS - 1) * PG_PS>();
-  __syncthreads();
-#pragma unroll
-  for (int b = 0; b < PG_TM; ++b) read_x(0, 0, b, xf[0]);
-#pragma unroll
-  for (int a = 0; a < PG_TN; ++a) {
-    if constexpr (W4) {
-      read_w(0, 0, a, raw);
-      unpack_half(a, 0, wf[0]);
-    } else {
-      read_w(0, 0, a, wf[0]);
-    }
-  }
-
-  if constexpr (SVDB) read_sub_scales(-1, 0, sv[0]);  // first flush: zero set, group 0's scales
-
   float sa_t = 0.0f;
   uint16_t b_t = 0;
 
-  // Stage kt at position HALF (0 .. PER-1) of a PER-stage period that starts
-  // at a multiple of PER, so group parities are compile-time.  Sub-step J
-  // belongs to group (4 kt + J) / SUBG and flushes slice (4 HALF + J) % SUBG
-  // of the group before it.  LAST: the final stage (no barrier or DMA;
-  // requests sa and bias; then flushes its own last group).
-  auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
-    constexpr int HALF = decltype(halfc)::value;
-    constexpr bool LAST = decltype(lastc)::value != 0;
-    const int sl = kt % PG_NS;
-    if constexpr (LAST) {
-      sa_t = p.sa[min(m0 + tid % PG_BM, M - 1)];
-      if (p.bias) b_t = p.bias[min(n0 + tid % PG_BN, N - 1)];
-    }
-    // group of sub-step J of stage k: (4 k + J) / SUBG; it flushes the one before
-#define PG_SUB(J)                                                                            \
-  {                                                                                          \
-    constexpr int S = 4 * HALF + (J);                                                        \
-    constexpr int CS = (S / SUBG) & 1;                                                       \
-    constexpr bool FIRST = (S % SUBG) == 0;                                                  \
-    constexpr int SL = S % SUBG;                                                             \
-    const int cg = (4 * kt + (J)) / SUBG - 1;                                                \
-    const int ng = (4 * kt + (J) + 1) / SUBG - 1;                                            \
-    if constexpr ((J) < 3) {                                                                 \
-      step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[(J) & 1],       \
-           xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, ng, (S + 1) % SUBG,  \
-           cg);                                                                              \
-    } else if constexpr (!LAST) {                                                            \
-      wait_stage();                                                                          \
-      __syncthreads();                                                                       \
-      step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1],      \
-           (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, ng, (S + 1) % SUBG,  \
-           cg);                                                                              \
-    } else {                                                                                 \
-      step(ic<CS>{}, ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1], 0,    \
-           wf[0], xf[0], 0, 0, 0, 0, cg);                                                    \
-    }                                                                                        \
-  }
-    PG_SUB(0)
-    PG_SUB(1)
-    PG_SUB(2)
-    PG_SUB(3)
-#undef PG_SUB
-    if constexpr (LAST) {
-      // flush the last group (set of sub-step 3), in order
-      constexpr int CSL = ((4 * HALF + 3) / SUBG) & 1;
-      const int gl = G - 1;
+  // One pass over K into facc: prologue, k-loop and the last group's flush.
+  // FAST (fp16 scales only) flushes with the biased sums (kPgBiasBits).
+  auto kpass = [&](auto fastc) __attribute__((always_inline)) {
+    constexpr bool FAST = decltype(fastc)::value != 0;
+    // Two int32 group sets alternate by group (set = group parity); while
+    // group g accumulates, group g-1 is flushed, EPS of its accumulators per
+    // sub-step over the SUBG sub-steps of group g (accumulator e of a set:
+    // combo e / EPC, block (e / 4) % TM, element e % 4 of the combo's quad).
+    // Before the first group the other set holds a zero sum and its "scales"
+    // are the zero row, so that flush adds +0.0.
+    constexpr int EPC = PG_TM * 4;          // accumulators per (a, q) combo
+    constexpr int CPF = EPS >= EPC ? EPS / EPC : 1;  // combos of one sub-step's flush
+    constexpr int EPM = EPS / NMF;          // accumulators flushed after each MFMA
+    static_assert(EPS % EPC == 0 || EPC % EPS == 0, "flush split");
+    static_assert(!FAST || SWH, "the fast flush needs fp16 scales");
+    // A group's sum starts from C0: 0, or the fast flush's bias bit pattern.
+    constexpr int32_t C0 = FAST ? kPgBiasBits : 0;
+    i32x16 cinit;
 #pragma unroll
-      for (int combo = 0; combo < NCOMBO; ++combo) {
-        float s4[4];
-        read_scales(gl, combo, s4);
-        const int aa = combo / 4, q = combo % 4;
+    for (int r = 0; r < 16; ++r) cinit[r] = C0;
+    i32x16 D[2][PG_TN][PG_TM];
 #pragma unroll
-        for (int bb = 0; bb < PG_TM; ++bb)
+    for (int a = 0; a < PG_TN; ++a)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const float t = (float)D[CSL][aa][bb][4 * q + rr] * s4[rr];
-            facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+      for (int b = 0; b < PG_TM; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          D[0][a][b][r] = C0;
+          D[1][a][b][r] = C0;
+          facc[a][b][r] = 0.0f;
+        }
+
+    // the 4 scales of combo (a, q) of group g (g < 0: zeros):
+    // n = wn*WN + 32a + 8q + 4h + [0..3]
+    // FAST: sr keeps the 4 fp16 scales packed (the flush's fma widens them)
+    // and sv holds c = -B * s for each.
+    auto read_scales = [&](int g, int combo, float (&sv)[4], uint32_t (&sr)[2])
+                           __attribute__((always_inline)) {
+      // the row sits in the slot of the stage the group starts in (a
+      // wave-uniform choice: g < 0 reads the zero row)
+      const int8_t* base = g < 0 ? smem + kZeroRow
+                                 : smem + PG_RING + ((g * SUBG / 4) % PG_SNS) * PG_SSLOT +
+                                       (g % SRPS) * ROWB;
+      const int nl = wn * PG_WN + (combo / 4) * 32 + 8 * (combo % 4) + 4 * h;
+      if constexpr (FAST) {
+        const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
+        sr[0] = (uint32_t)v[0];
+        sr[1] = (uint32_t)v[1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = __builtin_fmaf(pg_half(sr, i), -kPgBias, 0.0f);
+      } else if constexpr (SWH) {
+        const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
+        sv[0] = h2f((uint16_t)((uint32_t)v[0] & 0xffffu));
+        sv[1] = h2f((uint16_t)((uint32_t)v[0] >> 16));
+        sv[2] = h2f((uint16_t)((uint32_t)v[1] & 0xffffu));
+        sv[3] = h2f((uint16_t)((uint32_t)v[1] >> 16));
+      } else {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(base + nl * 4);
+        sv[0] = v[0];
+        sv[1] = v[1];
+        sv[2] = v[2];
+        sv[3] = v[3];
+      }
+    };
+    // Scales of the flush.  gs = 128: double-buffered by sub-step (sub-step j
+    // flushes with sv[j & 1] and reads the next sub-step's into sv[(j+1) & 1]).
+    // gs = 64 at two workgroups per CU (twice the combos per sub-step): one
+    // buffer, read at the start of the sub-step, to save registers.
+    // The fast flush's 8-wave tiles (two waves per SIMD) read them at the
+    // start of the sub-step too: its scales take 6 registers per combo.
+    constexpr bool SVDB = (GS == 128) || (OCC == 1 && !(FAST && NW == 8));
+    float sv[SVDB ? 2 : 1][CPF][4];
+    uint32_t sr[SVDB ? 2 : 1][CPF][2];  // FAST only
+    auto read_sub_scales = [&](int g, int slice, int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < CPF; ++c) read_scales(g, slice * EPS / EPC + c, sv[buf][c], sr[buf][c]);
+    };
+    // t = f32(f32(D_g) * s): exact conversion and one rounding of the product,
+    // or (FAST) one fma of the biased sum F = B + D_g that rounds D_g * s once
+    auto term = [&](int32_t d, const float (&s)[4], const uint32_t (&r)[2], int i)
+                    __attribute__((always_inline)) -> float {
+      if constexpr (FAST)
+        return __builtin_fmaf(__builtin_bit_cast(float, d), pg_half(r, i), s[i]);
+      else
+        return (float)d * s[i];
+    };
+
+    // One k sub-step J of the stage in a fixed order (sched_barrier): the
+    // MFMAs into set CS (C = 0 when `first`), the next sub-step's fragment
+    // reads one per MFMA in consumption order (rd) together with its flush
+    // scales (group ng, slice ns), this wave's DMA loads of stage dst into slot
+    // dsl (dma), and the flush of slice SL of the previous group from set
+    // 1 - CS (EPM accumulators after each MFMA).
+    auto step = [&](auto CSc, auto firstc, auto rdc, auto dmac, auto SLc, auto Jc,
+                    const i32x4 (&wc)[PG_TN], const i32x4 (&xc)[PG_TM], int rs,
+                    i32x4 (&wn_)[PG_TN], i32x4 (&xn)[PG_TM], int dst, int dsl, int ng, int ns,
+                    int cg) __attribute__((always_inline)) {
+      constexpr int CS = decltype(CSc)::value, SL = decltype(SLc)::value, J = decltype(Jc)::value;
+      constexpr int JN = (J + 1) % 4;  // the sub-step whose operands are read
+      constexpr bool first = decltype(firstc)::value != 0;
+      constexpr bool rd = decltype(rdc)::value != 0;
+      constexpr bool dma = decltype(dmac)::value != 0;
+      if constexpr (!SVDB) read_sub_scales(cg, SL, 0);
+#pragma unroll
+      for (int idx = 0; idx < NMF; ++idx) {
+        const int a = idx / PG_TM, b = idx % PG_TM;
+        if constexpr (first)
+          D[CS][a][b] = mfma32(wc[a], xc[b], cinit);
+        else
+          D[CS][a][b] = mfma32(wc[a], xc[b], D[CS][a][b]);
+        if constexpr (rd && !W4) {
+#pragma unroll
+          for (int q = 0; q < NR; ++q)
+            if ((q < NMF ? q : NMF - 1) == idx) {
+              if (q == 0)
+                read_w(rs, JN, 0, wn_);
+              else if (q <= PG_TM)
+                read_x(rs, JN, q - 1, xn);
+              else
+                read_w(rs, JN, q - PG_TM, wn_);
+            }
+        }
+        if constexpr (rd && W4) {
+          constexpr bool new_pair = (JN % 2) == 0;
+          constexpr int NRD = PG_TM + (new_pair ? PG_TN : 0);
+#pragma unroll
+          for (int q = 0; q < NRD; ++q)
+            if ((q < NMF ? q : NMF - 1) == idx) {
+              if (q < PG_TM)
+                read_x(rs, JN, q, xn);
+              else
+                read_w(rs, JN, q - PG_TM, raw);
+            }
+          // unpack of block a2: in the last PG_TN slots, never before the slot
+          // that reads its new chunk (PG_TM + a2, clamped)
+#pragma unroll
+          for (int a2 = 0; a2 < PG_TN; ++a2) {
+            constexpr int first_slot = new_pair ? (NMF > PG_TN ? NMF - PG_TN : 0) : 0;
+            const int want =
+                first_slot + a2 > PG_TM + a2 || !new_pair ? first_slot + a2 : PG_TM + a2;
+            if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
           }
+        }
+        if constexpr (rd && SVDB) {
+          if (idx == 0) read_sub_scales(ng, ns, JN & 1);
+        }
+        if constexpr (dma) {
+#pragma unroll
+          for (int d = 0; d < PG_PS; ++d)
+            if (d * NMF / PG_PS == idx) dma_one(dst, dsl, d);
+          if (idx == 0 && wave == 0) dma_scales(dst);
+        }
+#pragma unroll
+        for (int e = idx * EPM; e < (idx + 1) * EPM; ++e) {
+          const int eg = SL * EPS + e;  // accumulator of the set
+          const int combo = eg / EPC, bb = (eg / 4) % PG_TM, rr = eg % 4;
+          const int c = combo - SL * EPS / EPC;  // combo within the sub-step's scales
+          const int aa = combo / 4, r = 4 * (combo % 4) + rr;
+          constexpr int SB = SVDB ? (J & 1) : 0;
+          const float t = term(D[1 - CS][aa][bb][r], sv[SB][c], sr[SB][c], rr);
+          facc[aa][bb][r] = facc[aa][bb][r] + t;
+          // Pins this flush element to its slot: without it the compiler sinks
+          // the whole flush of a group below the next group's MFMAs, in one
+          // VALU block that the MFMAs no longer hide (and, at 64 x 64 waves,
+          // with both versions of the set alive at once).
+          asm volatile("" : "+v"(facc[aa][bb][r]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+
+    auto wait_stage = [&]() __attribute__((always_inline)) {
+      if (wave == 0)
+        wait_vmcnt<(PG_NS - 2) * (PG_PS + 1)>();
+      else
+        wait_vmcnt<(PG_NS - 2) * PG_PS>();
+    };
+
+    i32x4 wf[2][PG_TN], xf[2][PG_TM];
+    // The zero row of the flush before the first group (read after the
+    // prologue's barrier).
+    if (tid < ROWB / 16) *reinterpret_cast<i32x4*>(smem + kZeroRow + tid * 16) = i32x4{0, 0, 0, 0};
+    // Prologue: stages 0 .. NS-1 (a stage past the end reloads stage nk-1 into
+    // a slot nobody reads, so every stage issue moves the same loads).
+#pragma unroll
+    for (int st = 0; st < PG_NS; ++st) {
+      dma_stage(min(st, nk - 1), st);
+      if (wave == 0) dma_scales(min(st, nk - 1));
+    }
+    if (wave == 0)
+      wait_vmcnt<(PG_NS - 1) * (PG_PS + 1)>();
+    else
+      wait_vmcnt<(PG_NS - 1) * PG_PS>();
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < PG_TM; ++b) read_x(0, 0, b, xf[0]);
+#pragma unroll
+    for (int a = 0; a < PG_TN; ++a) {
+      if constexpr (W4) {
+        read_w(0, 0, a, raw);
+        unpack_half(a, 0, wf[0]);
+      } else {
+        read_w(0, 0, a, wf[0]);
       }
     }
+
+    if constexpr (SVDB) read_sub_scales(-1, 0, 0);  // first flush: zero sum, zero scales
+
+    // Stage kt at position HALF (0 .. PER-1) of a PER-stage period that starts
+    // at a multiple of PER, so group parities are compile-time.  Sub-step J
+    // belongs to group (4 kt + J) / SUBG and flushes slice (4 HALF + J) % SUBG
+    // of the group before it.  LAST: the final stage (no barrier or DMA;
+    // requests sa and bias; then flushes its own last group).
+    auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
+      constexpr int HALF = decltype(halfc)::value;
+      constexpr bool LAST = decltype(lastc)::value != 0;
+      const int sl = kt % PG_NS;
+      if constexpr (LAST) {
+        sa_t = p.sa[min(m0 + tid % PG_BM, M - 1)];
+        if (p.bias) b_t = p.bias[min(n0 + tid % PG_BN, N - 1)];
+      }
+      // group of sub-step J of stage k: (4 k + J) / SUBG; it flushes the one before
+#define PG_SUB(J)                                                                            \
+    {                                                                                          \
+      constexpr int S = 4 * HALF + (J);                                                        \
+      constexpr int CS = (S / SUBG) & 1;                                                       \
+      constexpr bool FIRST = (S % SUBG) == 0;                                                  \
+      constexpr int SL = S % SUBG;                                                             \
+      const int cg = (4 * kt + (J)) / SUBG - 1;                                                \
+      const int ng = (4 * kt + (J) + 1) / SUBG - 1;                                            \
+      if constexpr ((J) < 3) {                                                                 \
+        step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[(J) & 1],       \
+             xf[(J) & 1], sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, ng, (S + 1) % SUBG,  \
+             cg);                                                                              \
+      } else if constexpr (!LAST) {                                                            \
+        wait_stage();                                                                          \
+        __syncthreads();                                                                       \
+        step(ic<CS>{}, ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1],      \
+             (kt + 1) % PG_NS, wf[0], xf[0], min(kt + PG_NS, nk - 1), sl, ng, (S + 1) % SUBG,  \
+             cg);                                                                              \
+      } else {                                                                                 \
+        step(ic<CS>{}, ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<SL>{}, ic<(J)>{}, wf[1], xf[1], 0,    \
+             wf[0], xf[0], 0, 0, 0, 0, cg);                                                    \
+      }                                                                                        \
+    }
+      PG_SUB(0)
+      PG_SUB(1)
+      PG_SUB(2)
+      PG_SUB(3)
+#undef PG_SUB
+      if constexpr (LAST) {
+        // flush the last group (set of sub-step 3), in order
+        constexpr int CSL = ((4 * HALF + 3) / SUBG) & 1;
+        const int gl = G - 1;
+#pragma unroll
+        for (int combo = 0; combo < NCOMBO; ++combo) {
+          float s4[4];
+          uint32_t r4[2];
+          read_scales(gl, combo, s4, r4);
+          const int aa = combo / 4, q = combo % 4;
+#pragma unroll
+          for (int bb = 0; bb < PG_TM; ++bb)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const float t = term(D[CSL][aa][bb][4 * q + rr], s4, r4, rr);
+              facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+            }
+        }
+      }
+    };
+
+    int kt = 0;
+    if constexpr (PER == 2) {
+      for (; kt + 2 < nk; kt += 2) {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<0>{});
+      }
+      if (kt + 1 < nk) {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<1>{});
+      } else {
+        stage(kt, ic<0>{}, ic<1>{});
+      }
+    } else {
+      // gs 256: K % 256 == 0, so nk is even and 2 or 4 stages remain
+      for (; kt + 4 < nk; kt += 4) {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<0>{});
+        stage(kt + 2, ic<2>{}, ic<0>{});
+        stage(kt + 3, ic<3>{}, ic<0>{});
+      }
+      if (kt + 2 < nk) {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<0>{});
+        stage(kt + 2, ic<2>{}, ic<0>{});
+        stage(kt + 3, ic<3>{}, ic<1>{});
+      } else {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<1>{});
+      }
+    }
+    wait_vmcnt<0>();  // reloads past the end land before LDS is reused
   };
 
-  int kt = 0;
-  if constexpr (PER == 2) {
-    for (; kt + 2 < nk; kt += 2) {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<0>{});
-    }
-    if (kt + 1 < nk) {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<1>{});
-    } else {
-      stage(kt, ic<0>{}, ic<1>{});
-    }
+  // the fast flush where its registers fit (int8 weights at two workgroups
+  // per CU would drop to one)
+  constexpr bool FASTOK = SWH && !(WF == W_I8 && OCC == 2);
+  if constexpr (FASTOK) {
+    kpass(ic<1>{});
+    // A NaN accumulator means a scale of the tile's columns was not finite
+    // (finite fp16 scales keep every fast term finite: |D * s| < 2^22 * 2^16).
+    // Then the workgroup redoes the tile with the exact flush; every wave
+    // takes part, since all of them feed the DMA ring.
+    bool bad = false;
+#pragma unroll
+    for (int a = 0; a < PG_TN; ++a)
+#pragma unroll
+      for (int b = 0; b < PG_TM; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bad = bad || __builtin_isnan(facc[a][b][r]);
+    __shared__ uint32_t vote[NW];
+    const bool wbad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    if (lane == 0) vote[wave] = wbad ? 1u : 0u;
+    __syncthreads();
+    uint32_t any = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) any |= vote[w];
+    if (any) kpass(ic<0>{});
   } else {
-    // gs 256: K % 256 == 0, so nk is even and 2 or 4 stages remain
-    for (; kt + 4 < nk; kt += 4) {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<0>{});
-      stage(kt + 2, ic<2>{}, ic<0>{});
-      stage(kt + 3, ic<3>{}, ic<0>{});
-    }
-    if (kt + 2 < nk) {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<0>{});
-      stage(kt + 2, ic<2>{}, ic<0>{});
-      stage(kt + 3, ic<3>{}, ic<1>{});
-    } else {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<1>{});
-    }
+    kpass(ic<0>{});
   }
-  wait_vmcnt<0>();  // reloads past the end land before LDS is reused
 
   // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
   float* ssa = reinterpret_cast<float*>(smem + PG_OUT);

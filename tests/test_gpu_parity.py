@@ -405,6 +405,64 @@ def test_w4a8_pergroup_full_size_rows(gs):
     assert_bits_equal(y[rows], exp, f"w4g gs{gs} full-size rows")
 
 
+# fp16 group scales take the fast flush (each group's int32 sum starts from
+# the bit pattern of 1.5 * 2^23 and one fma of those bits rounds D * s once);
+# a tile whose scales include +-inf or NaN gives NaN there and is redone with
+# the exact flush.  Special scales sit in a few columns (so some tiles stay
+# fast and some are redone), rows of zeros give D_g = 0 against the infinite
+# scales (NaN in the reference), and every tile shape runs: 128 x 128 of
+# 8 waves (gs 64, 2048 x 1280), two 128 x 64 workgroups per CU (gs 128),
+# 64 x 64 tiles (128 x 512), M = 48 and the M <= 16 weight stream.  Infinite
+# scales in group 0 also check the flush before the first group, which must
+# add +0.0 whatever group 0's scales are.
+_SPECIAL_SCALES = {(0, 6): np.inf, (0, 78): -np.inf, (1, 5): np.inf, (2, 77): -np.inf,
+                   (0, 200): np.nan, (3, 300): 0.0, (1, 301): -0.0, (0, 302): 2.0 ** -24,
+                   (2, 303): 65504.0, (1, 304): -65504.0, (0, 1100): np.inf}
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("M,N,K", [(2048, 1280, 512), (128, 512, 1024), (48, 1280, 1024),
+                                   (8, 1280, 2048)])
+def test_w4a8_pergroup_special_scales(gs, M, N, K):
+    x = O.synth_activations(M, K, 80 + M)
+    x[5, :] = 0
+    x[130 % M, :] = 0
+    w4 = np.random.default_rng(81 + N).integers(-8, 8, (N, K), dtype=np.int8)
+    w4[:, :gs] = -8                                # |D| at its largest in group 0
+    packed = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 82 + K).astype(np.float16)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        if n < N:
+            sc[g % (K // gs), n] = v
+    b = (np.random.default_rng(83).standard_normal(N) * 0.1).astype(np.float16)
+    y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs, T(b)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.w4a8_pergroup_linear(x, packed, sc, gs, b)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_bits_equal(y, exp, f"w4g special scales gs{gs} {M}x{N}x{K}")
+
+
+# The same special scales (fp32) on int8 weights: every per-group tile shape
+# and group size, including the 8-wave gs 256 tile (2048 x 1280).
+@pytest.mark.parametrize("gs", [64, 128, 256])
+@pytest.mark.parametrize("M,N,K", [(2048, 1280, 1024), (128, 512, 1024), (48, 1280, 1024),
+                                   (8, 1280, 2048)])
+def test_pergroup_special_scales(gs, M, N, K):
+    x, w, _, b = synth_pc(M, N, K, 84 + M)
+    x[5, :] = 0
+    w[:, :gs] = -127
+    sw = O.synth_scales((K // gs, N), 85 + gs)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        if n < N:
+            sw[g % (K // gs), n] = v
+    sw[1, 6] = np.float32(3.0e38)                  # the product overflows to inf
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.pergroup_linear(x, w, sw, gs, b)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_bits_equal(y, exp, f"pg special scales gs{gs} {M}x{N}x{K}")
+
+
 # Decode-sized GEMV on quantized activations (M <= 4, K <= 16384, K % 16 == 0
 # for int8 / % 32 for int4): one wave per weight row, v_dot4 products; N=17
 # leaves most waves of the last workgroup without a row.
