@@ -412,7 +412,8 @@ def test_w4a8_pergroup_full_size_rows(gs):
 # fast and some are redone), rows of zeros give D_g = 0 against the infinite
 # scales (NaN in the reference), and every tile shape runs: 128 x 128 of
 # 8 waves (gs 64, 2048 x 1280), two 128 x 64 workgroups per CU (gs 128),
-# 64 x 64 tiles (128 x 512), M = 48 and the M <= 16 weight stream.  Infinite
+# 64 x 64 tiles (128 x 512), M = 48, the M <= 16 weight stream, the decode
+# GEMV (M = 1, 3) and the register-staged kernel (N % 8 != 0).  Infinite
 # scales in group 0 also check the flush before the first group, which must
 # add +0.0 whatever group 0's scales are.
 _SPECIAL_SCALES = {(0, 6): np.inf, (0, 78): -np.inf, (1, 5): np.inf, (2, 77): -np.inf,
@@ -422,11 +423,14 @@ _SPECIAL_SCALES = {(0, 6): np.inf, (0, 78): -np.inf, (1, 5): np.inf, (2, 77): -n
 
 @pytest.mark.parametrize("gs", [64, 128])
 @pytest.mark.parametrize("M,N,K", [(2048, 1280, 512), (128, 512, 1024), (48, 1280, 1024),
-                                   (8, 1280, 2048)])
+                                   (8, 1280, 2048), (3, 1280, 2048), (1, 1280, 2048),
+                                   (300, 1004, 384)])
 def test_w4a8_pergroup_special_scales(gs, M, N, K):
     x = O.synth_activations(M, K, 80 + M)
-    x[5, :] = 0
-    x[130 % M, :] = 0
+    if M > 2:                                      # (no zero row at M <= 2)
+        x[5 % M, :] = 0
+    if M > 130:
+        x[130, :] = 0
     w4 = np.random.default_rng(81 + N).integers(-8, 8, (N, K), dtype=np.int8)
     w4[:, :gs] = -8                                # |D| at its largest in group 0
     packed = O.pack_w4_lo_first(w4)
@@ -446,10 +450,11 @@ def test_w4a8_pergroup_special_scales(gs, M, N, K):
 # and group size, including the 8-wave gs 256 tile (2048 x 1280).
 @pytest.mark.parametrize("gs", [64, 128, 256])
 @pytest.mark.parametrize("M,N,K", [(2048, 1280, 1024), (128, 512, 1024), (48, 1280, 1024),
-                                   (8, 1280, 2048)])
+                                   (8, 1280, 2048), (3, 1280, 2048), (300, 1004, 768)])
 def test_pergroup_special_scales(gs, M, N, K):
     x, w, _, b = synth_pc(M, N, K, 84 + M)
-    x[5, :] = 0
+    if M > 2:
+        x[5 % M, :] = 0
     w[:, :gs] = -127
     sw = O.synth_scales((K // gs, N), 85 + gs)
     for (g, n), v in _SPECIAL_SCALES.items():
