@@ -539,6 +539,48 @@ def test_skinny_dma_exact(M, N, K):
     assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"skinny dma w4 {M}x{N}x{K}")
 
 
+# Special activation rows through the small-M kernels (the fused decode GEMV
+# at (2, 2560, 1536), the LDS weight stream at the others): zeros (s = 1),
+# NaN (-128), one inf (s = inf: NaN and +-inf outputs), fp16 maxima,
+# subnormals; every format and epilogue against the oracle, and per-channel
+# also against the quantize and GEMM entry points called one after the other.
+@pytest.mark.parametrize("M,N,K", [(2, 2560, 1536), (5, 1000, 4096), (8, 10240, 2560),
+                                   (9, 4096, 2048), (16, 12288, 4096), (16, 64, 1536)])
+def test_small_m_special_rows(M, N, K):
+    x, w, sw, b = synth_pc(M, N, K, 170 + M)
+    x[0, :] = 0
+    x[1, :3] = [np.nan, 3.0, -6.0]
+    if M > 2:
+        x[2, 7] = np.inf
+    if M > 3:
+        x[3, :] = np.where(np.arange(K) % 3 == 0, -65504.0, 65504.0)
+    if M > 4:
+        x[4, :] = 0
+        x[4, :4] = np.array([6e-8, -1.2e-7, 3e-8, 0], np.float16)
+    with np.errstate(invalid="ignore", over="ignore"):
+        for bias in (b, None):
+            y = H(C.perchannel_linear(T(x), T(w), T(sw), None if bias is None else T(bias)))
+            assert_bits_equal(y, O.perchannel_linear(x, w, sw, bias), f"small-M pc {M}x{N}x{K}")
+            q, sa = C.quantize_per_token(T(x))
+            y2 = H(C.perchannel_gemm(q, sa, T(w), T(sw), None if bias is None else T(bias)))
+            assert_bits_equal(y, y2, f"small-M pc vs quantize + gemm {M}x{N}x{K}")
+        for gs in (64, 128, 256):
+            swg = O.synth_scales((K // gs, N), 171 + gs)
+            y = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
+            assert_bits_equal(y, O.pergroup_linear(x, w, swg, gs, b), f"small-M pg{gs} {M}x{N}x{K}")
+        w4 = np.random.default_rng(172).integers(-8, 8, (N, K), dtype=np.int8)
+        pk = O.pack_w4_lo_first(w4)
+        for gs in (64, 128):
+            sc = O.synth_scales((K // gs, N), 173 + gs).astype(np.float16)
+            y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b)))
+            assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, b),
+                              f"small-M w4g{gs} {M}x{N}x{K}")
+        wf = np.random.default_rng(174).standard_normal((K, N)).astype(np.float32)
+        packed, sw4 = O.pack_weight_int4(wf)
+        y = H(C.w4a8_linear(T(x), T(packed), T(sw4)))
+        assert_bits_equal(y, O.w4a8_linear(x, packed, sw4), f"small-M w4 {M}x{N}x{K}")
+
+
 # Per-group at mid M on small N: 64 x 64 tiles of four 32 x 32 waves, where the
 # 128-row tiles would fill at most half the CUs.  (65, 2560, 10240) leaves a
 # one-row tile, (200, 1032, 2048) a ragged row tile and N past the last
