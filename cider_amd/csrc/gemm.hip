@@ -367,7 +367,12 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
                        int gs, hipStream_t s) {
-  if (gemv_q_supported(a, wf, false)) return launch_gemv_q(a, wf, epi, gs, s);
+  // The GEMV on quantized activations for M <= 2.  At M = 3 and 4 the LDS
+  // weight stream below was ahead on every shape measured (whole linears in
+  // HIP graphs: per-channel N=10240 K=2560 M=4 9.9 against 13.5 us, per-group
+  // gs 128 10.6 against 16.3 us, W4A8 N=12288 K=4096 10.4 against 14.5 us);
+  // at M = 2 it was ahead on 7 of 10 shapes and up to 1.5 us behind on two.
+  if (a.M <= 2 && gemv_q_supported(a, wf, false)) return launch_gemv_q(a, wf, epi, gs, s);
   const bool vec = (wf == W_I4 ? a.K % 32 == 0 : a.K % 16 == 0) && a.N % 4 == 0 &&
                    aligned16(a.x) && aligned16(a.w) && aligned16(a.y) &&
                    (a.sw == nullptr || aligned16(a.sw));
