@@ -394,9 +394,12 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     // win once they fill half the CUs and M > 32, where the skinny kernel
     // moves to 4 row blocks per wave and 4 waves per workgroup (N=12288
     // K=4096 M=48, int8 gs 64: 45.1 vs 30.7 us; int4 gs 128: 36.2 vs 25.8 us),
-    // and for int8 weights at gs 128 from the smallest M (N=10240 K=2560 M=8:
-    // 16.8 vs 14.2 us).  Below that the skinny kernel keeps int4 and gs 64
-    // (N=12288 K=4096 M=16, int4 gs 128: 16.2 vs 25.7 us).
+    // and for int8 weights from the smallest M the shapes above do not take
+    // (whole linears, int8 gs 64 N=10240 K=2560 M=17 / 24 / 32: 16.1 / 16.2
+    // / 16.3 against 21.9 / 23.1 / 25.8 us on the skinny kernel; N=12288
+    // K=4096: 22.6-23.0 against 26.3-29.4 us).  Below M = 32 the skinny kernel
+    // keeps int4 weights (N=12288 K=4096 M=17, int4 gs 128: 22.8 against 29.0
+    // us on the DMA tiles; gs 64 was split by shape).
     // M <= 16 with K % 512 == 0 (K >= 1536): the weight stream through LDS
     // (skinny_dma.hip), whole linears against the kernels below: int8
     // per-channel M=16 N=2560 K=10240 13.1 vs 19.0 us (64 x 64 DMA tiles);
@@ -411,7 +414,7 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int epi, bool sw_half,
     if (a.M <= 16 && (epi == EPI_PG || wf == W_I4) && skinny_stream_supported(a, wf, epi, gs))
       return launch_skinny_stream(a, wf, epi, gs, s);
     if (dma && ((a.N + 63) / 64 >= 128 || a.M > 48)) return launch_gemm_dma(a, epi, wf, s);
-    if (dma_pg && gs != 256 && (a.N + 63) / 64 >= 128 && (a.M > 32 || (wf == W_I8 && gs == 128)))
+    if (dma_pg && gs != 256 && (a.N + 63) / 64 >= 128 && (a.M > 32 || wf == W_I8))
       return launch_gemm_dma_pg(a, gs, sw_half, wf, s);
     return launch_skinny(a, wf, epi, sw_half, gs, s);
   }

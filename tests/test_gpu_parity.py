@@ -653,11 +653,12 @@ def test_skinny_wave_splits_exact(M, N, K):
 # are loaded from the last valid row and never stored.  Per-group at >= 128 column tiles runs the 128-row per-group DMA
 # tiles for M > 32, and for int8 weights at gs 128 at every M: (16, 10240,
 # 2560) and (5, 12288, 512) int8 gs 128; (33, 8192, 1024) and (64, 8192, 512)
-# every per-group variant; the others stay on the skinny kernel ((64, 512, 4096)
+# every per-group variant, (17, 10240, 2560) and (24, 8192, 1024) int8
+# per-group at M <= 32; the others stay on the skinny kernel ((64, 512, 4096)
 # and (40, 2560, 2048): per-group with 4 row blocks and 8 waves per workgroup).
 @pytest.mark.parametrize("M,N,K", [(16, 10240, 2560), (5, 12288, 512), (33, 8192, 1024),
                                    (64, 8192, 512), (64, 512, 4096), (40, 2560, 2048),
-                                   (49, 96, 256)])
+                                   (49, 96, 256), (17, 10240, 2560), (24, 8192, 1024)])
 def test_small_m_dma_tiles(M, N, K):
     x, w, sw, b = synth_pc(M, N, K, 98 + M)
     y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
