@@ -620,6 +620,319 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   }
 }
 
+// One group set, int8 weights: the same pipeline with waves of 64 x 64
+// (TM = TN = 2) at two waves per SIMD.  Two waves on one SIMD do not overlap
+// one wave's MFMAs with the other's VALU work (a microbenchmark of 4 MFMAs +
+// 48 flush-like VALU ops per wave and iteration: 498 cycles per SIMD at two
+// waves, against 244 for the MFMAs and 302 for the VALU ops alone), so the
+// alternating second set of gemm_dma_pg_kernel buys nothing there, and its
+// registers are better spent on a wave tile twice as large: per output and
+// group 4 bytes of LDS fragment reads instead of 6, and a 256 x 128 tile
+// loads (256 + 128) x K bytes per 32 K outputs instead of 256 x K per 16 K.
+// Each group's sum D_g lives in one int32 set; the first sub-step of group g
+// flushes block row a of group g-1 (acc = acc + f32(f32(D) * s), in group
+// order, exactly as above) right before the MFMAs that start blocks (a, b) of
+// group g from C = 0.  Before the first group D is zero and the scales are the
+// zero row; the last group is flushed after the k-loop.
+template <int BM, int BN, int GS, bool SWH, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const GemmArgs p) {
+  static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
+  using C = PgCfg<BM, BN, W_I8, 1, WGM, WGN>;
+  constexpr int NW = C::NW, WM = C::WM, WN = C::WN, TM = C::TM, TN = C::TN;
+  constexpr int BK = C::BK, CH = C::CH, RPI = C::RPI, CHW = C::CHW, RPIW = C::RPIW;
+  constexpr int WI = C::WI, XI = C::XI, PS = C::PS, W_BYTES = C::W_BYTES, STAGE = C::STAGE;
+  constexpr int NS = C::NS, RING = C::RING, SSLOT = C::SSLOT, SNS = C::SNS;
+  constexpr int OUT_LD = C::OUT_LD, OUT = C::OUT;
+  constexpr int SUBG = GS / 32;                  // k sub-steps per group (a stage has 4)
+  constexpr int SRPS = SUBG < 4 ? 4 / SUBG : 1;  // scale rows a stage brings
+  constexpr int PER = SUBG < 8 ? 1 : 2;          // stages per period of group starts
+  constexpr int ESZ = SWH ? 2 : 4;
+  constexpr int CPR = BN * ESZ / 16, ROWB = BN * ESZ;
+  constexpr int NMF = TN * TM, NR = TN + TM;
+  static_assert(CPR * 16 * SRPS <= SSLOT && 64 / CPR >= SRPS, "scale rows per stage");
+  constexpr int kZeroRow = RING + (SNS - 1) * SSLOT;
+  static_assert(SNS - 1 - NS >= 2 && ROWB <= SSLOT, "zero row slot");
+  __shared__ __attribute__((aligned(1024))) int8_t smem[C::SMEM];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WGM, wn = wave / WGM;
+  const int h = lane >> 5, frow = lane & 31;
+  const int M = p.M, N = p.N, K = p.K;
+  const int G = K / GS, nk = K / BK;
+  int m0, n0;
+  tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
+
+  const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * K;
+  const int8_t* const xbase = p.x + (int64_t)m0 * K;
+  uint32_t woff[WI], xoff[XI];
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    const int row = (wave * WI + i) * RPIW + lane / CHW;
+    woff[i] = (uint32_t)((int64_t)(min(n0 + row, N - 1) - n0) * K +
+                         ((lane % CHW) ^ swz<BK>(row)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const int row = (wave * XI + i) * RPI + lane / CH;
+    xoff[i] = (uint32_t)((int64_t)(min(m0 + row, M - 1) - m0) * K +
+                         ((lane % CH) ^ swz<BK>(row)) * 16);
+  }
+  const int srow = lane / CPR;
+  const int8_t* ssrc = reinterpret_cast<const int8_t*>(p.sw) +
+                       (int64_t)min(n0 + (lane % CPR) * (16 / ESZ), N - 16 / ESZ) * ESZ;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(__attribute__((address_space(3))) int8_t*)smem);
+
+  auto dma_one = [&](int st, int slot, int d) __attribute__((always_inline)) {
+    const uint32_t sb = lds0 + (uint32_t)(slot * STAGE);
+    if (d < WI)
+      dma16s(wbase + (int64_t)st * BK, woff[d < WI ? d : 0], sb + (wave * WI + d) * 1024);
+    else
+      dma16s(xbase + (int64_t)st * BK, xoff[d >= WI ? d - WI : 0],
+             sb + W_BYTES + (wave * XI + d - WI) * 1024);
+  };
+  auto dma_scales = [&](int st) __attribute__((always_inline)) {
+    const int g = min(st * 4 / SUBG + srow, G - 1);
+    dma16(ssrc + (int64_t)g * N * ESZ, lds0 + RING + (uint32_t)((st % SNS) * SSLOT));
+  };
+  // k mapping of sub-step j for lane half h: k in [32 j + 16 h, + 16) for both
+  // operands (chunk 2j + h of the stage's 128-byte rows)
+  auto read_x = [&](int slot, int j, int b, i32x4 (&xfn)[TM]) __attribute__((always_inline)) {
+    const int8_t* Xs = smem + slot * STAGE + W_BYTES;
+    const int row = wm * WM + b * 32 + frow;
+    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + (((2 * j + h) ^ swz<BK>(row)) << 4));
+  };
+  auto read_w = [&](int slot, int j, int a, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
+    const int8_t* Ws = smem + slot * STAGE;
+    const int row = wn * WN + a * 32 + frow;
+    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * BK + (((2 * j + h) ^ swz<BK>(row)) << 4));
+  };
+  // the 4 scales of group g (g < 0: the zero row) for quad q of block a:
+  // n = wn*WN + 32a + 8q + 4h + [0..3]
+  auto read_scales = [&](int g, int a, int q, float (&s4)[4]) __attribute__((always_inline)) {
+    const int8_t* base = g < 0 ? smem + kZeroRow
+                               : smem + RING + ((g * SUBG / 4) % SNS) * SSLOT + (g % SRPS) * ROWB;
+    const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
+    if constexpr (SWH) {
+      const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
+      s4[0] = h2f((uint16_t)((uint32_t)v[0] & 0xffffu));
+      s4[1] = h2f((uint16_t)((uint32_t)v[0] >> 16));
+      s4[2] = h2f((uint16_t)((uint32_t)v[1] & 0xffffu));
+      s4[3] = h2f((uint16_t)((uint32_t)v[1] >> 16));
+    } else {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(base + nl * 4);
+      s4[0] = v[0];
+      s4[1] = v[1];
+      s4[2] = v[2];
+      s4[3] = v[3];
+    }
+  };
+
+  i32x16 D[TN][TM];
+  float facc[TN][TM][16];
+#pragma unroll
+  for (int a = 0; a < TN; ++a)
+#pragma unroll
+    for (int b = 0; b < TM; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        D[a][b][r] = 0;
+        facc[a][b][r] = 0.0f;
+      }
+  i32x16 zero16;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) zero16[r] = 0;
+  // flush of block row a (blocks (a, 0 .. TM-1)) for group g, quad by quad:
+  // four scales live at a time, each element pinned after its add so the
+  // compiler keeps the conversions next to their use
+  auto flush_row = [&](int g, int a) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float s4[4];
+      read_scales(g, a, q, s4);
+#pragma unroll
+      for (int b = 0; b < TM; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float t = (float)D[a][b][4 * q + r] * s4[r];
+          facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
+          asm volatile("" : "+v"(facc[a][b][4 * q + r]));
+        }
+    }
+  };
+
+  // One k sub-step in a fixed order: per MFMA slot (block a, b), the flush of
+  // the block's previous group (first sub-step of a group), the MFMA, one of
+  // the next sub-step's fragment reads (rd) and a share of the DMA loads of
+  // stage dst into slot dsl (dma).
+  auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, const i32x4 (&wc)[TN],
+                  const i32x4 (&xc)[TM], int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst,
+                  int dsl, int fg) __attribute__((always_inline)) {
+    constexpr bool first = decltype(firstc)::value != 0;
+    constexpr bool rd = decltype(rdc)::value != 0;
+    constexpr bool dma = decltype(dmac)::value != 0;
+    constexpr int JN = decltype(JNc)::value;
+#pragma unroll
+    for (int idx = 0; idx < NMF; ++idx) {
+      const int a = idx / TM, b = idx % TM;
+      if constexpr (first) {
+        if (b == 0) flush_row(fg, a);
+        D[a][b] = mfma32(wc[a], xc[b], zero16);
+      } else {
+        D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
+      }
+      if constexpr (rd) {
+#pragma unroll
+        for (int q = 0; q < NR; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q == 0)
+              read_w(rs, JN, 0, wn_);
+            else if (q <= TM)
+              read_x(rs, JN, q - 1, xn);
+            else
+              read_w(rs, JN, q - TM, wn_);
+          }
+      }
+      if constexpr (dma) {
+#pragma unroll
+        for (int d = 0; d < PS; ++d)
+          if (d * NMF / PS == idx) dma_one(dst, dsl, d);
+        if (idx == 0 && wave == 0) dma_scales(dst);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto wait_stage = [&]() __attribute__((always_inline)) {
+    if (wave == 0)
+      wait_vmcnt<(NS - 2) * (PS + 1)>();
+    else
+      wait_vmcnt<(NS - 2) * PS>();
+  };
+
+  i32x4 wf[2][TN], xf[2][TM];
+  if (tid < ROWB / 16) *reinterpret_cast<i32x4*>(smem + kZeroRow + tid * 16) = i32x4{0, 0, 0, 0};
+  // Prologue: stages 0 .. NS-1 (a stage past the end reloads stage nk-1 into
+  // a slot nobody reads, so every stage issue moves the same loads).
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int s2 = min(st, nk - 1);
+    const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
+#pragma unroll
+    for (int i = 0; i < WI; ++i) dma16s(wbase + (int64_t)s2 * BK, woff[i], sb + (wave * WI + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+      dma16s(xbase + (int64_t)s2 * BK, xoff[i], sb + W_BYTES + (wave * XI + i) * 1024);
+    if (wave == 0) dma_scales(s2);
+  }
+  if (wave == 0)
+    wait_vmcnt<(NS - 1) * (PS + 1)>();
+  else
+    wait_vmcnt<(NS - 1) * PS>();
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
+#pragma unroll
+  for (int a = 0; a < TN; ++a) read_w(0, 0, a, wf[0]);
+
+  float sa_t = 0.0f;
+  uint16_t b_t = 0;
+  // Stage kt at position HALF of a PER-stage period: sub-step J starts group
+  // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before.
+  auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
+    constexpr int HALF = decltype(halfc)::value;
+    constexpr bool LAST = decltype(lastc)::value != 0;
+    const int sl = kt % NS;
+    if constexpr (LAST) {
+      sa_t = p.sa[min(m0 + tid % BM, M - 1)];
+      if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
+    }
+#define PG1_SUB(J)                                                                              \
+  {                                                                                             \
+    constexpr bool FIRST = ((4 * HALF + (J)) % SUBG) == 0;                                      \
+    const int fg = (4 * kt + (J)) / SUBG - 1;                                                   \
+    if constexpr ((J) < 3) {                                                                    \
+      step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, wf[(J) & 1], xf[(J) & 1], sl,          \
+           wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, fg);                                     \
+    } else if constexpr (!LAST) {                                                               \
+      wait_stage();                                                                             \
+      __syncthreads();                                                                          \
+      step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, wf[1], xf[1], (kt + 1) % NS, wf[0], xf[0],   \
+           min(kt + NS, nk - 1), sl, fg);                                                       \
+    } else {                                                                                    \
+      step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, 0, fg);    \
+    }                                                                                           \
+  }
+    PG1_SUB(0)
+    PG1_SUB(1)
+    PG1_SUB(2)
+    PG1_SUB(3)
+#undef PG1_SUB
+  };
+  int kt = 0;
+  if constexpr (PER == 1) {
+    for (; kt + 1 < nk; ++kt) stage(kt, ic<0>{}, ic<0>{});
+    stage(kt, ic<0>{}, ic<1>{});
+  } else {
+    // gs 256: K % 256 == 0, so nk is even
+    for (; kt + 2 < nk; kt += 2) {
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<0>{});
+    }
+    stage(kt, ic<0>{}, ic<0>{});
+    stage(kt + 1, ic<1>{}, ic<1>{});
+  }
+  // the last group
+#pragma unroll
+  for (int a = 0; a < TN; ++a) flush_row(G - 1, a);
+  wait_vmcnt<0>();  // reloads past the end land before LDS is reused
+
+  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
+  float* ssa = reinterpret_cast<float*>(smem + OUT);
+  uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + BM);
+  __syncthreads();  // every wave is done with the ring
+  if (tid < BM) ssa[tid] = sa_t;
+  if (tid < BN) sbias[tid] = b_t;
+  __syncthreads();
+#pragma unroll
+  for (int a = 0; a < TN; ++a) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
+      const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+      const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[0] >> 16)),
+                           h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[1] >> 16))};
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int ml = wm * WM + b * 32 + frow;
+        const float sam = ssa[ml];
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = facc[a][b][4 * q + r] * sam;
+          if (p.bias) v = v + bv[r];
+          o[r] = v;
+        }
+        *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
+            i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int LPR = BN / 8, RPS = 64 / LPR;
+  const int cl = (lane % LPR) * 8;
+  const int n = n0 + cl;
+#pragma unroll 4
+  for (int rr = wave * RPS + lane / LPR; rr < BM; rr += NW * RPS) {
+    const int m = m0 + rr;
+    if (m < M && n < N)
+      *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
+          *reinterpret_cast<const i32x4*>(smem + rr * OUT_LD + cl * 2);
+  }
+}
+
 // Eligible: int8 or int4 weights, per-group gs 64 / 128 (gs 256: int8 and
 // K % 256 == 0), K % 128 == 0, N % 8 == 0, 16-byte aligned operands
 // (launch_gemm checks).
@@ -656,6 +969,24 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
       if (gs == 128) return run_pg64<128, false, W_I8>(a, s);
       return run_pg64<256, false, W_I8>(a, s);
     }
+  }
+  if (wf == W_I8 && !sw_half &&
+      (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128) >= 4 * (int64_t)num_cus()) {
+    // int8 weights with fp32 scales on grids of at least four rounds of
+    // 256 x 128 tiles: the one-set kernel's 64 x 64 waves (M=4096 N=10240
+    // K=2560: gs 128 188.5 -> 164.2 us, gs 64 228.8 -> 211.0 us, gs 256 163.2
+    // -> 148.4 us; M=8192 gs 64 446 -> 422 us).  Its larger tiles lost where
+    // they make one or two rounds with a partial one (M=1024 N=10240 K=2560
+    // gs 128: 59.3 against 51.3 us; M=4096 N=2560 K=10240: 204 against 173
+    // us) and were level at 2.5 rounds (M=2048).
+    const int tiles = ((a.M + 255) / 256) * ((a.N + 127) / 128);
+    if (gs == 64)
+      gemm_dma_pg1_kernel<256, 128, 64, false, 4, 2><<<tiles, 512, 0, s>>>(a);
+    else if (gs == 128)
+      gemm_dma_pg1_kernel<256, 128, 128, false, 4, 2><<<tiles, 512, 0, s>>>(a);
+    else
+      gemm_dma_pg1_kernel<256, 128, 256, false, 4, 2><<<tiles, 512, 0, s>>>(a);
+    return hipGetLastError();
   }
   if (gs == 256) {
     // int8 weights only (the W4A8 formats define gs 64 / 128); the 8-wave

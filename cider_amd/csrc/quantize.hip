@@ -9,8 +9,8 @@
 // MI355X design: one 64-lane wavefront owns one row, so the absmax is a pure
 // cross-lane reduction (no LDS, no barrier); a workgroup of 4 waves handles 4
 // rows.  Up to 64 rows (decode-sized batches) get a 1024-thread workgroup per
-// row instead, and rows of 2048 to 16384 elements a 256-thread one at any
-// M.  A row stays in registers between the absmax and the quantize pass
+// row instead, and rows of 2048 to 16384 elements a 256-thread one, except
+// at M >= 2048 with rows of at most 3072 elements.  A row stays in registers between the absmax and the quantize pass
 // (each element is read from HBM once); rows past 16384 elements are re-read,
 // which hits in L2.
 #include "common.hpp"
@@ -142,7 +142,12 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
     return hipGetLastError();
   }
   const int per_lane = (nvec + kWave - 1) / kWave;
-  if (nvec >= 256 && nvec <= 8 * 256) {
+  // Many rows of up to 3072 elements: one wave per row, the row in at most 6
+  // vectors per lane (4096 x 2560: 7.5 -> 6.4 us, 8192 x 2560: 13.0 -> 11.4
+  // us, 4096 x 2048: 6.8 -> 5.4 us against the 256-thread row workgroups;
+  // level at M <= 1024).
+  const bool wave_rows = M >= 2048 && per_lane <= 6;
+  if (!wave_rows && nvec >= 256 && nvec <= 8 * 256) {
     // Rows of 2048 .. 16384 elements at any M: a 256-thread workgroup per
     // row, its four waves' maxima meeting in LDS.  One wave per row held up
     // to 32 16-byte vectors per lane and ran at few waves per SIMD (4096 x
@@ -162,6 +167,10 @@ hipError_t launch_quantize(const uint16_t* x, int8_t* q, float* sa, int M,
     quantize_vec_kernel<2><<<grid, block, 0, s>>>(x, q, sa, M, K);
   else if (per_lane <= 4)
     quantize_vec_kernel<4><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 5)
+    quantize_vec_kernel<5><<<grid, block, 0, s>>>(x, q, sa, M, K);
+  else if (per_lane <= 6)
+    quantize_vec_kernel<6><<<grid, block, 0, s>>>(x, q, sa, M, K);
   else if (per_lane <= 8)
     quantize_vec_kernel<8><<<grid, block, 0, s>>>(x, q, sa, M, K);
   else if (per_lane <= 16)

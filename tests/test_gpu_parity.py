@@ -468,6 +468,30 @@ def test_pergroup_special_scales(gs, M, N, K):
     assert_bits_equal(y, exp, f"pg special scales gs{gs} {M}x{N}x{K}")
 
 
+# Grids of at least four rounds of 256 x 128 tiles run the one-set per-group
+# kernel (64 x 64 waves, int8 weights, fp32 scales): ragged M and N (the last
+# tile row and column partly outside), every group size, special scales in
+# the first and the last tile column; rows of the first tile row, across the
+# first tile-row boundary, in the middle and of the last tile row.
+@pytest.mark.parametrize("gs", [64, 128, 256])
+def test_pergroup_one_set_tiles(gs):
+    M, N, K = 4059, 8200, 768                      # 16 x 65 tiles of 256 x 128
+    x, w, _, b = synth_pc(M, N, K, 86 + gs)
+    x[5, :] = 0
+    w[:, :gs] = -127
+    sw = O.synth_scales((K // gs, N), 87 + gs)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        sw[g % (K // gs), n] = v
+        sw[(g + 1) % (K // gs), N - 1 - n % 64] = v
+    sw[1, 6] = np.float32(3.0e38)                  # the product overflows to inf
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    rows = np.r_[0:8, 250:262, 2000:2004, M - 27:M]
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_bits_equal(y[rows], exp, f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
+
+
 # Decode-sized GEMV on quantized activations (M <= 4, K <= 16384, K % 16 == 0
 # for int8 / % 32 for int4): one wave per weight row, v_dot4 products; N=17
 # leaves most waves of the last workgroup without a row.
