@@ -620,7 +620,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   }
 }
 
-// One group set, int8 weights: the same pipeline with waves of 64 x 64
+// One group set (int8 or int4 weights): the same pipeline with waves of 64 x 64
 // (TM = TN = 2) at two waves per SIMD.  Two waves on one SIMD do not overlap
 // one wave's MFMAs with the other's VALU work (a microbenchmark of 4 MFMAs +
 // 48 flush-like VALU ops per wave and iteration: 498 cycles per SIMD at two
@@ -634,10 +634,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 // order, exactly as above) right before the MFMAs that start blocks (a, b) of
 // group g from C = 0.  Before the first group D is zero and the scales are the
 // zero row; the last group is flushed after the k-loop.
-template <int BM, int BN, int GS, bool SWH, int WGM, int WGN>
+template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
-  using C = PgCfg<BM, BN, W_I8, 1, WGM, WGN>;
+  using C = PgCfg<BM, BN, WF, 1, WGM, WGN>;
+  constexpr bool W4 = (WF == W_I4);
+  constexpr int WB = C::WB;
   constexpr int NW = C::NW, WM = C::WM, WN = C::WN, TM = C::TM, TN = C::TN;
   constexpr int BK = C::BK, CH = C::CH, RPI = C::RPI, CHW = C::CHW, RPIW = C::RPIW;
   constexpr int WI = C::WI, XI = C::XI, PS = C::PS, W_BYTES = C::W_BYTES, STAGE = C::STAGE;
@@ -663,14 +665,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
   int m0, n0;
   tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
 
-  const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * K;
+  const int64_t ldw = W4 ? (K >> 1) : K;
+  const int8_t* const wbase = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n0 * ldw;
   const int8_t* const xbase = p.x + (int64_t)m0 * K;
   uint32_t woff[WI], xoff[XI];
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     const int row = (wave * WI + i) * RPIW + lane / CHW;
-    woff[i] = (uint32_t)((int64_t)(min(n0 + row, N - 1) - n0) * K +
-                         ((lane % CHW) ^ swz<BK>(row)) * 16);
+    woff[i] = (uint32_t)((int64_t)(min(n0 + row, N - 1) - n0) * ldw +
+                         ((lane % CHW) ^ swz<WB>(row)) * 16);
   }
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
@@ -687,7 +690,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
   auto dma_one = [&](int st, int slot, int d) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + (uint32_t)(slot * STAGE);
     if (d < WI)
-      dma16s(wbase + (int64_t)st * BK, woff[d < WI ? d : 0], sb + (wave * WI + d) * 1024);
+      dma16s(wbase + (int64_t)st * WB, woff[d < WI ? d : 0], sb + (wave * WI + d) * 1024);
     else
       dma16s(xbase + (int64_t)st * BK, xoff[d >= WI ? d - WI : 0],
              sb + W_BYTES + (wave * XI + d - WI) * 1024);
@@ -696,17 +699,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
     const int g = min(st * 4 / SUBG + srow, G - 1);
     dma16(ssrc + (int64_t)g * N * ESZ, lds0 + RING + (uint32_t)((st % SNS) * SSLOT));
   };
-  // k mapping of sub-step j for lane half h: k in [32 j + 16 h, + 16) for both
-  // operands (chunk 2j + h of the stage's 128-byte rows)
+  // k mapping of sub-step j for lane half h (the same for both operands):
+  //   int8 weights: k in [32 j + 16 h, + 16)               (X chunk 2j + h)
+  //   int4 weights: k in [64 (j/2) + 32 h + 16 (j%2), + 16) (X chunk
+  //     4 (j/2) + 2h + j%2; the W4 chunk 2 (j/2) + h holds the pair's 32
+  //     nibbles, read once per pair, half j%2 unpacked per sub-step)
   auto read_x = [&](int slot, int j, int b, i32x4 (&xfn)[TM]) __attribute__((always_inline)) {
     const int8_t* Xs = smem + slot * STAGE + W_BYTES;
     const int row = wm * WM + b * 32 + frow;
-    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + (((2 * j + h) ^ swz<BK>(row)) << 4));
+    const int c = W4 ? 4 * (j / 2) + 2 * h + (j % 2) : 2 * j + h;
+    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + ((c ^ swz<BK>(row)) << 4));
   };
+  // int8: fragment of W block a for sub-step j;  int4: the raw 16-byte chunk
+  // of W block a for the sub-step pair j / 2
   auto read_w = [&](int slot, int j, int a, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
     const int8_t* Ws = smem + slot * STAGE;
     const int row = wn * WN + a * 32 + frow;
-    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * BK + (((2 * j + h) ^ swz<BK>(row)) << 4));
+    const int c = W4 ? 2 * (j / 2) + h : 2 * j + h;
+    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * WB + ((c ^ swz<WB>(row)) << 4));
+  };
+  i32x4 raw[TN];  // int4 only: packed chunks of the current sub-step pair
+  auto unpack_half = [&](int a, int half, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
+    dst[a] = half == 0 ? pg_unpack_w4_8((uint32_t)raw[a][0], (uint32_t)raw[a][1])
+                       : pg_unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
   };
   // the 4 scales of group g (g < 0: the zero row) for quad q of block a:
   // n = wn*WN + 32a + 8q + 4h + [0..3]
@@ -745,7 +760,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
   for (int r = 0; r < 16; ++r) zero16[r] = 0;
   // flush of block row a (blocks (a, 0 .. TM-1)) for group g, quad by quad:
   // four scales live at a time, each element pinned after its add so the
-  // compiler keeps the conversions next to their use
+  // compiler keeps the conversions next to their use.  (The fast flush of
+  // fp16 scales, one fma per term from a biased sum, measured slower here:
+  // int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
   auto flush_row = [&](int g, int a) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -782,7 +799,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
       } else {
         D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
       }
-      if constexpr (rd) {
+      if constexpr (rd && !W4) {
 #pragma unroll
         for (int q = 0; q < NR; ++q)
           if ((q < NMF ? q : NMF - 1) == idx) {
@@ -793,6 +810,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
             else
               read_w(rs, JN, q - TM, wn_);
           }
+      }
+      if constexpr (rd && W4) {
+        // X fragments first; on a new pair the raw W chunks next, each
+        // unpacked in a later slot than its read (the slots issue reads
+        // before unpacks); otherwise the held chunks' second halves
+        constexpr bool new_pair = (JN % 2) == 0;
+        constexpr int NRD = TM + (new_pair ? TN : 0);
+#pragma unroll
+        for (int q = 0; q < NRD; ++q)
+          if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q < TM)
+              read_x(rs, JN, q, xn);
+            else
+              read_w(rs, JN, q - TM, raw);
+          }
+#pragma unroll
+        for (int a2 = 0; a2 < TN; ++a2) {
+          constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
+          const int want = first_slot + a2 > TM + a2 || !new_pair ? first_slot + a2 : TM + a2;
+          if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
+        }
       }
       if constexpr (dma) {
 #pragma unroll
@@ -819,7 +857,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
     const int s2 = min(st, nk - 1);
     const uint32_t sb = lds0 + (uint32_t)(st * STAGE);
 #pragma unroll
-    for (int i = 0; i < WI; ++i) dma16s(wbase + (int64_t)s2 * BK, woff[i], sb + (wave * WI + i) * 1024);
+    for (int i = 0; i < WI; ++i) dma16s(wbase + (int64_t)s2 * WB, woff[i], sb + (wave * WI + i) * 1024);
 #pragma unroll
     for (int i = 0; i < XI; ++i)
       dma16s(xbase + (int64_t)s2 * BK, xoff[i], sb + W_BYTES + (wave * XI + i) * 1024);
@@ -833,7 +871,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
 #pragma unroll
   for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
 #pragma unroll
-  for (int a = 0; a < TN; ++a) read_w(0, 0, a, wf[0]);
+  for (int a = 0; a < TN; ++a) {
+    if constexpr (W4) {
+      read_w(0, 0, a, raw);
+      unpack_half(a, 0, wf[0]);
+    } else {
+      read_w(0, 0, a, wf[0]);
+    }
+  }
 
   float sa_t = 0.0f;
   uint16_t b_t = 0;
@@ -970,23 +1015,37 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
       return run_pg64<256, false, W_I8>(a, s);
     }
   }
-  if (wf == W_I8 && !sw_half &&
-      (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128) >= 4 * (int64_t)num_cus()) {
-    // int8 weights with fp32 scales on grids of at least four rounds of
-    // 256 x 128 tiles: the one-set kernel's 64 x 64 waves (M=4096 N=10240
-    // K=2560: gs 128 188.5 -> 164.2 us, gs 64 228.8 -> 211.0 us, gs 256 163.2
-    // -> 148.4 us; M=8192 gs 64 446 -> 422 us).  Its larger tiles lost where
-    // they make one or two rounds with a partial one (M=1024 N=10240 K=2560
-    // gs 128: 59.3 against 51.3 us; M=4096 N=2560 K=10240: 204 against 173
-    // us) and were level at 2.5 rounds (M=2048).
-    const int tiles = ((a.M + 255) / 256) * ((a.N + 127) / 128);
-    if (gs == 64)
-      gemm_dma_pg1_kernel<256, 128, 64, false, 4, 2><<<tiles, 512, 0, s>>>(a);
-    else if (gs == 128)
-      gemm_dma_pg1_kernel<256, 128, 128, false, 4, 2><<<tiles, 512, 0, s>>>(a);
-    else
-      gemm_dma_pg1_kernel<256, 128, 256, false, 4, 2><<<tiles, 512, 0, s>>>(a);
-    return hipGetLastError();
+  {
+    // The one-set kernel's 64 x 64 waves in 256 x 128 tiles, for int8 weights
+    // with fp32 scales and int4 weights with fp16 scales, on grids of at least
+    // three rounds, or two without a partial one.  M=4096 N=10240 K=2560 (5
+    // rounds): gs 128 188.5 -> 164.2 us, gs 64 228.8 -> 211.0 us, gs 256
+    // 163.2 -> 148.4 us; int4 M=4096 N=12288 K=4096 (6): gs 128 368.8 ->
+    // 340.8 us, gs 64 478.4 -> 464.7 us; int4 M=4096 N=4096 K=12288 (2):
+    // gs 128 361.6 -> 322.6 us, gs 64 level; int4 M=2048 N=12288 K=4096 (3):
+    // gs 128 191.3 -> 172.0 us.  Its larger tiles lost where they make one or
+    // two rounds with a partial one (M=1024 N=10240 K=2560 gs 128: 59.3
+    // against 51.3 us; M=4096 N=2560 K=10240: 204 against 173 us) and were
+    // level at 2.5 rounds (M=2048 N=10240 K=2560).
+    const int64_t tiles = (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128);
+    const int64_t cus = num_cus(), rounds = tiles / cus;
+    const bool fmt = (wf == W_I8 && !sw_half) || (wf == W_I4 && sw_half && gs != 256);
+    if (fmt && (rounds >= 3 || (rounds == 2 && tiles % cus == 0))) {
+      const unsigned grid = (unsigned)tiles;
+      if (wf == W_I4) {
+        if (gs == 64)
+          gemm_dma_pg1_kernel<256, 128, 64, true, W_I4, 4, 2><<<grid, 512, 0, s>>>(a);
+        else
+          gemm_dma_pg1_kernel<256, 128, 128, true, W_I4, 4, 2><<<grid, 512, 0, s>>>(a);
+      } else if (gs == 64) {
+        gemm_dma_pg1_kernel<256, 128, 64, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+      } else if (gs == 128) {
+        gemm_dma_pg1_kernel<256, 128, 128, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+      } else {
+        gemm_dma_pg1_kernel<256, 128, 256, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+      }
+      return hipGetLastError();
+    }
   }
   if (gs == 256) {
     // int8 weights only (the W4A8 formats define gs 64 / 128); the 8-wave

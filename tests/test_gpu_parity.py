@@ -492,6 +492,28 @@ def test_pergroup_one_set_tiles(gs):
     assert_bits_equal(y[rows], exp, f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
 
 
+# The same kernel with int4 weights and fp16 group scales.
+@pytest.mark.parametrize("gs", [64, 128])
+def test_w4a8_pergroup_one_set_tiles(gs):
+    M, N, K = 4059, 8200, 768
+    x = O.synth_activations(M, K, 88 + gs)
+    x[5, :] = 0
+    w4 = np.random.default_rng(89).integers(-8, 8, (N, K), dtype=np.int8)
+    w4[:, :gs] = -8
+    packed = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 90 + gs).astype(np.float16)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        sc[g % (K // gs), n] = v
+        sc[(g + 1) % (K // gs), N - 1 - n % 64] = v
+    b = (np.random.default_rng(91).standard_normal(N) * 0.1).astype(np.float16)
+    y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs, T(b)))
+    rows = np.r_[0:8, 250:262, 2000:2004, M - 27:M]
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.w4a8_pergroup_linear(x[rows], packed, sc, gs, b)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_bits_equal(y[rows], exp, f"w4g one-set tiles gs{gs} {M}x{N}x{K} rows")
+
+
 # Decode-sized GEMV on quantized activations (M <= 4, K <= 16384, K % 16 == 0
 # for int8 / % 32 for int4): one wave per weight row, v_dot4 products; N=17
 # leaves most waves of the last workgroup without a row.
