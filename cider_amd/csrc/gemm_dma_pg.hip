@@ -758,35 +758,43 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
   i32x16 zero16;
 #pragma unroll
   for (int r = 0; r < 16; ++r) zero16[r] = 0;
-  // flush of block row a (blocks (a, 0 .. TM-1)) for group g, quad by quad:
-  // four scales live at a time, each element pinned after its add so the
-  // compiler keeps the conversions next to their use.  (The fast flush of
-  // fp16 scales, one fma per term from a biased sum, measured slower here:
-  // int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
-  auto flush_row = [&](int g, int a) __attribute__((always_inline)) {
+  // The scales of the next flush, read from LDS one sub-step ahead (read
+  // next to the flush, each quad's LDS latency stood exposed before its
+  // terms).
+  float svp[TN][4][4];
+  auto prefetch = [&](int g) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float s4[4];
-      read_scales(g, a, q, s4);
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) read_scales(g, a, q, svp[a][q]);
+  };
+  // flush of block row a (blocks (a, 0 .. TM-1)), each element pinned after
+  // its add so the compiler keeps the conversions next to their use.  (The
+  // fast flush of fp16 scales, one fma per term from a biased sum, measured
+  // slower here: int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
+  auto flush_row = [&](int a) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
 #pragma unroll
       for (int b = 0; b < TM; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float t = (float)D[a][b][4 * q + r] * s4[r];
+          const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
           facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
           asm volatile("" : "+v"(facc[a][b][4 * q + r]));
         }
-    }
   };
 
   // One k sub-step in a fixed order: per MFMA slot (block a, b), the flush of
   // the block's previous group (first sub-step of a group), the MFMA, one of
   // the next sub-step's fragment reads (rd) and a share of the DMA loads of
-  // stage dst into slot dsl (dma).
-  auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, const i32x4 (&wc)[TN],
+  // stage dst into slot dsl (dma); before a sub-step that flushes (pre), the
+  // scales of group pg after the first MFMA.
+  auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, auto prec, const i32x4 (&wc)[TN],
                   const i32x4 (&xc)[TM], int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst,
-                  int dsl, int fg) __attribute__((always_inline)) {
+                  int dsl, int pg) __attribute__((always_inline)) {
     constexpr bool first = decltype(firstc)::value != 0;
+    constexpr bool pre = decltype(prec)::value != 0;
     constexpr bool rd = decltype(rdc)::value != 0;
     constexpr bool dma = decltype(dmac)::value != 0;
     constexpr int JN = decltype(JNc)::value;
@@ -794,7 +802,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
     for (int idx = 0; idx < NMF; ++idx) {
       const int a = idx / TM, b = idx % TM;
       if constexpr (first) {
-        if (b == 0) flush_row(fg, a);
+        if (b == 0) flush_row(a);
         D[a][b] = mfma32(wc[a], xc[b], zero16);
       } else {
         D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
@@ -838,6 +846,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
           if (d * NMF / PS == idx) dma_one(dst, dsl, d);
         if (idx == 0 && wave == 0) dma_scales(dst);
       }
+      if constexpr (pre) {
+        if (idx == 0) prefetch(pg);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -879,11 +890,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
       read_w(0, 0, a, wf[0]);
     }
   }
+  prefetch(-1);  // the first flush: zero sums, zero scales
 
   float sa_t = 0.0f;
   uint16_t b_t = 0;
   // Stage kt at position HALF of a PER-stage period: sub-step J starts group
-  // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before.
+  // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before;
+  // the sub-step before it reads that group's scales (PRE).
   auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
     constexpr int HALF = decltype(halfc)::value;
     constexpr bool LAST = decltype(lastc)::value != 0;
@@ -895,17 +908,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
 #define PG1_SUB(J)                                                                              \
   {                                                                                             \
     constexpr bool FIRST = ((4 * HALF + (J)) % SUBG) == 0;                                      \
-    const int fg = (4 * kt + (J)) / SUBG - 1;                                                   \
+    constexpr bool PRE = ((4 * HALF + (J) + 1) % SUBG) == 0;                                    \
+    const int pg = (4 * kt + (J) + 1) / SUBG - 1;                                               \
     if constexpr ((J) < 3) {                                                                    \
-      step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, wf[(J) & 1], xf[(J) & 1], sl,          \
-           wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, fg);                                     \
+      step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, ic<PRE>{}, wf[(J) & 1], xf[(J) & 1],   \
+           sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, pg);                                 \
     } else if constexpr (!LAST) {                                                               \
       wait_stage();                                                                             \
       __syncthreads();                                                                          \
-      step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, wf[1], xf[1], (kt + 1) % NS, wf[0], xf[0],   \
-           min(kt + NS, nk - 1), sl, fg);                                                       \
+      step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], (kt + 1) % NS,      \
+           wf[0], xf[0], min(kt + NS, nk - 1), sl, pg);                                         \
     } else {                                                                                    \
-      step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, 0, fg);    \
+      step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, \
+           0, pg);                                                                              \
     }                                                                                           \
   }
     PG1_SUB(0)
@@ -927,9 +942,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const G
     stage(kt, ic<0>{}, ic<0>{});
     stage(kt + 1, ic<1>{}, ic<1>{});
   }
-  // the last group
+  // the last group (its scales were read in the last sub-step)
 #pragma unroll
-  for (int a = 0; a < TN; ++a) flush_row(G - 1, a);
+  for (int a = 0; a < TN; ++a) flush_row(a);
   wait_vmcnt<0>();  // reloads past the end land before LDS is reused
 
   // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
