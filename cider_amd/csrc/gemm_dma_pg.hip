@@ -621,23 +621,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 }
 
 // One group set (int8 or int4 weights): the same pipeline with waves of 64 x 64
-// (TM = TN = 2) at two waves per SIMD.  Two waves on one SIMD do not overlap
-// one wave's MFMAs with the other's VALU work (a microbenchmark of 4 MFMAs +
-// 48 flush-like VALU ops per wave and iteration: 498 cycles per SIMD at two
-// waves, against 244 for the MFMAs and 302 for the VALU ops alone), so the
-// alternating second set of gemm_dma_pg_kernel buys nothing there, and its
-// registers are better spent on a wave tile twice as large: per output and
-// group 4 bytes of LDS fragment reads instead of 6, and a 256 x 128 tile
-// loads (256 + 128) x K bytes per 32 K outputs instead of 256 x K per 16 K.
+// (TM = TN = 2) at two waves per SIMD (launched as 128 x 128 tiles of four
+// waves, two workgroups per CU).  Two waves on one SIMD do not overlap one
+// wave's MFMAs with the other's VALU work when both mix them (a
+// microbenchmark of 4 MFMAs + 48 flush-like VALU ops per wave and iteration:
+// 498 cycles per SIMD at two waves, against 244 for the MFMAs and 302 for the
+// VALU ops alone), so the alternating second set of gemm_dma_pg_kernel buys
+// little there, and its registers are better spent on a wave tile twice as
+// large: per output and group 4 bytes of LDS fragment reads instead of 6.
 // Each group's sum D_g lives in one int32 set; the first sub-step of group g
 // flushes block row a of group g-1 (acc = acc + f32(f32(D) * s), in group
 // order, exactly as above) right before the MFMAs that start blocks (a, b) of
-// group g from C = 0.  Before the first group D is zero and the scales are the
-// zero row; the last group is flushed after the k-loop.
-template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_dma_pg1_kernel(const GemmArgs p) {
+// group g from C = 0, with scales read into registers during the sub-step
+// before.  Before the first group D is zero and the scales are the zero row;
+// the last group is flushed after the k-loop.
+template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN, int OCC = 1>
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
-  using C = PgCfg<BM, BN, WF, 1, WGM, WGN>;
+  using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
   constexpr bool W4 = (WF == W_I4);
   constexpr int WB = C::WB;
   constexpr int NW = C::NW, WM = C::WM, WN = C::WN, TM = C::TM, TN = C::TN;
@@ -1031,33 +1032,35 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
     }
   }
   {
-    // The one-set kernel's 64 x 64 waves in 256 x 128 tiles, for int8 weights
-    // with fp32 scales and int4 weights with fp16 scales, on grids of at least
-    // three rounds, or two without a partial one.  M=4096 N=10240 K=2560 (5
-    // rounds): gs 128 188.5 -> 164.2 us, gs 64 228.8 -> 211.0 us, gs 256
-    // 163.2 -> 148.4 us; int4 M=4096 N=12288 K=4096 (6): gs 128 368.8 ->
-    // 340.8 us, gs 64 478.4 -> 464.7 us; int4 M=4096 N=4096 K=12288 (2):
-    // gs 128 361.6 -> 322.6 us, gs 64 level; int4 M=2048 N=12288 K=4096 (3):
-    // gs 128 191.3 -> 172.0 us.  Its larger tiles lost where they make one or
-    // two rounds with a partial one (M=1024 N=10240 K=2560 gs 128: 59.3
-    // against 51.3 us; M=4096 N=2560 K=10240: 204 against 173 us) and were
-    // level at 2.5 rounds (M=2048 N=10240 K=2560).
-    const int64_t tiles = (int64_t)((a.M + 255) / 256) * ((a.N + 127) / 128);
-    const int64_t cus = num_cus(), rounds = tiles / cus;
+    // The one-set kernel: 128 x 128 tiles of four 64 x 64 waves, two
+    // workgroups per CU, for int8 weights with fp32 scales and int4 weights
+    // with fp16 scales, once its tiles fill the 512 workgroup slots (bit-
+    // identical to the kernels below).  Against the two-set kernel's tiles
+    // (weights from HBM where they exceed the MALL): M=4096 N=10240 K=2560 gs
+    // 128 188.5 -> 153.9 us, gs 64 228.8 -> 197.4 us, gs 256 163.2 -> 136.5
+    // us; M=4096 N=2560 K=10240 gs 128 171.1 -> 159.1 us; M=1024 N=10240
+    // K=2560 gs 128 49.4 -> 46.7 us; M=2048 95.3 -> 79.7 us; int4 M=4096
+    // N=12288 K=4096 gs 128 368.8 -> 337.3 us, gs 64 478.4 -> 430.0 us; int4
+    // M=1024 N=12288 K=4096 gs 128 95.9 -> 90.5 us.  256 x 128 tiles of 8
+    // waves (one workgroup per CU) ran level at five rounds and up to 20 %
+    // slower where their grid leaves a partial round; below one round of
+    // 128 x 128 tiles the two-set kernel stayed ahead on some shapes (int4
+    // M=512 N=12288 K=4096 gs 128: 52.3 against 55.8 us).
+    const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128);
     const bool fmt = (wf == W_I8 && !sw_half) || (wf == W_I4 && sw_half && gs != 256);
-    if (fmt && (rounds >= 3 || (rounds == 2 && tiles % cus == 0))) {
+    if (fmt && tiles >= 2 * (int64_t)num_cus()) {
       const unsigned grid = (unsigned)tiles;
       if (wf == W_I4) {
         if (gs == 64)
-          gemm_dma_pg1_kernel<256, 128, 64, true, W_I4, 4, 2><<<grid, 512, 0, s>>>(a);
+          gemm_dma_pg1_kernel<128, 128, 64, true, W_I4, 2, 2, 2><<<grid, 256, 0, s>>>(a);
         else
-          gemm_dma_pg1_kernel<256, 128, 128, true, W_I4, 4, 2><<<grid, 512, 0, s>>>(a);
+          gemm_dma_pg1_kernel<128, 128, 128, true, W_I4, 2, 2, 2><<<grid, 256, 0, s>>>(a);
       } else if (gs == 64) {
-        gemm_dma_pg1_kernel<256, 128, 64, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 64, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
       } else if (gs == 128) {
-        gemm_dma_pg1_kernel<256, 128, 128, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 128, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
       } else {
-        gemm_dma_pg1_kernel<256, 128, 256, false, W_I8, 4, 2><<<grid, 512, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 256, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
       }
       return hipGetLastError();
     }

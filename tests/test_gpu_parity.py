@@ -468,14 +468,14 @@ def test_pergroup_special_scales(gs, M, N, K):
     assert_bits_equal(y, exp, f"pg special scales gs{gs} {M}x{N}x{K}")
 
 
-# Grids of at least four rounds of 256 x 128 tiles run the one-set per-group
-# kernel (64 x 64 waves, int8 weights, fp32 scales): ragged M and N (the last
+# Grids of at least 512 tiles of 128 x 128 run the one-set per-group kernel
+# (64 x 64 waves, int8 weights with fp32 scales): ragged M and N (the last
 # tile row and column partly outside), every group size, special scales in
-# the first and the last tile column; rows of the first tile row, across the
-# first tile-row boundary, in the middle and of the last tile row.
+# the first and the last tile column; rows of the first tile row, across
+# tile-row boundaries, in the middle and of the last tile row.
 @pytest.mark.parametrize("gs", [64, 128, 256])
 def test_pergroup_one_set_tiles(gs):
-    M, N, K = 4059, 8200, 768                      # 16 x 65 tiles of 256 x 128
+    M, N, K = 4059, 8200, 768                      # 32 x 65 tiles of 128 x 128
     x, w, _, b = synth_pc(M, N, K, 86 + gs)
     x[5, :] = 0
     w[:, :gs] = -127
