@@ -492,6 +492,20 @@ def test_pergroup_one_set_tiles(gs):
     assert_bits_equal(y[rows], exp, f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
 
 
+# The one-set kernel at its shortest k-loops: one and two stages of 128 (the
+# loop body never runs; the prologue's reload of the last stage fills the
+# second ring slot), 512 tiles of 128 x 128.
+@pytest.mark.parametrize("gs,K", [(64, 128), (128, 128), (64, 256), (128, 256), (256, 256)])
+def test_pergroup_one_set_short_k(gs, K):
+    M, N = 2048, 4096
+    x, w, _, b = synth_pc(M, N, K, 92 + gs + K)
+    sw = O.synth_scales((K // gs, N), 93 + gs)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    rows = np.r_[0:4, 1020:1030, M - 6:M]
+    exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
+    assert_bits_equal(y[rows], exp, f"pg one-set short K gs{gs} {M}x{N}x{K} rows")
+
+
 # The same kernel with int4 weights and fp16 group scales.
 @pytest.mark.parametrize("gs", [64, 128])
 def test_w4a8_pergroup_one_set_tiles(gs):
