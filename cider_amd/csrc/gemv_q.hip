@@ -281,6 +281,166 @@ hipError_t run_m(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s) {
   }
 }
 
+
+// ---- M == 1, int4 weights, per-group fp16 scales, x quantized in the kernel:
+// the streaming layout of the decode MV (mv_stream.hip) instead of one wave
+// per row.  A wave owns R consecutive weight rows (R * K / 2 contiguous
+// bytes) and lane l requests the 16-byte chunks l, l + 64, ..., l + 64 (C - 1)
+// of them at entry, so each lane has C loads in flight (the one-row waves
+// above have K / 2048, two at K = 4096).  Each workgroup quantizes x (the
+// quantize kernel's helpers: the same q and scale) into LDS and stages the
+// fp16 group scales of its NW * R rows as 16-byte vectors.  A chunk is 32 k of
+// one row and one group (gs 64 / 128), the CPG chunks of a group sit in
+// consecutive lanes: D_g is their shuffle sum (exact int32), its term
+// f32(f32(D_g) * s) goes to LDS, and one lane per row chains the terms in
+// group order, then y = h(f32(chain * sa) (+ bias)), as the kernel above.
+template <int R, int C, int GS, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __restrict__ x16,
+                                                            const uint8_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ sw,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ y, int N) {
+  constexpr int NT = 64 * NW;
+  constexpr int RB = 1024 * C / R, K = 2 * RB;  // bytes per weight row, k per row
+  constexpr int CPR = RB / 16, CPG = GS / 32, G = K / GS;
+  constexpr int WR = NW * R;                      // weight rows of the workgroup
+  constexpr int NV8 = K / 8, XV = (NV8 + NT - 1) / NT;
+  constexpr int SVN = G * WR / 8, SV = (SVN + NT - 1) / NT;  // 16-byte scale vectors
+  static_assert(R * RB == 1024 * C && CPR % CPG == 0 && 64 % CPG == 0, "chunk layout");
+  static_assert(WR % 8 == 0, "whole 16-byte scale vectors per group row");
+  __shared__ __attribute__((aligned(16))) int8_t xq[K];
+  __shared__ __attribute__((aligned(16))) uint16_t ssc[G * WR];
+  __shared__ __attribute__((aligned(16))) float terms[NW][R][G];
+  __shared__ float red[NW];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nw0 = blockIdx.x * WR, n0 = nw0 + wave * R;
+
+  // x, the scale block and every weight chunk requested first (clamped, so
+  // the loads are unconditional; rows past N are never stored)
+  i32x4 xv[XV];
+#pragma unroll
+  for (int q = 0; q < XV; ++q) xv[q] = ld16(x16 + 8 * min(tid + NT * q, NV8 - 1));
+  i32x4 sv[SV];
+#pragma unroll
+  for (int q = 0; q < SV; ++q) {
+    const int e = min(tid + NT * q, SVN - 1);
+    const int g = e / (WR / 8), part = e % (WR / 8);
+    sv[q] = ld16(sw + (int64_t)g * N + min(nw0 + 8 * part, N - 8));
+  }
+  i32x4 wv[C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = lane + 64 * j, r = c / CPR, kc = c % CPR;
+    wv[j] = ld16(w + (int64_t)min(n0 + r, N - 1) * RB + 16 * kc);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // per-token quantization of x (one row)
+  float am = 0.0f;
+#pragma unroll
+  for (int q = 0; q < XV; ++q)
+    if (tid + NT * q < NV8) am = absmax8(xv[q], am);
+  am = wave_max(am);
+  if (lane == 0) red[wave] = am;
+#pragma unroll
+  for (int q = 0; q < SV; ++q) {
+    const int e = tid + NT * q;
+    if (e < SVN) *reinterpret_cast<i32x4*>(ssc + 8 * e) = sv[q];
+  }
+  __syncthreads();
+  float a = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) a = fmaxf(a, red[i]);
+  const float sa = row_scale(a), inv = 1.0f / sa;
+#pragma unroll
+  for (int q = 0; q < XV; ++q) {
+    const int e = tid + NT * q;
+    if (e < NV8) *reinterpret_cast<i32x2*>(xq + 8 * e) = quant8(xv[q], inv);
+  }
+  __syncthreads();
+
+  // chunks: 32 int4 (k 32 kc .. 32 kc + 31, low nibble first) against 32 q
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = lane + 64 * j, r = c / CPR, kc = c % CPR;
+    i32x4 lo, hi;
+    uint32_t a0, a1;
+    unpack_w4_word((uint32_t)wv[j][0], a0, a1);
+    lo[0] = (int)a0;
+    lo[1] = (int)a1;
+    unpack_w4_word((uint32_t)wv[j][1], a0, a1);
+    lo[2] = (int)a0;
+    lo[3] = (int)a1;
+    unpack_w4_word((uint32_t)wv[j][2], a0, a1);
+    hi[0] = (int)a0;
+    hi[1] = (int)a1;
+    unpack_w4_word((uint32_t)wv[j][3], a0, a1);
+    hi[2] = (int)a0;
+    hi[3] = (int)a1;
+    int d = dot16(lo, *reinterpret_cast<const i32x4*>(xq + 32 * kc), 0);
+    d = dot16(hi, *reinterpret_cast<const i32x4*>(xq + 32 * kc + 16), d);
+#pragma unroll
+    for (int off = CPG / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off);
+    if ((lane % CPG) == 0) {
+      const int g = kc / CPG;
+      terms[wave][r][g] = (float)d * h2f(ssc[g * WR + wave * R + r]);
+    }
+  }
+  // the wave's own LDS slice: visible to its other lanes after the fence
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (lane < R && n0 + lane < N) {
+    const float* tm = terms[wave][lane];
+    float chain = 0.0f;
+#pragma unroll 8
+    for (int g = 0; g < G; ++g) chain = chain + tm[g];
+    float v = chain * sa;
+    if (bias) v = v + h2f(bias[n0 + lane]);
+    y[n0 + lane] = f2h(v);
+  }
+}
+
+// (R, C, NW) of the streaming M == 1 kernel for K: four 4-row waves up to
+// K = 8192, eight 1-row waves above (whole 1 KB wave loads need R * K / 2 to
+// be a multiple of 1024).  Measured against the one-row-per-wave kernel, fused
+// quantization in both, weights from HBM: N=12288 K=4096 gs 128 10.4 -> 7.9
+// us, gs 64 10.8 -> 8.1 us; N=4096 K=12288 gs 128 11.1 -> 9.6 us, gs 64 11.9
+// -> 11.0 us.
+template <int GS>
+hipError_t run_gemv1_w4pg(const uint16_t* x, const GemmArgs& a, hipStream_t s) {
+  const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
+  const uint16_t* sw = reinterpret_cast<const uint16_t*>(a.sw);
+  uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
+#define CIDER_G1(RR, CC, NWW)                                                                  \
+  case 1024 * (CC) / (RR) * 2:                                                                 \
+    gemv1_w4pg_kernel<RR, CC, GS, NWW><<<(a.N + (NWW) * (RR) - 1) / ((NWW) * (RR)), 64 * (NWW), \
+                                         0, s>>>(x, w, sw, a.bias, y, a.N);                    \
+    return hipGetLastError();
+  switch (a.K) {
+    CIDER_G1(4, 4, 4)   // 2048
+    CIDER_G1(4, 6, 4)   // 3072
+    CIDER_G1(4, 8, 4)   // 4096
+    CIDER_G1(4, 10, 4)  // 5120
+    CIDER_G1(4, 12, 4)  // 6144
+    CIDER_G1(4, 14, 4)  // 7168
+    CIDER_G1(4, 16, 4)  // 8192
+    CIDER_G1(1, 5, 8)   // 10240
+    CIDER_G1(1, 6, 8)   // 12288
+    CIDER_G1(1, 7, 8)   // 14336
+    CIDER_G1(1, 8, 8)   // 16384
+    default: return hipErrorNotSupported;
+  }
+#undef CIDER_G1
+}
+
+bool gemv1_w4pg_supported(const GemmArgs& a, int wf, int epi, int gs) {
+  return a.M == 1 && wf == W_I4 && epi == EPI_PG && (gs == 64 || gs == 128) &&
+         a.K >= 2048 && a.K <= 16384 && a.K % 1024 == 0 && (a.K <= 8192 || a.K % 2048 == 0) &&
+         a.N % 8 == 0 && ((uintptr_t)a.w & 15) == 0 && ((uintptr_t)a.sw & 15) == 0;
+}
+
 }  // namespace
 
 bool gemv_q_supported(const GemmArgs& a, int wf, bool fused) {
@@ -297,6 +457,8 @@ hipError_t launch_gemv_q(const GemmArgs& a, int wf, int epi, int gs, hipStream_t
 
 hipError_t launch_gemv_qx(const uint16_t* x, const GemmArgs& a, int wf, int epi, int gs,
                           hipStream_t s) {
+  if (gemv1_w4pg_supported(a, wf, epi, gs) && ((uintptr_t)x & 15) == 0)
+    return gs == 64 ? run_gemv1_w4pg<64>(x, a, s) : run_gemv1_w4pg<128>(x, a, s);
   GemmArgs b = a;
   b.x = reinterpret_cast<const int8_t*>(x);
   b.sa = nullptr;

@@ -557,6 +557,30 @@ def test_gemv_q_exact(M, N, K):
                           O.w4a8_pergroup_linear(x, pk, sc, gs, b), f"gemv w4g{gs} {M}x{N}x{K}")
 
 
+# W4A8 per-group at M == 1 with K a multiple of 1024 from 2048 (of 2048 past
+# 8192) and N % 8 == 0: the streaming GEMV (4 rows per wave up to K = 8192, 1
+# row per wave in 8-wave workgroups above), x quantized in the kernel.  N of
+# 8, 24, 1032 and 4104 leave the last workgroup partly outside; special
+# scales in the first rows.
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("N,K", [(1032, 4096), (8, 8192), (24, 10240), (4104, 3072),
+                                 (256, 16384), (520, 2048)])
+def test_w4a8_gemv1_stream(gs, N, K):
+    x = O.synth_activations(1, K, 94 + N)
+    w4 = np.random.default_rng(95 + K).integers(-8, 8, (N, K), dtype=np.int8)
+    w4[:, :gs] = -8
+    pk = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 96 + gs).astype(np.float16)
+    sc[0, 0], sc[1 % (K // gs), 1] = np.inf, np.nan
+    sc[0, 2], sc[0, 3] = 0.0, 65504.0
+    for bias in (True, False):
+        b = (np.random.default_rng(97).standard_normal(N) * 0.1).astype(np.float16) if bias else None
+        y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, None if b is None else T(b)))
+        with np.errstate(invalid="ignore", over="ignore"):
+            exp = O.w4a8_pergroup_linear(x, pk, sc, gs, b)
+        assert_bits_equal(y, exp, f"w4g M=1 stream gs{gs} N={N} K={K} bias={bias}")
+
+
 # M <= 16 with K % 512 == 0 and K >= 1536: the weight stream through LDS
 # (skinny_dma.hip) for every format.  Covered: 8 and 16 activation slots
 # (M <= 8 re-reads rows for the MFMA's columns past 8), one to four blocks of
