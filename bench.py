@@ -336,7 +336,8 @@ def compact_sweep(torch, lib, _lib, args, dev, stream):
     does not cover, timed as in sweep(): per-group gs 128 / 64 at M=4096, the
     M=1 MV on the down-projection shape, W4A8 per-group gs 128 at M=4096 and
     M=16 (the decode-batch path), per-channel at M=16 and M=8192, and the
-    M=16 per-group cases of the LDS weight stream (int8 gs 128, W4A8 gs 64)."""
+    M=16 per-group cases of the LDS weight stream (int8 gs 128, W4A8 gs 64),
+    and W4A8 gs 128 at M=1 (the streaming GEMV with the quantization fused)."""
     vp = ctypes.c_void_p
 
     def cur():
@@ -411,6 +412,7 @@ def compact_sweep(torch, lib, _lib, args, dev, stream):
     w4_case(16, 12288, 4096, 128)
     w8_case(16, 10240, 2560, 128)
     w4_case(16, 12288, 4096, 64)
+    w4_case(1, 12288, 4096, 128)
     torch.cuda.synchronize()
     return recs
 
