@@ -282,7 +282,8 @@ hipError_t run_m(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s) {
 }
 
 
-// ---- M == 1, int4 weights, per-group fp16 scales, x quantized in the kernel:
+// ---- M == 1, int4 weights, per-group fp16 or per-channel fp32 scales, x
+// quantized in the kernel:
 // the streaming layout of the decode MV (mv_stream.hip) instead of one wave
 // per row.  A wave owns R consecutive weight rows (R * K / 2 contiguous
 // bytes) and lane l requests the 16-byte chunks l, l + 64, ..., l + 64 (C - 1)
@@ -294,23 +295,27 @@ hipError_t run_m(const GemmArgs& a, int wf, int epi, int gs, hipStream_t s) {
 // consecutive lanes: D_g is their shuffle sum (exact int32), its term
 // f32(f32(D_g) * s) goes to LDS, and one lane per row chains the terms in
 // group order, then y = h(f32(chain * sa) (+ bias)), as the kernel above.
+// Per-channel (GS == 0): each lane sums its chunks per row (exact int32), the
+// rows' sums meet in xor butterflies, y = h(f32(f32(acc) * sa) * sw[n] (+ bias)).
 template <int R, int C, int GS, int NW>
-__global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __restrict__ x16,
-                                                            const uint8_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ sw,
-                                                            const uint16_t* __restrict__ bias,
-                                                            uint16_t* __restrict__ y, int N) {
+__global__ __launch_bounds__(64 * NW) void gemv1_w4_kernel(const uint16_t* __restrict__ x16,
+                                                          const uint8_t* __restrict__ w,
+                                                          const void* __restrict__ sw_,
+                                                          const uint16_t* __restrict__ bias,
+                                                          uint16_t* __restrict__ y, int N) {
+  constexpr bool PG = GS > 0;
   constexpr int NT = 64 * NW;
   constexpr int RB = 1024 * C / R, K = 2 * RB;  // bytes per weight row, k per row
-  constexpr int CPR = RB / 16, CPG = GS / 32, G = K / GS;
+  constexpr int CPR = RB / 16, CPG = PG ? GS / 32 : 1, G = PG ? K / GS : 1;
   constexpr int WR = NW * R;                      // weight rows of the workgroup
   constexpr int NV8 = K / 8, XV = (NV8 + NT - 1) / NT;
-  constexpr int SVN = G * WR / 8, SV = (SVN + NT - 1) / NT;  // 16-byte scale vectors
+  constexpr int SVN = PG ? G * WR / 8 : 1, SV = PG ? (SVN + NT - 1) / NT : 1;  // scale vectors
   static_assert(R * RB == 1024 * C && CPR % CPG == 0 && 64 % CPG == 0, "chunk layout");
   static_assert(WR % 8 == 0, "whole 16-byte scale vectors per group row");
+  const uint16_t* sw = reinterpret_cast<const uint16_t*>(sw_);
   __shared__ __attribute__((aligned(16))) int8_t xq[K];
-  __shared__ __attribute__((aligned(16))) uint16_t ssc[G * WR];
-  __shared__ __attribute__((aligned(16))) float terms[NW][R][G];
+  __shared__ __attribute__((aligned(16))) uint16_t ssc[PG ? G * WR : 8];
+  __shared__ __attribute__((aligned(16))) float terms[NW][R][PG ? G : 1];
   __shared__ float red[NW];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -322,11 +327,13 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __r
 #pragma unroll
   for (int q = 0; q < XV; ++q) xv[q] = ld16(x16 + 8 * min(tid + NT * q, NV8 - 1));
   i32x4 sv[SV];
+  if constexpr (PG) {
 #pragma unroll
-  for (int q = 0; q < SV; ++q) {
-    const int e = min(tid + NT * q, SVN - 1);
-    const int g = e / (WR / 8), part = e % (WR / 8);
-    sv[q] = ld16(sw + (int64_t)g * N + min(nw0 + 8 * part, N - 8));
+    for (int q = 0; q < SV; ++q) {
+      const int e = min(tid + NT * q, SVN - 1);
+      const int g = e / (WR / 8), part = e % (WR / 8);
+      sv[q] = ld16(sw + (int64_t)g * N + min(nw0 + 8 * part, N - 8));
+    }
   }
   i32x4 wv[C];
 #pragma unroll
@@ -343,10 +350,12 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __r
     if (tid + NT * q < NV8) am = absmax8(xv[q], am);
   am = wave_max(am);
   if (lane == 0) red[wave] = am;
+  if constexpr (PG) {
 #pragma unroll
-  for (int q = 0; q < SV; ++q) {
-    const int e = tid + NT * q;
-    if (e < SVN) *reinterpret_cast<i32x4*>(ssc + 8 * e) = sv[q];
+    for (int q = 0; q < SV; ++q) {
+      const int e = tid + NT * q;
+      if (e < SVN) *reinterpret_cast<i32x4*>(ssc + 8 * e) = sv[q];
+    }
   }
   __syncthreads();
   float a = red[0];
@@ -361,6 +370,9 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __r
   __syncthreads();
 
   // chunks: 32 int4 (k 32 kc .. 32 kc + 31, low nibble first) against 32 q
+  int acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0;
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     const int c = lane + 64 * j, r = c / CPR, kc = c % CPR;
@@ -380,12 +392,35 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __r
     hi[3] = (int)a1;
     int d = dot16(lo, *reinterpret_cast<const i32x4*>(xq + 32 * kc), 0);
     d = dot16(hi, *reinterpret_cast<const i32x4*>(xq + 32 * kc + 16), d);
+    if constexpr (PG) {
 #pragma unroll
-    for (int off = CPG / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off);
-    if ((lane % CPG) == 0) {
-      const int g = kc / CPG;
-      terms[wave][r][g] = (float)d * h2f(ssc[g * WR + wave * R + r]);
+      for (int off = CPG / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off);
+      if ((lane % CPG) == 0) {
+        const int g = kc / CPG;
+        terms[wave][r][g] = (float)d * h2f(ssc[g * WR + wave * R + r]);
+      }
+    } else {
+      // the chunk's row is rlo or rlo + 1 (constants once unrolled)
+      const int rlo = (64 * j) / CPR, rhi = (64 * j + 63) / CPR;
+      acc[rlo] += r == rlo ? d : 0;
+      if (rhi != rlo && rhi < R) acc[rhi] += r == rhi ? d : 0;
     }
+  }
+  if constexpr (!PG) {
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
+    if (lane < R && n0 + lane < N) {
+      int av = acc[0];
+#pragma unroll
+      for (int r = 1; r < R; ++r) av = lane == r ? acc[r] : av;
+      float v = (float)av * sa;
+      v = v * reinterpret_cast<const float*>(sw_)[n0 + lane];
+      if (bias) v = v + h2f(bias[n0 + lane]);
+      y[n0 + lane] = f2h(v);
+    }
+    return;
   }
   // the wave's own LDS slice: visible to its other lanes after the fence
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -407,16 +442,16 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4pg_kernel(const uint16_t* __r
 // be a multiple of 1024).  Measured against the one-row-per-wave kernel, fused
 // quantization in both, weights from HBM: N=12288 K=4096 gs 128 10.4 -> 7.9
 // us, gs 64 10.8 -> 8.1 us; N=4096 K=12288 gs 128 11.1 -> 9.6 us, gs 64 11.9
-// -> 11.0 us.
+// -> 11.0 us; per-channel N=12288 K=4096 9.3 -> 7.4 us, N=4096 K=12288 9.2 ->
+// 8.0 us.
 template <int GS>
-hipError_t run_gemv1_w4pg(const uint16_t* x, const GemmArgs& a, hipStream_t s) {
+hipError_t run_gemv1_w4(const uint16_t* x, const GemmArgs& a, hipStream_t s) {
   const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
-  const uint16_t* sw = reinterpret_cast<const uint16_t*>(a.sw);
   uint16_t* y = reinterpret_cast<uint16_t*>(a.y);
-#define CIDER_G1(RR, CC, NWW)                                                                  \
-  case 1024 * (CC) / (RR) * 2:                                                                 \
-    gemv1_w4pg_kernel<RR, CC, GS, NWW><<<(a.N + (NWW) * (RR) - 1) / ((NWW) * (RR)), 64 * (NWW), \
-                                         0, s>>>(x, w, sw, a.bias, y, a.N);                    \
+#define CIDER_G1(RR, CC, NWW)                                                                 \
+  case 1024 * (CC) / (RR) * 2:                                                                \
+    gemv1_w4_kernel<RR, CC, GS, NWW><<<(a.N + (NWW) * (RR) - 1) / ((NWW) * (RR)), 64 * (NWW), \
+                                       0, s>>>(x, w, a.sw, a.bias, y, a.N);                   \
     return hipGetLastError();
   switch (a.K) {
     CIDER_G1(4, 4, 4)   // 2048
@@ -435,8 +470,8 @@ hipError_t run_gemv1_w4pg(const uint16_t* x, const GemmArgs& a, hipStream_t s) {
 #undef CIDER_G1
 }
 
-bool gemv1_w4pg_supported(const GemmArgs& a, int wf, int epi, int gs) {
-  return a.M == 1 && wf == W_I4 && epi == EPI_PG && (gs == 64 || gs == 128) &&
+bool gemv1_w4_supported(const GemmArgs& a, int wf, int epi, int gs) {
+  return a.M == 1 && wf == W_I4 && (epi == EPI_PC || (epi == EPI_PG && (gs == 64 || gs == 128))) &&
          a.K >= 2048 && a.K <= 16384 && a.K % 1024 == 0 && (a.K <= 8192 || a.K % 2048 == 0) &&
          a.N % 8 == 0 && ((uintptr_t)a.w & 15) == 0 && ((uintptr_t)a.sw & 15) == 0;
 }
@@ -457,8 +492,10 @@ hipError_t launch_gemv_q(const GemmArgs& a, int wf, int epi, int gs, hipStream_t
 
 hipError_t launch_gemv_qx(const uint16_t* x, const GemmArgs& a, int wf, int epi, int gs,
                           hipStream_t s) {
-  if (gemv1_w4pg_supported(a, wf, epi, gs) && ((uintptr_t)x & 15) == 0)
-    return gs == 64 ? run_gemv1_w4pg<64>(x, a, s) : run_gemv1_w4pg<128>(x, a, s);
+  if (gemv1_w4_supported(a, wf, epi, gs) && ((uintptr_t)x & 15) == 0) {
+    if (epi == EPI_PC) return run_gemv1_w4<0>(x, a, s);
+    return gs == 64 ? run_gemv1_w4<64>(x, a, s) : run_gemv1_w4<128>(x, a, s);
+  }
   GemmArgs b = a;
   b.x = reinterpret_cast<const int8_t*>(x);
   b.sa = nullptr;

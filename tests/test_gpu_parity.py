@@ -581,6 +581,18 @@ def test_w4a8_gemv1_stream(gs, N, K):
         assert_bits_equal(y, exp, f"w4g M=1 stream gs{gs} N={N} K={K} bias={bias}")
 
 
+# The same streaming GEMV with per-channel fp32 scales (the reference's own
+# W4A8, weights in its [K/2, N] layout, no bias).
+@pytest.mark.parametrize("N,K", [(1032, 4096), (8, 8192), (24, 10240), (4104, 3072),
+                                 (256, 16384), (520, 2048), (12288, 4096)])
+def test_w4a8_gemv1_stream_perchannel(N, K):
+    x = O.synth_activations(1, K, 98 + N)
+    wf = np.random.default_rng(99 + K).standard_normal((K, N)).astype(np.float32)
+    packed, sw = O.pack_weight_int4(wf)
+    y = H(C.w4a8_linear(T(x), T(packed), T(sw)))
+    assert_bits_equal(y, O.w4a8_linear(x, packed, sw), f"w4 pc M=1 stream N={N} K={K}")
+
+
 # M <= 16 with K % 512 == 0 and K >= 1536: the weight stream through LDS
 # (skinny_dma.hip) for every format.  Covered: 8 and 16 activation slots
 # (M <= 8 re-reads rows for the MFMA's columns past 8), one to four blocks of
