@@ -492,6 +492,18 @@ def test_pergroup_one_set_tiles(gs):
     assert_bits_equal(y[rows], exp, f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
 
 
+# Few rows on a very wide N also reach the one-set kernel (M <= 64 with N >= 8192
+# takes the per-group DMA tiles; 512 tiles of 128 x 128 from N = 65536): every
+# tile has one partial tile row, and the last tile column is ragged.
+@pytest.mark.parametrize("gs", [64, 128])
+def test_pergroup_one_set_few_rows(gs):
+    M, N, K = 40, 65544, 256
+    x, w, _, b = synth_pc(M, N, K, 98 + gs)
+    sw = O.synth_scales((K // gs, N), 99 + gs)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"pg one-set few rows gs{gs}")
+
+
 # The one-set kernel at its shortest k-loops: one and two stages of 128 (the
 # loop body never runs; the prologue's reload of the last stage fills the
 # second ring slot), 512 tiles of 128 x 128.
