@@ -16,18 +16,23 @@
 // kernel does not take run the register-staged kernel of gemm.hip.)
 //
 // MI355X design
-//   * 256 threads = 4 waves (2 x 2), one workgroup per CU; tile BM (m) x BN
-//     (n) from {256 x 256, 192 x 256, 128 x 256, 128 x 128, 128 x 64, 64 x 128,
-//     64 x 64},
-//     picked per shape by measured rate and the rounds the grid needs on the
-//     256 CUs.  At 256 x 256 (the large-M tile) each wave owns a 128 x 128
-//     sub-tile = 4 x 4 blocks of 32 x 32 (16 int32 accumulators per lane per
-//     block, 256 AGPRs): the fewest fragment reads per MAC, which the LDS
-//     bandwidth (~128 B/clk per CU) rewards; 128 x 256 (waves of 64 x 128)
-//     wins where its rounds fit the grid better.  Weights are the MFMA A
-//     operand, activations the B operand.  At 256 x 256 there is no register
-//     to spare: a spill reload is a vector-memory load, and waiting for it
-//     waits for every DMA load in flight (one spilled build ran 15 % slower).
+//   * One workgroup per CU; tile BM (m) x BN (n) from {256 x 256, 192 x 256,
+//     128 x 256, 128 x 128, 128 x 64, 64 x 128, 64 x 64}, picked per shape by
+//     measured rate and the rounds the grid needs on the 256 CUs.  Waves: 2
+//     along m and NWV / 2 along n.  The 256-column tiles run NWV = 8 waves,
+//     two per SIMD: at 256 x 256 each wave owns 128 x 64 = 4 x 2 blocks of
+//     32 x 32 (16 int32 accumulators per lane per block, 128 registers), and
+//     while one wave of a SIMD waits on its DMA issue, fragment reads or
+//     epilogue, the other's MFMAs run.  That costs 1.5x the fragment reads of
+//     four 128 x 128 waves (LDS ~126 B/clk per CU at the full MFMA rate,
+//     against ~128 delivered) and measured faster anyway: uniform 256 x 256 at
+//     M=4096 N=10240 K=2560 113.8 -> 105.9 us, the mixed grid 104.4 -> 99.8
+//     us, M=8192 199.6 -> 188.0 us, int4 N=12288 K=4096 199.9 -> 190.3 us;
+//     192 x 256 and 128 x 256 4-10 %; N=2560 K=10240 level.  The smaller
+//     tiles keep four waves (2 x 2).  Weights are the MFMA A operand,
+//     activations the B operand.  A spill reload is a vector-memory load, and
+//     waiting for it waits for every DMA load in flight (one spilled build ran
+//     15 % slower).
 //   * K advances BK bytes per stage (128; 64 is kept for tuning); stage s
 //     lives in ring slot s % NS, NS = as many stages as fit the 160 KB LDS
 //     (2 at 256 x 256 x 128, 3 at 128 x 256, up to 8 for small tiles).  Each
@@ -87,14 +92,14 @@ namespace cider {
 namespace {
 
 
-template <int BM, int BN, int BK, int WF = W_I8>
+template <int BM, int BN, int BK, int WF = W_I8, int NWV = 4>
 struct DmaCfg {
   static constexpr int CH = BK / 16;                // 16-byte chunks per X row
   static constexpr int RPI = 1024 / BK;             // X rows per DMA instruction
   static constexpr int WB = (WF == W_I4) ? BK / 2 : BK;  // weight bytes per row and stage
   static constexpr int CHW = WB / 16;               // 16-byte chunks per W row
   static constexpr int RPIW = 1024 / WB;            // W rows per DMA instruction
-  static constexpr int WI = BN / RPIW / 4, XI = BM / RPI / 4;  // per wave
+  static constexpr int WI = BN / RPIW / NWV, XI = BM / RPI / NWV;  // per wave
   static constexpr int PS = WI + XI;                // vmcnt units per stage
   static constexpr int SUBS = BK / 32;              // MFMA k sub-steps per stage
   static constexpr int W_BYTES = BN * WB, X_BYTES = BM * BK, STAGE = W_BYTES + X_BYTES;
@@ -129,7 +134,7 @@ using icst = std::integral_constant<int, V>;
 // One BM x BN output tile over the whole K.  smem: DmaCfg::SMEM bytes of LDS.
 // WF = W_I8: weights int8 [N, K]; W_I4: packed int4 [N, K/2] (element k in
 // byte k/2, low nibble first, two's complement), unpacked in registers.
-template <int BM, int BN, int BK, int EPI, int WF = W_I8>
+template <int BM, int BN, int BK, int EPI, int WF = W_I8, int NWV = 4>
 __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const int n0,
                                          int8_t* __restrict__ smem, const int kloop = 0) {
   static_assert((BM == 64 || BM == 128 || BM == 192 || BM == 256) &&
@@ -137,9 +142,10 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
                 "tile shape");
   static_assert(BK == 64 || BK == 128, "k stage");
   static_assert(WF == W_I8 || BK == 128, "int4 weights use 128-byte k-stages");
-  using C = DmaCfg<BM, BN, BK, WF>;
+  using C = DmaCfg<BM, BN, BK, WF, NWV>;
   constexpr bool W4 = (WF == W_I4);
-  constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+  // waves: 2 along m, NWV / 2 along n
+  constexpr int WM = BM / 2, WN = BN / (NWV / 2), TM = WM / 32, TN = WN / 32;
   constexpr int WI = C::WI, XI = C::XI, PS = C::PS, NS = C::NS, SUBS = C::SUBS;
   constexpr int W_BYTES = C::W_BYTES, STAGE = C::STAGE, CH = C::CH, RPI = C::RPI;
   constexpr int WB = C::WB, CHW = C::CHW, RPIW = C::RPIW;
@@ -465,7 +471,7 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
     const int cl = (lane % LPR) * 8;  // first column of this lane's 8
     const int n = n0 + cl;
 #pragma unroll 4
-    for (int rr = wave * RPS + lane / LPR; rr < BM; rr += 4 * RPS) {
+    for (int rr = wave * RPS + lane / LPR; rr < BM; rr += NWV * RPS) {
       const int m = m0 + rr;
       if (m < M && n < N)
         *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
@@ -475,12 +481,12 @@ __device__ __forceinline__ void dma_tile(const GemmArgs& p, const int m0, const 
 }
 
 // Uniform grid: one BM x BN tile per workgroup.
-template <int BM, int BN, int BK, int EPI, int WF>
-__global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
-  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK, WF>::SMEM];
+template <int BM, int BN, int BK, int EPI, int WF, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV, 1) void gemm_dma_kernel(const GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) int8_t smem[DmaCfg<BM, BN, BK, WF, NWV>::SMEM];
   int m0, n0;
   tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), p.M, 0, p.N, m0, n0);
-  dma_tile<BM, BN, BK, EPI, WF>(p, m0, n0, smem);
+  dma_tile<BM, BN, BK, EPI, WF, NWV>(p, m0, n0, smem);
 }
 
 // Two tile sizes in one grid, so that the last round of workgroups is not
@@ -488,28 +494,31 @@ __global__ __launch_bounds__(256, 1) void gemm_dma_kernel(const GemmArgs p) {
 // [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
 // many tiles of half the work.  Workgroups start in index order, so the small
 // tiles form the last round; each region has its own XCD remap.
-template <int EPI, int WF>
-__global__ __launch_bounds__(256, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
-                                                                int nsplit) {
-  constexpr int S1 = DmaCfg<256, 256, 128, WF>::SMEM, S2 = DmaCfg<128, 256, 128, WF>::SMEM;
+template <int EPI, int WF, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
+                                                                     int nsplit) {
+  constexpr int S1 = DmaCfg<256, 256, 128, WF, NWV>::SMEM,
+                S2 = DmaCfg<128, 256, 128, WF, NWV>::SMEM;
   __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
   const int b = blockIdx.x;
   int m0, n0;
   if (b < nbig) {
     tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
-    dma_tile<256, 256, 128, EPI, WF>(p, m0, n0, smem);
+    dma_tile<256, 256, 128, EPI, WF, NWV>(p, m0, n0, smem);
   } else {
     tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
-    dma_tile<128, 256, 128, EPI, WF>(p, m0, n0, smem);
+    dma_tile<128, 256, 128, EPI, WF, NWV>(p, m0, n0, smem);
   }
 }
 
 namespace {
 
+// 256-column tiles run eight waves (two per SIMD), the smaller tiles four.
 template <int BM, int BN, int BK, int EPI, int WF = W_I8>
 hipError_t run_dma(const GemmArgs& a, hipStream_t s) {
+  constexpr int NWV = BN == 256 ? 8 : 4;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  gemm_dma_kernel<BM, BN, BK, EPI, WF><<<tiles, 256, 0, s>>>(a);
+  gemm_dma_kernel<BM, BN, BK, EPI, WF, NWV><<<tiles, 64 * NWV, 0, s>>>(a);
   return hipGetLastError();
 }
 
@@ -561,7 +570,7 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
         const int nsplit = (tn - tail_cols) * 256;
         const int nbig = (int)(T - R);
         const int nsmall = ((a.M + 127) / 128) * tail_cols;
-        gemm_dma_mixed_kernel<EPI, WF><<<nbig + nsmall, 256, 0, s>>>(a, nbig, nsplit);
+        gemm_dma_mixed_kernel<EPI, WF, 8><<<nbig + nsmall, 512, 0, s>>>(a, nbig, nsplit);
         return hipGetLastError();
       }
     }
