@@ -743,8 +743,8 @@ def gemm_kernel_name(M, N, K, dev):
         if T > cus and 0 < R and 2 * R <= cus and R % tm == 0:
             tail = (0.6 + 0.4 * 2 * R / cus) * 128 * 256 / 0.87
             if (T // cus) * 256 * 256 + tail < best_cost * 0.999:
-                return ("gemm_dma_mixed_kernel<PC, I8, 8> (256x256 tiles + 128x256 last round, "
-                        "8 waves)")
+                return ("gemm_dma_mixed_kernel<PC, I8, 8> (256x256 tiles + 128x256 tiles, "
+                        "half of them first and half last, 8 waves)")
         waves = 8 if best[1] == 256 else 4
         return "gemm_dma_kernel<%d, %d, 128, PC, I8, %d> (%dx%d tiles, %d waves)" % (
             best[0], best[1], waves, best[0], best[1], waves)

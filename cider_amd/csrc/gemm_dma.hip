@@ -490,23 +490,31 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_dma_kernel(const GemmArgs p)
 }
 
 // Two tile sizes in one grid, so that the last round of workgroups is not
-// half empty: workgroups [0, nbig) take 256 x 256 tiles of columns
-// [0, nsplit); the rest take 128 x 256 tiles of columns [nsplit, N), twice as
-// many tiles of half the work.  Workgroups start in index order, so the small
-// tiles form the last round; each region has its own XCD remap.
+// half empty: the big workgroups take 256 x 256 tiles of columns [0, nsplit),
+// the small ones 128 x 256 tiles of columns [nsplit, N), twice as many tiles
+// of half the work.  Workgroups start in index order: [0, s1) small tiles
+// 0 .. s1-1, [s1, s1 + nbig) the big tiles, the rest the other small tiles.
+// With s1 = half the small tiles, half the CUs start on a small tile and run
+// half a tile out of phase with the other half from then on, so the tile
+// epilogues' output stores (a 256 x 256 tile writes 128 KB, a round of
+// tiles 32 MB at once, for about 4.6 us at M=4096 N=10240 K=2560) meet the
+// other half's k-loops instead of each other (that shape: 102.0 -> 95.9 us,
+// bit-identical).  Each region keeps its own XCD remap; s1 and nbig are
+// multiples of 8, so a region's index keeps the XCD of its workgroup.
 template <int EPI, int WF, int NWV = 4>
 __global__ __launch_bounds__(64 * NWV, 1) void gemm_dma_mixed_kernel(const GemmArgs p, int nbig,
-                                                                     int nsplit) {
+                                                                     int nsplit, int s1) {
   constexpr int S1 = DmaCfg<256, 256, 128, WF, NWV>::SMEM,
                 S2 = DmaCfg<128, 256, 128, WF, NWV>::SMEM;
   __shared__ __attribute__((aligned(1024))) int8_t smem[S1 > S2 ? S1 : S2];
   const int b = blockIdx.x;
   int m0, n0;
-  if (b < nbig) {
-    tile_coords<256, 256>(xcd_remap(b, nbig), p.M, 0, nsplit, m0, n0);
+  if (b >= s1 && b < s1 + nbig) {
+    tile_coords<256, 256>(xcd_remap(b - s1, nbig), p.M, 0, nsplit, m0, n0);
     dma_tile<256, 256, 128, EPI, WF, NWV>(p, m0, n0, smem);
   } else {
-    tile_coords<128, 256>(xcd_remap(b - nbig, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
+    const int bs = b < s1 ? b : b - nbig;
+    tile_coords<128, 256>(xcd_remap(bs, gridDim.x - nbig), p.M, nsplit, p.N, m0, n0);
     dma_tile<128, 256, 128, EPI, WF, NWV>(p, m0, n0, smem);
   }
 }
@@ -570,7 +578,10 @@ hipError_t pick_tile(const GemmArgs& a, hipStream_t s) {
         const int nsplit = (tn - tail_cols) * 256;
         const int nbig = (int)(T - R);
         const int nsmall = ((a.M + 127) / 128) * tail_cols;
-        gemm_dma_mixed_kernel<EPI, WF, 8><<<nbig + nsmall, 512, 0, s>>>(a, nbig, nsplit);
+        // half the small tiles first (a multiple of 8), when the big region
+        // starts on an XCD boundary; otherwise all of them last
+        const int s1 = nbig % 8 == 0 ? nsmall / 2 / 8 * 8 : 0;
+        gemm_dma_mixed_kernel<EPI, WF, 8><<<nbig + nsmall, 512, 0, s>>>(a, nbig, nsplit, s1);
         return hipGetLastError();
       }
     }
