@@ -668,10 +668,13 @@ __global__ __launch_bounds__(256) void splitk_dequant_kernel(const GemmArgs p,
 // 256: 25.6 -> 17.9 us (8 slices), 32.3 -> 23.8 us (8), 32.6 -> 28.8 us (4);
 // N=4096 K=12288 M=64: 37.1 -> 23.7 us (8).  Grids of more tiles gained
 // little or lost (N=10240 K=2560 M=32, 80 tiles: 12.4 us whole, 16.2 us in
-// two slices).  The caller also checks the DMA conditions (K % 128 == 0,
-// N % 8 == 0, aligned operands).
+// two slices).  The caller also checks the alignment of the operands.  The
+// tile's per-lane weight and activation offsets are 32-bit (up to 128 rows x
+// K bytes, and the slices address the full row pitch K), so K * 256 must stay
+// below 2^32 as for launch_gemm's DMA tiles.
 int splitk_ways(int M, int N, int K) {
   if (M <= 16 || M > 512 || N % 8 != 0 || K % 128 != 0) return 1;
+  if ((int64_t)K * 256 >= ((int64_t)1 << 32)) return 1;
   const int bm = M <= 64 ? 64 : 128;
   const int tiles = ((M + bm - 1) / bm) * ((N + 127) / 128);
   const int cus = num_cus();

@@ -8,7 +8,8 @@ leading dimensions, calls ``ops.perchannel_linear`` / ``ops.pergroup_linear``
 the shape (``cider/nn.py:102-113``).  ``W8A8Linear`` is an alias, as in the
 reference (``cider/nn.py:212``).  ``W4A8Linear`` holds reference-layout packed
 int4 weights (``cider/nn.py:216-241``) and keeps a repacked copy in the
-library layout, made once at construction.
+library layout, made on its first forward on the GPU and made again when the
+packed weights change (in-place update, ``load_state_dict``).
 """
 
 from __future__ import annotations
@@ -200,21 +201,35 @@ class W4A8Linear(torch.nn.Module):
                              .contiguous())
         self._K = K
         # library layout, made on first use on the GPU; valid for the
-        # (version, address, shape, device) of packed_weight it was made from
+        # (version, address, shape, device) of packed_weight it was made from.
+        # _w4_done: event recorded after the repack on the stream that made it
         self._w4_nk = None
         self._w4_sig = None
+        self._w4_done = None
 
     def _packed_nk(self) -> torch.Tensor:
+        """The library-layout copy, ordered for the current stream: a repack
+        runs on the calling stream and records an event; every use waits for
+        that event on its own stream and marks the copy as used there, so the
+        caching allocator keeps the memory until that stream's work is done
+        even after a later repack replaces the copy."""
         w = self.packed_weight
+        use = torch.cuda.current_stream(w.device)
         sig = (w._version, w.data_ptr(), tuple(w.shape), w.device)
         if self._w4_nk is None or self._w4_sig != sig:
-            self._w4_nk = ops.repack_w4_ref(w)
-            self._w4_sig = sig
+            out = ops.repack_w4_ref(w)
+            done = torch.cuda.Event()
+            done.record(use)
+            self._w4_nk, self._w4_sig, self._w4_done = out, sig, done
+            return out
+        use.wait_event(self._w4_done)
+        self._w4_nk.record_stream(use)
         return self._w4_nk
 
     def _load_from_state_dict(self, *args, **kwargs):
         self._w4_nk = None
         self._w4_sig = None
+        self._w4_done = None
         super()._load_from_state_dict(*args, **kwargs)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -388,6 +388,10 @@ class _RepackCache:
     def __init__(self, capacity: int = 16):
         self.capacity = capacity
         self.entries = collections.OrderedDict()
+        # id(source) -> (weakref, finalizer): one finalizer per live source
+        # tensor, however often its entry is replaced (in-place updates) or
+        # evicted and made again
+        self._fins = {}
         self._lock = threading.Lock()
 
     @staticmethod
@@ -399,6 +403,9 @@ class _RepackCache:
             e = self.entries.get(key)
             if e is not None and e[0] is ref:
                 del self.entries[key]
+            f = self._fins.get(key)
+            if f is not None and f[0] is ref:
+                del self._fins[key]
 
     def get(self, t: torch.Tensor, stream) -> torch.Tensor:
         use = torch.cuda.current_stream(t.device) if stream is None else stream
@@ -417,13 +424,17 @@ class _RepackCache:
         out = repack_w4_ref(t, stream)
         done = torch.cuda.Event()
         done.record(use)
-        ref = weakref.ref(t)
         with self._lock:
+            f = self._fins.get(key)
+            if f is not None and f[0]() is t and f[1].alive:
+                ref = f[0]
+            else:
+                ref = weakref.ref(t)
+                self._fins[key] = (ref, weakref.finalize(t, self._drop, key, ref))
             self.entries[key] = (ref, self._sig(t), out, done)
             self.entries.move_to_end(key)
             while len(self.entries) > self.capacity:
                 self.entries.popitem(last=False)
-        weakref.finalize(t, self._drop, key, ref)
         return out
 
 

@@ -59,6 +59,27 @@ def test_workspace_bytes(lib):
     assert ws(_lib.CIDER_OP_W4A8_REF, 1, 70, 64) == 256 + 256 + 2304
 
 
+def test_splitk_workspace_respects_32bit_tile_offsets(lib):
+    """The split-K GEMM's tiles address rows by 32-bit per-lane offsets; K
+    with K * 256 >= 2**32 must run one pass (no partial-sum part in the
+    workspace), while the usual mid-M shapes keep their K slices."""
+    from cider_amd import _lib
+    ws = _lib.workspace_bytes
+
+    def quant(M, K):
+        a = lambda v: (v + 255) // 256 * 256
+        return a(M * K) + a(4 * M)
+
+    # M=128 N=2560 K=10240: 20 tiles of 128 x 128, 8 slices of the int32 sums
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 128, 2560, 10240) == \
+        quant(128, 10240) + 8 * 128 * 2560 * 4
+    # one tile, K = 2**26: 2**26 * 256 = 2**34 bytes of offsets, no split
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 32, 128, 1 << 26) == quant(32, 1 << 26)
+    # just below the limit the split still applies
+    k = (1 << 24) - 1024
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 32, 128, k) > quant(32, k)
+
+
 def _err(lib):
     return lib.cider_last_error().decode()
 

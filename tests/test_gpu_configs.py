@@ -196,3 +196,51 @@ def test_functional_w4a8_cache_across_streams():
     pd.copy_(T(packed2))
     sd.copy_(T(sw2))
     assert_bits_equal(H(C.w4a8_linear(xd, pd, sd)), O.w4a8_linear(x, packed2, sw2), "updated")
+
+
+def test_w4a8_module_across_streams():
+    """W4A8Linear's library-layout copy, made on one stream, is used on
+    another: the second stream waits for the repack."""
+    K, N, M = 1024, 192, 40
+    rng = np.random.default_rng(35)
+    w = rng.standard_normal((K, N)).astype(np.float32)
+    layer = C.W4A8Linear.from_weights(w, device=DEV)
+    packed, sw = O.pack_weight_int4(w)
+    x = O.synth_activations(M, K, 36)
+    xd = T(x)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        y1 = layer(xd)
+    with torch.cuda.stream(s2):
+        y2 = layer(xd)
+    torch.cuda.synchronize()
+    exp = O.w4a8_linear(x, packed, sw)
+    assert_bits_equal(y1.cpu().numpy(), exp, "stream 1 (repack)")
+    assert_bits_equal(y2.cpu().numpy(), exp, "stream 2 (cached copy)")
+
+
+def test_repack_cache_one_finalizer_per_source():
+    """Repeated misses on one live source tensor (in-place updates) replace
+    its cache entry without stacking finalizers."""
+    from cider_amd import ops as OPS
+    K, N = 256, 64
+    rng = np.random.default_rng(37)
+    packed, sw = O.pack_weight_int4(rng.standard_normal((K, N)).astype(np.float32))
+    x = O.synth_activations(3, K, 38)
+    pd, sd, xd = T(packed), T(sw), T(x)
+    cache = OPS._repack_cache
+    for i in range(4):
+        packed_i, sw_i = O.pack_weight_int4(rng.standard_normal((K, N)).astype(np.float32))
+        pd.copy_(T(packed_i))
+        sd.copy_(T(sw_i))
+        assert_bits_equal(H(C.w4a8_linear(xd, pd, sd)), O.w4a8_linear(x, packed_i, sw_i),
+                          f"update {i}")
+        fin = cache._fins[id(pd)][1]
+        if i == 0:
+            first = fin
+        assert fin is first and fin.alive
+    del pd
+    import gc
+    gc.collect()
+    assert not first.alive

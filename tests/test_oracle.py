@@ -618,3 +618,22 @@ def test_mv_bar_accepts_the_oracle_and_rejects_planted_mistakes(gs):
                       ("scale off by 1%", run(w, (sw * F32(1.01)).astype(F32)))):
         with pytest.raises(AssertionError):
             assert_mv_close(bad, x, w, sw, b, gs, name)
+
+
+def test_sum_bar_compares_non_finite_outputs_per_element():
+    """The tolerance bar of tests/util.py (assert_sum_close, under the MV
+    bar) requires the oracle's NaN positions and inf signs element by
+    element: -inf for +inf, a NaN moved to another output, or a finite value
+    for a NaN fail it; a matching NaN / NaN pair and matching infinities
+    pass."""
+    from tests.util import assert_sum_close
+    ref = np.array([1.0, np.inf, np.nan, -np.inf, 2.0], np.float16)
+    exact = np.array([1.0, np.inf, np.nan, -np.inf, 2.0])
+    mag = np.abs(np.nan_to_num(exact, nan=0.0, posinf=0.0, neginf=0.0))
+    assert_sum_close(ref.copy(), ref, exact, mag, 8, "same")
+    for name, bad in (("inf sign", [1.0, -np.inf, np.nan, -np.inf, 2.0]),
+                      ("NaN moved", [np.nan, np.inf, 3.0, -np.inf, 2.0]),
+                      ("NaN lost", [1.0, np.inf, 0.0, -np.inf, 2.0]),
+                      ("finite off", [1.0, np.inf, np.nan, -np.inf, 2.5])):
+        with pytest.raises(AssertionError):
+            assert_sum_close(np.array(bad, np.float16), ref, exact, mag, 8, name)

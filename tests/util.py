@@ -108,16 +108,36 @@ def assert_mv_close(got, x, w, sw, bias, gs, what="", ref=None):
                O.mv_pergroup(x, w, sw, bias, gs))
     ref = np.asarray(ref, np.float16).reshape(-1)
     exact, mag = mv_exact(x, w, sw, bias, gs)
-    g, r = got.astype(np.float64), ref.astype(np.float64)
-    assert np.isfinite(g).all() == np.isfinite(r).all(), f"{what}: non-finite outputs differ"
-    d = 2 * (-(-K // 64)) + 16
+    assert_sum_close(got, ref, exact, mag, 2 * (-(-K // 64)) + 16, what, "MV bar")
+
+
+def assert_sum_close(got, ref, exact, mag, depth, what="", bar="bar"):
+    """fp16 outputs of a sum whose fp32 evaluation order is free (any tree,
+    fma or not): every output is within 1e-3 relative or 1 fp16 ulp of the
+    oracle's output ``ref``, or within gamma_depth * mag + 1 fp16 ulp of the
+    float64 value ``exact`` (``mag``: the sum of the absolute terms), the
+    fp32 error bound of any evaluation of that depth.  Non-finite outputs
+    must match the oracle element by element (NaN positions, inf signs); the
+    bar applies to the elements finite in both."""
+    g = np.asarray(got, np.float16).reshape(-1).astype(np.float64)
+    r = np.asarray(ref, np.float16).reshape(-1).astype(np.float64)
+    exact = np.asarray(exact, np.float64).reshape(-1)
+    mag = np.asarray(mag, np.float64).reshape(-1)
+    assert g.shape == r.shape, (g.shape, r.shape)
+    nan_g, nan_r = np.isnan(g), np.isnan(r)
+    assert (nan_g == nan_r).all(), f"{what}: NaN positions differ from the oracle's"
+    inf_g, inf_r = np.isinf(g), np.isinf(r)
+    assert (inf_g == inf_r).all() and (g[inf_g] == r[inf_r]).all(), \
+        f"{what}: inf outputs differ from the oracle's"
+    fin = ~(nan_r | inf_r)
+    g, r, exact, mag = g[fin], r[fin], exact[fin], mag[fin]
     u = 2.0 ** -24
-    bound = d * u / (1 - d * u) * mag + f16_ulp(exact)
+    bound = depth * u / (1 - depth * u) * mag + f16_ulp(exact)
     near_ref = (np.abs(g - r) <= f16_ulp(r)) | (np.abs(g - r) <= 1e-3 * np.abs(r))
     near_exact = np.abs(g - exact) <= bound
     ok = near_ref | near_exact
     if not ok.all():
         idx = np.flatnonzero(~ok)[:5]
         raise AssertionError(
-            f"{what}: {np.count_nonzero(~ok)} of {ok.size} outputs outside the MV bar; "
+            f"{what}: {np.count_nonzero(~ok)} of {ok.size} outputs outside the {bar}; "
             f"e.g. at {idx}: got {g[idx]} oracle {r[idx]} exact {exact[idx]} bound {bound[idx]}")
