@@ -98,23 +98,86 @@ void oracle_quantize_per_token(const uint16_t* x, int M, int K, int8_t* q,
 
 /* ---- a3: C = A * B^T in int32 (w8a8_matmul.metal:301-453) -------------- */
 
+/* Integer sums are exact in any order, so the GEMM is blocked for the host:
+ * 4 rows of a x 2 rows of b per register block, 16 k per step (int8 widened
+ * to int16, pairwise products summed into int32 lanes by vpmaddwd), with a
+ * scalar tail for K % 16.  Compiled for AVX2 and, where the host has it,
+ * AVX-512BW (the same code, chosen at load time by target_clones). */
+#if defined(__x86_64__) && defined(__GNUC__)
+#include <immintrin.h>
+#define ORACLE_X86 1
+#endif
+
+static int32_t dot_scalar(const int8_t* a, const int8_t* b, int k0, int K) {
+  int32_t acc = 0;
+  for (int k = k0; k < K; k++) acc += (int32_t)a[k] * (int32_t)b[k];
+  return acc;
+}
+
+#ifdef ORACLE_X86
+__attribute__((target("avx2"))) static inline int32_t hsum8(__m256i v) {
+  __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4e));
+  s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xb1));
+  return _mm_cvtsi128_si32(s);
+}
+
+/* c[i][j] = sum_k a_i[k] b_j[k] for i < 4, j < 2 */
+__attribute__((target("avx2"))) static void block4x2(const int8_t* a0, int64_t lda,
+                                                     const int8_t* b0, int64_t ldb, int K,
+                                                     int32_t c[4][2]) {
+  __m256i acc[4][2];
+  for (int i = 0; i < 4; i++) acc[i][0] = acc[i][1] = _mm256_setzero_si256();
+  const int K16 = K & ~15;
+  for (int k = 0; k < K16; k += 16) {
+    __m256i bv0 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(b0 + k)));
+    __m256i bv1 = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(b0 + ldb + k)));
+    for (int i = 0; i < 4; i++) {
+      __m256i av = _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(a0 + i * lda + k)));
+      acc[i][0] = _mm256_add_epi32(acc[i][0], _mm256_madd_epi16(av, bv0));
+      acc[i][1] = _mm256_add_epi32(acc[i][1], _mm256_madd_epi16(av, bv1));
+    }
+  }
+  for (int i = 0; i < 4; i++)
+    for (int j = 0; j < 2; j++)
+      c[i][j] = hsum8(acc[i][j]) + dot_scalar(a0 + i * lda, b0 + j * ldb, K16, K);
+}
+
+static int have_avx2(void) {
+  __builtin_cpu_init();
+  return __builtin_cpu_supports("avx2");
+}
+#endif
+
 void oracle_i8_gemm_nt(const int8_t* a, const int8_t* b, int M, int N, int K,
                        int32_t* c) {
   const int NB = 64;
+#ifdef ORACLE_X86
+  const int simd = have_avx2();
+#else
+  const int simd = 0;
+#endif
 #pragma omp parallel for collapse(2) schedule(dynamic, 1)
   for (int m0 = 0; m0 < M; m0 += 4) {
     for (int n0 = 0; n0 < N; n0 += NB) {
       int m1 = m0 + 4 < M ? m0 + 4 : M;
       int n1 = n0 + NB < N ? n0 + NB : N;
-      for (int m = m0; m < m1; m++) {
-        const int8_t* ar = a + (int64_t)m * K;
-        for (int n = n0; n < n1; n++) {
-          const int8_t* br = b + (int64_t)n * K;
-          int32_t acc = 0;
-          for (int k = 0; k < K; k++) acc += (int32_t)ar[k] * (int32_t)br[k];
-          c[(int64_t)m * N + n] = acc;
+      int n = n0;
+#ifdef ORACLE_X86
+      if (simd && m1 - m0 == 4) {
+        for (; n + 2 <= n1; n += 2) {
+          int32_t blk[4][2];
+          block4x2(a + (int64_t)m0 * K, K, b + (int64_t)n * K, K, K, blk);
+          for (int i = 0; i < 4; i++) {
+            c[(int64_t)(m0 + i) * N + n] = blk[i][0];
+            c[(int64_t)(m0 + i) * N + n + 1] = blk[i][1];
+          }
         }
       }
+#endif
+      for (int m = m0; m < m1; m++)
+        for (int nn = n; nn < n1; nn++)
+          c[(int64_t)m * N + nn] = dot_scalar(a + (int64_t)m * K, b + (int64_t)nn * K, 0, K);
     }
   }
 }

@@ -12,13 +12,15 @@
   this: the GPU's fp16 intermediates move some of the rounding decisions,
   so the two roundings are independent noise.)  A wrong head grouping,
   RoPE or cache index drops the cosine far below (tests/test_qwen3.py).
-* The full-depth models (36 / 28 layers) through properties that need no
-  float reference: finite logits, decode continuing a prefill agrees with
-  prefilling one token more (the decode MV has no activation quantization,
-  so the two differ by that noise over 4 linears per layer; measured cosine
-  above 0.999 at both depths, the bar is 0.995), chunked prefill of a
-  multimodal prompt agrees with one-shot prefill, and HIP-graph decode
-  reproduces eager decode token for token.
+* The full-depth models (36 / 28 layers) at the BASELINE workloads
+  (configs[3]: a 2048-token prefill and 128 greedy decode steps; configs[4]:
+  the 1334 / 2393 / 3455-token prompts with 2 / 3 / 4 images) through
+  properties that need no float reference: finite logits, decode continuing
+  a prefill agrees with prefilling one token more (the decode MV has no
+  activation quantization, so the two differ by that noise over 4 linears
+  per layer; measured cosine above 0.999 at both depths, the bar is 0.995),
+  chunked prefill of a multimodal prompt agrees with one-shot prefill, and
+  HIP-graph decode reproduces eager decode token for token.
 """
 
 import pytest
@@ -71,43 +73,73 @@ def test_qwen3_vl_2b_width_two_layers_vs_fp32():
     _close_width(got, ref, "qwen3-vl-2b width, 2 layers")
 
 
-def test_qwen3_8b_full_depth_properties():
+def test_qwen3_8b_config3_workload():
+    """configs[3] at its workload: the full 36-layer Qwen3-8B shape, a prefill
+    of 2048 ids uniform over the vocabulary, then 128 greedy decode steps.
+    Checked by properties: finite logits over the whole prefill; decode at
+    position 2048 agrees with prefilling one token more; the 128 steps
+    replayed from a HIP graph equal eager decoding token for token; and the
+    last step, attending over 2175 cached positions, agrees with a prefill of
+    the whole generated sequence."""
     cfg = Q.QWEN3_8B
     assert cfg.num_layers == 36 and cfg.hidden_size == 4096 and cfg.vocab_size == 151936
-    L, steps = 200, 6
+    L, steps = 2048, 128
     a = Q.Qwen3(cfg, max_len=L + steps + 2, seed=31)
     ids = torch.randint(0, cfg.vocab_size, (L + 1,), device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(32))
     full = a.prefill(ids)                        # positions 0..L
-    assert torch.isfinite(full).all()
+    assert full.shape == (L + 1, cfg.vocab_size) and torch.isfinite(full).all()
     a.prefill(ids[:L])                           # cache for 0..L-1
     dec = a.decode_step(ids[L:L + 1], torch.tensor([L], device="cuda"))
     assert torch.isfinite(dec).all()
     c = _cos(dec[0], full[L])
-    print(f"qwen3-8b full depth: decode vs prefill cosine {c:.6f}", flush=True)
-    assert c > 0.995, f"decode vs prefill at full depth: cosine {c:.5f}"
-    # graph replays reproduce eager decoding token for token
+    print(f"qwen3-8b configs[3]: decode vs prefill at {L}: cosine {c:.6f}", flush=True)
+    assert c > 0.995, f"decode vs prefill at position {L}: cosine {c:.5f}"
+    del full
+    # 128 greedy steps: graph replays reproduce eager decoding token for token
     ta = a.generate(ids[:L], steps, graph=True)
     tb = a.generate(ids[:L], steps, graph=False)
-    assert torch.equal(ta, tb)
+    assert ta.shape == (steps,) and torch.equal(ta, tb), \
+        f"graph and eager decoding differ at step {int((ta != tb).nonzero()[0])}"
+    print(f"qwen3-8b configs[3]: {steps} graph steps = eager, "
+          f"{int(ta.unique().numel())} distinct tokens", flush=True)
+    # the last decode step (slot L + steps - 1, 2175 positions) against a
+    # prefill of prompt + generated tokens
+    seq = torch.cat([ids[:L], ta])               # L + steps ids
+    last = L + steps - 1
+    ref = a.prefill(seq)[last]
+    a.prefill(seq[:last])
+    dec = a.decode_step(seq[last:last + 1], torch.tensor([last], device="cuda"))
+    c = _cos(dec[0], ref)
+    print(f"qwen3-8b configs[3]: decode vs prefill at {last}: cosine {c:.6f}", flush=True)
+    assert c > 0.995, f"decode vs prefill at position {last}: cosine {c:.5f}"
     del a
     torch.cuda.empty_cache()
 
 
-def test_qwen3_vl_2b_full_depth_properties():
+@pytest.mark.parametrize("L,n_img", [(1334, 2), (2393, 3), (3455, 4)])
+def test_qwen3_vl_2b_config4_prompts(L, n_img):
+    """configs[4] at its three prompts (1334 / 2393 / 3455 tokens with 2 / 3 /
+    4 image blocks of 256 tokens, 3-axis M-RoPE positions), full 28-layer
+    Qwen3-VL-2B shape: chunked prefill (chunk 512) agrees with one-shot
+    prefill; decode continues the M-RoPE positions (the next token decoded
+    agrees with prefilling it); HIP-graph decode reproduces eager decode
+    token for token over 32 steps."""
     cfg = V.QWEN3_VL_2B
     assert cfg.num_layers == 28 and cfg.hidden_size == 2048 and cfg.vocab_size == 151936
-    segs = V.synth_segments(1334, 2, seed=41)
-    L, steps = 1334, 6
+    segs = V.synth_segments(L, n_img, seed=41 + L)
+    assert sum(1 for kind, _ in segs if kind == "image") == n_img
+    steps = 32
     m = V.Qwen3VL(cfg, max_len=L + steps + 2, seed=42)
     x, _ = m.embed_prompt(segs, seed=43)
+    assert x.shape == (L, cfg.hidden_size)
     pos3 = V.rope_index(segs)
     chunked = m.prefill_chunked(x, pos3, chunk=512)
     assert torch.isfinite(chunked).all()
     one = m.prefill_chunked(x, pos3, chunk=L)
     c = _cos(chunked, one)
-    print(f"qwen3-vl-2b full depth: chunked vs one-shot cosine {c:.6f}", flush=True)
-    assert c > 0.995, f"chunked vs one-shot prefill at full depth: cosine {c:.5f}"
+    print(f"qwen3-vl-2b {L} tokens: chunked vs one-shot cosine {c:.6f}", flush=True)
+    assert c > 0.995, f"chunked vs one-shot prefill at {L} tokens: cosine {c:.5f}"
     # decode continues the M-RoPE positions: the next token decoded equals
     # prefilling it as text at the next position
     m.prefill_chunked(x, pos3, chunk=512)
@@ -117,8 +149,10 @@ def test_qwen3_vl_2b_full_depth_properties():
     p2 = torch.cat([pos3, torch.full((3, 1), int(pos3.max()) + 1)], 1)
     full = m.prefill_chunked(x2, p2, chunk=512)
     c = _cos(dec[0], full[0])
-    print(f"qwen3-vl-2b full depth: decode vs prefill cosine {c:.6f}", flush=True)
+    print(f"qwen3-vl-2b {L} tokens: decode vs prefill cosine {c:.6f}", flush=True)
     assert c > 0.995, f"decode vs prefill of the same token: cosine {c:.5f}"
     ta = m.generate_from_prompt(segs, steps, seed=43, chunk=512, graph=True)
     tb = m.generate_from_prompt(segs, steps, seed=43, chunk=512, graph=False)
     assert torch.equal(ta, tb)
+    del m
+    torch.cuda.empty_cache()
