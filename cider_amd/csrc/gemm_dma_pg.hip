@@ -635,7 +635,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 // group g from C = 0, with scales read into registers during the sub-step
 // before.  Before the first group D is zero and the scales are the zero row;
 // the last group is flushed after the k-loop.
-template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN, int OCC = 1>
+template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN, int OCC = 1, int FL = 0>
 __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
   using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
@@ -780,8 +780,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       for (int b = 0; b < TM; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
-          facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
+          if constexpr (FL == 1) {
+            facc[a][b][4 * q + r] =
+                __builtin_fmaf((float)D[a][b][4 * q + r], svp[a][q][r], facc[a][b][4 * q + r]);
+          } else {
+            const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
+            facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
+          }
           asm volatile("" : "+v"(facc[a][b][4 * q + r]));
         }
   };
