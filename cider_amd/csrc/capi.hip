@@ -162,7 +162,6 @@ int cider_version(void) { return 100; }  // 0.1.0
 const char* cider_last_error(void) { return g_last_error.c_str(); }
 
 size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K, int group_size) {
-  (void)group_size;
   if (M <= 0 || K < 0) return 0;
   switch (op) {
     case CIDER_OP_PERCHANNEL:
@@ -172,10 +171,18 @@ size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K, int group_
       if (N <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return quant_ws_bytes(M, K);
       return quant_ws_bytes(M, K) + align256(cider::splitk_bytes((int)M, (int)N, (int)K));
     case CIDER_OP_PERGROUP:
-      return M <= 1 ? 0 : quant_ws_bytes(M, K);
+      // quantized activations and scales, plus the fp32 partial sums of the
+      // split-K GEMM where that shape takes it
+      if (M <= 1) return 0;
+      if (N <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return quant_ws_bytes(M, K);
+      return quant_ws_bytes(M, K) +
+             align256(cider::pg_splitk_bytes((int)M, (int)N, (int)K, group_size));
     case CIDER_OP_W4A8:
-    case CIDER_OP_W4A8_PERGROUP:
       return quant_ws_bytes(M, K);
+    case CIDER_OP_W4A8_PERGROUP:
+      if (N <= 0 || M > INT32_MAX || N > INT32_MAX || K > INT32_MAX) return quant_ws_bytes(M, K);
+      return quant_ws_bytes(M, K) +
+             align256(cider::pg_splitk_bytes((int)M, (int)N, (int)K, group_size));
     case CIDER_OP_W4A8_REF:
       if (N < 0) return 0;
       return quant_ws_bytes(M, K) + align256((size_t)N * (size_t)(K / 2));
@@ -285,6 +292,23 @@ int cider_perchannel_linear_noalloc(const void* x_f16, const int8_t* w_nk, const
   return cider_perchannel_linear(x_f16, w_nk, sw, bias_f16, y_f16, ws, need, M, N, K, stream);
 }
 
+namespace {
+
+// The split-K partial sums of a per-group linear in the caller's workspace
+// (after the quantized activations), when the shape takes the split and the
+// workspace holds them; nullptr runs the one-pass GEMM (same contract, the
+// sequential chain).
+float* pg_splitk_part(const cider::GemmArgs& g, void* ws, size_t ws_bytes, int gs) {
+  const int S = cider::pg_splitk_ways(g.M, g.N, g.K, gs);
+  if (S <= 1) return nullptr;
+  const size_t qbytes = quant_ws_bytes(g.M, g.K);
+  if (ws_bytes < qbytes + cider::pg_splitk_bytes(g.M, g.N, g.K, gs)) return nullptr;
+  if (!(aligned16(g.x) && aligned16(g.w) && aligned16(g.y) && aligned16(g.sw))) return nullptr;
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + qbytes);
+}
+
+}  // namespace
+
 int cider_pergroup_linear(const void* x_f16, const int8_t* w_nk, const float* sw_gn,
                           const void* bias_f16, void* y_f16, void* ws, size_t ws_bytes,
                           int64_t M, int64_t N, int64_t K, int group_size, void* stream) {
@@ -316,6 +340,13 @@ int cider_pergroup_linear(const void* x_f16, const int8_t* w_nk, const float* sw
   float* sa;
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
   cider::GemmArgs g{q, w_nk, sa, sw_gn, bias, y_f16, (int)M, (int)N, (int)K};
+  float* part = pg_splitk_part(g, ws, ws_bytes, group_size);
+  if (part)
+    return hip_status(cider::launch_gemm_pg_splitk(g, group_size, false, cider::W_I8,
+                                                   cider::pg_splitk_ways((int)M, (int)N, (int)K,
+                                                                         group_size),
+                                                   part, s),
+                      fn);
   return hip_status(cider::launch_gemm(g, cider::W_I8, cider::EPI_PG, false, group_size, s), fn);
 }
 
@@ -408,6 +439,13 @@ int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
   CIDER_TRY(quantize_into_ws(fn, x_f16, ws, M, K, s, &q, &sa));
   cider::GemmArgs g{q, w4_nk, sa, scale_gn_f16, reinterpret_cast<const uint16_t*>(bias_f16),
                     y_f16, (int)M, (int)N, (int)K};
+  float* part = pg_splitk_part(g, ws, ws_bytes, group_size);
+  if (part)
+    return hip_status(cider::launch_gemm_pg_splitk(g, group_size, true, cider::W_I4,
+                                                   cider::pg_splitk_ways((int)M, (int)N, (int)K,
+                                                                         group_size),
+                                                   part, s),
+                      fn);
   return hip_status(cider::launch_gemm(g, cider::W_I4, cider::EPI_PG, true, group_size, s), fn);
 }
 

@@ -117,8 +117,100 @@ constexpr int PG_LAUNCH_BN = 64;
 
 }  // namespace
 
+// Whether every group scale of columns [n0, n0 + BN) (sw [G, N], fp32 or fp16)
+// is finite with |s| < 2^64.  Then |D_g * s| < 2^22 * 2^64 and no term or
+// running sum of the exact or the fma flush comes near the binary32 range
+// (K < 2^24), so neither chain meets an infinity or NaN, and the fma flush
+// differs from the exact one by the rounding of each product alone.  Each
+// thread reads 16-byte chunks of the block (L2-resident: every tile of the
+// column reads it); the caller votes over the workgroup.
+template <int BN, bool SWH>
+__device__ __forceinline__ bool pg_scales_tame(const GemmArgs& p, int n0, int G, int nthreads) {
+  constexpr int ESZ = SWH ? 2 : 4, PER16 = 16 / ESZ, CPRS = BN / PER16;
+  const int N = p.N, tid = threadIdx.x;
+  const int total = G * CPRS;
+  uint32_t mx = 0;
+  for (int c0 = 0; c0 < total; c0 += 8 * nthreads) {
+    i32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = min(c0 + u * nthreads + tid, total - 1);
+      const int g = idx / CPRS, col = min(n0 + (idx % CPRS) * PER16, N - PER16);
+      v[u] = *reinterpret_cast<const i32x4*>(reinterpret_cast<const int8_t*>(p.sw) +
+                                             ((int64_t)g * N + col) * ESZ);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)v[u][e];
+        if constexpr (SWH)
+          mx = max(mx, max(w & 0x7fffu, (w >> 16) & 0x7fffu));
+        else
+          mx = max(mx, w & 0x7fffffffu);
+      }
+  }
+  return SWH ? mx < 0x7c00u : mx < 0x5f800000u;  // fp16 finite / fp32 below 2^64
+}
+
+// The exact per-group chain for one BM x BN tile, straight from global
+// memory: each thread computes whole outputs (v_dot4 int32 group sums, then
+// acc = acc + f32(f32(D_g) * s) in group order, y = h(f32(acc * sa) [+ bias])).
+// The fallback of the fma-flush kernels for tiles whose scales are not all
+// finite and below 2^64; real weights' scales never are, so its speed does
+// not matter, only its results.  `kbeg`, `kend`: the k range (a split-K
+// slice), `part`: fp32 partial sums [M, N] of that slice instead of y.
+template <int BM, int BN, int GS, bool SWH, int WF>
+__device__ __forceinline__ void pg_exact_tile(const GemmArgs& p, int m0, int n0,
+                                                        int nthreads, int kbeg = 0,
+                                                        int kend = -1, float* part = nullptr) {
+  constexpr bool W4 = (WF == W_I4);
+  const int M = p.M, N = p.N, K = p.K;
+  if (kend < 0) kend = K;
+  const int64_t ldw = W4 ? (K >> 1) : K;
+  for (int idx = threadIdx.x; idx < BM * BN; idx += nthreads) {
+    const int m = m0 + idx / BN, n = n0 + idx % BN;
+    if (m >= M || n >= N) continue;
+    const int8_t* xr = p.x + (int64_t)m * K;
+    const int8_t* wr = reinterpret_cast<const int8_t*>(p.w) + (int64_t)n * ldw;
+    float acc = 0.0f;
+    for (int g = kbeg / GS; g < kend / GS; ++g) {
+      int32_t d = 0;
+      for (int k = g * GS; k < (g + 1) * GS; k += 8) {
+        const i32x2 xv = ld8(xr + k);
+        uint32_t w0, w1;
+        if constexpr (W4) {
+          unpack_w4_word(*reinterpret_cast<const uint32_t*>(wr + k / 2), w0, w1);
+        } else {
+          const i32x2 wv = ld8(wr + k);
+          w0 = (uint32_t)wv[0];
+          w1 = (uint32_t)wv[1];
+        }
+        d = __builtin_amdgcn_sdot4(xv[0], (int)w0, d, false);
+        d = __builtin_amdgcn_sdot4(xv[1], (int)w1, d, false);
+      }
+      const int64_t si = (int64_t)g * N + n;
+      const float sc = SWH ? h2f(reinterpret_cast<const uint16_t*>(p.sw)[si])
+                           : reinterpret_cast<const float*>(p.sw)[si];
+      const float t = (float)d * sc;
+      acc = acc + t;
+    }
+    if (part) {
+      part[(int64_t)m * N + n] = acc;
+    } else {
+      float v = acc * p.sa[m];
+      if (p.bias) v = v + h2f(p.bias[n]);
+      reinterpret_cast<uint16_t*>(p.y)[(int64_t)m * N + n] = f2h(v);
+    }
+  }
+}
+
+// ks > 0: split-K.  Workgroup (t, s) runs tile t over k in [s ks, (s+1) ks)
+// (whole groups and k-stages) and writes its fp32 group chain, before the
+// per-token scale, to part + s M N; pg_splitk_sum_kernel adds the slices.
 template <int BM, int BN, int GS, bool SWH, int WF, int OCC, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const GemmArgs p) {
+__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const GemmArgs pin,
+                                                                          int ks, float* part) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
   using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
   constexpr int NW = C::NW;
@@ -157,9 +249,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WGM, wn = wave / WGM;
   const int h = lane >> 5;
+  // K is the row pitch; the k-loop covers KL of it (a split-K slice: the
+  // operands and scales start at the slice, and the partial sums go to pp)
+  GemmArgs p = pin;
+  float* pp = nullptr;
+  if (ks > 0) {
+    const int sl = blockIdx.y;
+    p.x = pin.x + (int64_t)sl * ks;
+    p.w = reinterpret_cast<const int8_t*>(pin.w) + (int64_t)sl * (W4 ? ks / 2 : ks);
+    p.sw = reinterpret_cast<const int8_t*>(pin.sw) + (int64_t)(sl * (ks / GS)) * pin.N * ESZ;
+    pp = part + (int64_t)sl * pin.M * pin.N;
+  }
   const int M = p.M, N = p.N, K = p.K;
-  const int G = K / GS;
-  const int nk = K / PG_BK;
+  const int KL = ks > 0 ? ks : K;
+  const int G = KL / GS;
+  const int nk = KL / PG_BK;
   int m0, n0;
   tile_coords<PG_BM, PG_BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
 
@@ -243,9 +347,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   uint16_t b_t = 0;
 
   // One pass over K into facc: prologue, k-loop and the last group's flush.
-  // FAST (fp16 scales only) flushes with the biased sums (kPgBiasBits).
-  auto kpass = [&](auto fastc) __attribute__((always_inline)) {
-    constexpr bool FAST = decltype(fastc)::value != 0;
+  // MODE 0: the exact flush; 1 (FAST, fp16 scales only): the biased sums
+  // (kPgBiasBits), also exact; 2 (FMA, fp32 scales): facc = fma(f32(D), s,
+  // facc) for tiles whose scales pass pg_scales_tame (else the tile runs
+  // pg_exact_tile and kpass returns false: y is written, no epilogue).
+  auto kpass = [&](auto modec) __attribute__((always_inline)) -> bool {
+    constexpr int MODE = decltype(modec)::value;
+    constexpr bool FAST = MODE == 1, FMA = MODE == 2;
     // Two int32 group sets alternate by group (set = group parity); while
     // group g accumulates, group g-1 is flushed, EPS of its accumulators per
     // sub-step over the SUBG sub-steps of group g (accumulator e of a set:
@@ -401,8 +509,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
           const int c = combo - SL * EPS / EPC;  // combo within the sub-step's scales
           const int aa = combo / 4, r = 4 * (combo % 4) + rr;
           constexpr int SB = SVDB ? (J & 1) : 0;
-          const float t = term(D[1 - CS][aa][bb][r], sv[SB][c], sr[SB][c], rr);
-          facc[aa][bb][r] = facc[aa][bb][r] + t;
+          if constexpr (FMA) {
+            facc[aa][bb][r] = __builtin_fmaf((float)D[1 - CS][aa][bb][r], sv[SB][c][rr],
+                                             facc[aa][bb][r]);
+          } else {
+            const float t = term(D[1 - CS][aa][bb][r], sv[SB][c], sr[SB][c], rr);
+            facc[aa][bb][r] = facc[aa][bb][r] + t;
+          }
           // Pins this flush element to its slot: without it the compiler sinks
           // the whole flush of a group below the next group's MFMAs, in one
           // VALU block that the MFMAs no longer hide (and, at 64 x 64 waves,
@@ -431,11 +544,30 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       dma_stage(min(st, nk - 1), st);
       if (wave == 0) dma_scales(min(st, nk - 1));
     }
+    bool tame = true;
+    if constexpr (FMA) tame = pg_scales_tame<PG_BN, SWH>(p, n0, G, 64 * NW);
     if (wave == 0)
       wait_vmcnt<(PG_NS - 1) * (PG_PS + 1)>();
     else
       wait_vmcnt<(PG_NS - 1) * PG_PS>();
-    __syncthreads();
+    if constexpr (FMA) {
+      // workgroup vote in the unused upper half of the zero row's scale slot
+      // (its first scale DMA comes stages later)
+      static_assert(ROWB + 4 * NW <= PG_SSLOT, "vote words");
+      uint32_t* vote = reinterpret_cast<uint32_t*>(smem + kZeroRow + ROWB);
+      if (lane == 0) vote[wave] = __builtin_amdgcn_ballot_w64(!tame) != 0 ? 1u : 0u;
+      __syncthreads();
+      uint32_t any = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) any |= vote[w];
+      if (any) {
+        wait_vmcnt<0>();  // the prologue's DMA lands before the workgroup ends
+        pg_exact_tile<PG_BM, PG_BN, GS, SWH, WF>(p, m0, n0, 64 * NW, 0, KL, pp);
+        return false;
+      }
+    } else {
+      __syncthreads();
+    }
 #pragma unroll
     for (int b = 0; b < PG_TM; ++b) read_x(0, 0, b, xf[0]);
 #pragma unroll
@@ -506,8 +638,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
           for (int bb = 0; bb < PG_TM; ++bb)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
-              const float t = term(D[CSL][aa][bb][4 * q + rr], s4, r4, rr);
-              facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+              if constexpr (FMA) {
+                facc[aa][bb][4 * q + rr] = __builtin_fmaf((float)D[CSL][aa][bb][4 * q + rr],
+                                                          s4[rr], facc[aa][bb][4 * q + rr]);
+              } else {
+                const float t = term(D[CSL][aa][bb][4 * q + rr], s4, r4, rr);
+                facc[aa][bb][4 * q + rr] = facc[aa][bb][4 * q + rr] + t;
+              }
             }
         }
       }
@@ -544,12 +681,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       }
     }
     wait_vmcnt<0>();  // reloads past the end land before LDS is reused
+    return true;
   };
 
   // the fast flush where its registers fit (int8 weights at two workgroups
   // per CU would drop to one)
   constexpr bool FASTOK = SWH && !(WF == W_I8 && OCC == 2);
-  if constexpr (FASTOK) {
+  if constexpr (!SWH) {
+    if (!kpass(ic<2>{})) return;  // the tile ran the exact fallback
+  } else if constexpr (FASTOK) {
     kpass(ic<1>{});
     // A NaN accumulator means a scale of the tile's columns was not finite
     // (finite fp16 scales keep every fast term finite: |D * s| < 2^22 * 2^16).
@@ -574,6 +714,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
     kpass(ic<0>{});
   }
 
+  if (pp) {
+    // split-K slice: the chain's fp32 sums, 4 consecutive columns per store
+#pragma unroll
+    for (int a = 0; a < PG_TN; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int b = 0; b < PG_TM; ++b) {
+          const int m = m0 + wm * PG_WM + b * 32 + frow;
+          const int n = n0 + wn * PG_WN + a * 32 + 8 * q + 4 * h;
+          if (m < M && n < N)
+            *reinterpret_cast<f32x4*>(pp + (int64_t)m * N + n) =
+                f32x4{facc[a][b][4 * q], facc[a][b][4 * q + 1], facc[a][b][4 * q + 2],
+                      facc[a][b][4 * q + 3]};
+        }
+    return;
+  }
   // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
   float* ssa = reinterpret_cast<float*>(smem + PG_OUT);
   uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + PG_BM);
@@ -745,17 +902,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
     }
   };
 
-  i32x16 D[TN][TM];
   float facc[TN][TM][16];
-#pragma unroll
-  for (int a = 0; a < TN; ++a)
-#pragma unroll
-    for (int b = 0; b < TM; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        D[a][b][r] = 0;
-        facc[a][b][r] = 0.0f;
-      }
   i32x16 zero16;
 #pragma unroll
   for (int r = 0; r < 16; ++r) zero16[r] = 0;
@@ -769,95 +916,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
 #pragma unroll
       for (int q = 0; q < 4; ++q) read_scales(g, a, q, svp[a][q]);
   };
-  // flush of block row a (blocks (a, 0 .. TM-1)), each element pinned after
-  // its add so the compiler keeps the conversions next to their use.  (The
-  // fast flush of fp16 scales, one fma per term from a biased sum, measured
-  // slower here: int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
-  auto flush_row = [&](int a) __attribute__((always_inline)) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int b = 0; b < TM; ++b)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          if constexpr (FL == 1) {
-            facc[a][b][4 * q + r] =
-                __builtin_fmaf((float)D[a][b][4 * q + r], svp[a][q][r], facc[a][b][4 * q + r]);
-          } else {
-            const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
-            facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
-          }
-          asm volatile("" : "+v"(facc[a][b][4 * q + r]));
-        }
-  };
 
-  // One k sub-step in a fixed order: per MFMA slot (block a, b), the flush of
-  // the block's previous group (first sub-step of a group), the MFMA, one of
-  // the next sub-step's fragment reads (rd) and a share of the DMA loads of
-  // stage dst into slot dsl (dma); before a sub-step that flushes (pre), the
-  // scales of group pg after the first MFMA.
-  auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, auto prec, const i32x4 (&wc)[TN],
-                  const i32x4 (&xc)[TM], int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst,
-                  int dsl, int pg) __attribute__((always_inline)) {
-    constexpr bool first = decltype(firstc)::value != 0;
-    constexpr bool pre = decltype(prec)::value != 0;
-    constexpr bool rd = decltype(rdc)::value != 0;
-    constexpr bool dma = decltype(dmac)::value != 0;
-    constexpr int JN = decltype(JNc)::value;
-#pragma unroll
-    for (int idx = 0; idx < NMF; ++idx) {
-      const int a = idx / TM, b = idx % TM;
-      if constexpr (first) {
-        if (b == 0) flush_row(a);
-        D[a][b] = mfma32(wc[a], xc[b], zero16);
-      } else {
-        D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
-      }
-      if constexpr (rd && !W4) {
-#pragma unroll
-        for (int q = 0; q < NR; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx) {
-            if (q == 0)
-              read_w(rs, JN, 0, wn_);
-            else if (q <= TM)
-              read_x(rs, JN, q - 1, xn);
-            else
-              read_w(rs, JN, q - TM, wn_);
-          }
-      }
-      if constexpr (rd && W4) {
-        // X fragments first; on a new pair the raw W chunks next, each
-        // unpacked in a later slot than its read (the slots issue reads
-        // before unpacks); otherwise the held chunks' second halves
-        constexpr bool new_pair = (JN % 2) == 0;
-        constexpr int NRD = TM + (new_pair ? TN : 0);
-#pragma unroll
-        for (int q = 0; q < NRD; ++q)
-          if ((q < NMF ? q : NMF - 1) == idx) {
-            if (q < TM)
-              read_x(rs, JN, q, xn);
-            else
-              read_w(rs, JN, q - TM, raw);
-          }
-#pragma unroll
-        for (int a2 = 0; a2 < TN; ++a2) {
-          constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
-          const int want = first_slot + a2 > TM + a2 || !new_pair ? first_slot + a2 : TM + a2;
-          if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
-        }
-      }
-      if constexpr (dma) {
-#pragma unroll
-        for (int d = 0; d < PS; ++d)
-          if (d * NMF / PS == idx) dma_one(dst, dsl, d);
-        if (idx == 0 && wave == 0) dma_scales(dst);
-      }
-      if constexpr (pre) {
-        if (idx == 0) prefetch(pg);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
   auto wait_stage = [&]() __attribute__((always_inline)) {
     if (wave == 0)
       wait_vmcnt<(NS - 2) * (PS + 1)>();
@@ -880,122 +939,270 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       dma16s(xbase + (int64_t)s2 * BK, xoff[i], sb + W_BYTES + (wave * XI + i) * 1024);
     if (wave == 0) dma_scales(s2);
   }
+  // FL == 1: the fma flush for tiles whose scales are all finite with
+  // |s| < 2^64, the exact flush otherwise (a workgroup-uniform choice).  The
+  // scan's loads go out behind the prologue's, so their latency overlaps it.
+  bool tame = true;
+  if constexpr (FL == 1) tame = pg_scales_tame<BN, SWH>(p, n0, G, 64 * NW);
   if (wave == 0)
     wait_vmcnt<(NS - 1) * (PS + 1)>();
   else
     wait_vmcnt<(NS - 1) * PS>();
-  __syncthreads();
+  bool fma_tile = false;
+  if constexpr (FL == 1) {
+    // workgroup vote in the unused upper half of the zero row's scale slot
+    // (no extra LDS: at int4, 256 more bytes stopped two workgroups from
+    // sharing a CU); that slot's first scale DMA comes stages later
+    static_assert(ROWB + 4 * NW <= SSLOT, "vote words");
+    uint32_t* vote = reinterpret_cast<uint32_t*>(smem + kZeroRow + ROWB);
+    const bool wbad = __builtin_amdgcn_ballot_w64(!tame) != 0;
+    if (lane == 0) vote[wave] = wbad ? 1u : 0u;
+    __syncthreads();
+    uint32_t any = 0;
 #pragma unroll
-  for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
-#pragma unroll
-  for (int a = 0; a < TN; ++a) {
-    if constexpr (W4) {
-      read_w(0, 0, a, raw);
-      unpack_half(a, 0, wf[0]);
-    } else {
-      read_w(0, 0, a, wf[0]);
-    }
+    for (int w = 0; w < NW; ++w) any |= vote[w];
+    fma_tile = any == 0;
+  } else {
+    __syncthreads();
   }
-  prefetch(-1);  // the first flush: zero sums, zero scales
-
   float sa_t = 0.0f;
   uint16_t b_t = 0;
-  // Stage kt at position HALF of a PER-stage period: sub-step J starts group
-  // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before;
-  // the sub-step before it reads that group's scales (PRE).
-  auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
-    constexpr int HALF = decltype(halfc)::value;
-    constexpr bool LAST = decltype(lastc)::value != 0;
-    const int sl = kt % NS;
-    if constexpr (LAST) {
-      sa_t = p.sa[min(m0 + tid % BM, M - 1)];
-      if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
-    }
-#define PG1_SUB(J)                                                                              \
-  {                                                                                             \
-    constexpr bool FIRST = ((4 * HALF + (J)) % SUBG) == 0;                                      \
-    constexpr bool PRE = ((4 * HALF + (J) + 1) % SUBG) == 0;                                    \
-    const int pg = (4 * kt + (J) + 1) / SUBG - 1;                                               \
-    if constexpr ((J) < 3) {                                                                    \
-      step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, ic<PRE>{}, wf[(J) & 1], xf[(J) & 1],   \
-           sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, pg);                                 \
-    } else if constexpr (!LAST) {                                                               \
-      wait_stage();                                                                             \
-      __syncthreads();                                                                          \
-      step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], (kt + 1) % NS,      \
-           wf[0], xf[0], min(kt + NS, nk - 1), sl, pg);                                         \
-    } else {                                                                                    \
-      step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, \
-           0, pg);                                                                              \
-    }                                                                                           \
-  }
-    PG1_SUB(0)
-    PG1_SUB(1)
-    PG1_SUB(2)
-    PG1_SUB(3)
-#undef PG1_SUB
-  };
-  int kt = 0;
-  if constexpr (PER == 1) {
-    for (; kt + 1 < nk; ++kt) stage(kt, ic<0>{}, ic<0>{});
-    stage(kt, ic<0>{}, ic<1>{});
-  } else {
-    // gs 256: K % 256 == 0, so nk is even
-    for (; kt + 2 < nk; kt += 2) {
-      stage(kt, ic<0>{}, ic<0>{});
-      stage(kt + 1, ic<1>{}, ic<0>{});
-    }
-    stage(kt, ic<0>{}, ic<0>{});
-    stage(kt + 1, ic<1>{}, ic<1>{});
-  }
-  // the last group (its scales were read in the last sub-step)
+  // The k-loop with the flush of FMAc (1: fma, 0: exact): fragment reads of
+  // stage 0, the stages, and the last group's flush.
+  auto body = [&](auto fmac) __attribute__((always_inline)) {
+    constexpr bool FMA = decltype(fmac)::value != 0;
+    i32x16 D[TN][TM];
 #pragma unroll
-  for (int a = 0; a < TN; ++a) flush_row(a);
-  wait_vmcnt<0>();  // reloads past the end land before LDS is reused
-
-  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
-  float* ssa = reinterpret_cast<float*>(smem + OUT);
-  uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + BM);
-  __syncthreads();  // every wave is done with the ring
-  if (tid < BM) ssa[tid] = sa_t;
-  if (tid < BN) sbias[tid] = b_t;
-  __syncthreads();
+    for (int a = 0; a < TN; ++a)
 #pragma unroll
-  for (int a = 0; a < TN; ++a) {
+      for (int b = 0; b < TM; ++b)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
-      const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
-      const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
-                           h2f((uint16_t)((uint32_t)bb[0] >> 16)),
-                           h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
-                           h2f((uint16_t)((uint32_t)bb[1] >> 16))};
-#pragma unroll
-      for (int b = 0; b < TM; ++b) {
-        const int ml = wm * WM + b * 32 + frow;
-        const float sam = ssa[ml];
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v = facc[a][b][4 * q + r] * sam;
-          if (p.bias) v = v + bv[r];
-          o[r] = v;
+        for (int r = 0; r < 16; ++r) {
+          D[a][b][r] = 0;
+          facc[a][b][r] = 0.0f;
         }
-        *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
-            i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+    // flush of block row a (blocks (a, 0 .. TM-1)), each element pinned after
+    // its update so the compiler keeps the conversions next to their use.
+    // FMA: facc = fma(f32(D), s, facc), 2 VALU ops per accumulator (the
+    // product is not rounded on its own); exact: facc = facc + f32(f32(D) * s),
+    // the reference's two roundings, 3 ops.  (A bit-exact fast flush of fp16
+    // scales, one fma per term from a biased sum plus the add, measured slower
+    // here: int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
+    auto flush_row = [&](int a) __attribute__((always_inline)) {
+  #pragma unroll
+      for (int q = 0; q < 4; ++q)
+  #pragma unroll
+        for (int b = 0; b < TM; ++b)
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if constexpr (FMA) {
+              facc[a][b][4 * q + r] =
+                  __builtin_fmaf((float)D[a][b][4 * q + r], svp[a][q][r], facc[a][b][4 * q + r]);
+            } else {
+              const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
+              facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
+            }
+            asm volatile("" : "+v"(facc[a][b][4 * q + r]));
+          }
+    };
+
+    // One k sub-step in a fixed order: per MFMA slot (block a, b), the flush of
+    // the block's previous group (first sub-step of a group), the MFMA, one of
+    // the next sub-step's fragment reads (rd) and a share of the DMA loads of
+    // stage dst into slot dsl (dma); before a sub-step that flushes (pre), the
+    // scales of group pg after the first MFMA.
+    auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, auto prec, const i32x4 (&wc)[TN],
+                    const i32x4 (&xc)[TM], int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst,
+                    int dsl, int pg) __attribute__((always_inline)) {
+      constexpr bool first = decltype(firstc)::value != 0;
+      constexpr bool pre = decltype(prec)::value != 0;
+      constexpr bool rd = decltype(rdc)::value != 0;
+      constexpr bool dma = decltype(dmac)::value != 0;
+      constexpr int JN = decltype(JNc)::value;
+  #pragma unroll
+      for (int idx = 0; idx < NMF; ++idx) {
+        const int a = idx / TM, b = idx % TM;
+        if constexpr (first) {
+          if (b == 0) flush_row(a);
+          D[a][b] = mfma32(wc[a], xc[b], zero16);
+        } else {
+          D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
+        }
+        if constexpr (rd && !W4) {
+  #pragma unroll
+          for (int q = 0; q < NR; ++q)
+            if ((q < NMF ? q : NMF - 1) == idx) {
+              if (q == 0)
+                read_w(rs, JN, 0, wn_);
+              else if (q <= TM)
+                read_x(rs, JN, q - 1, xn);
+              else
+                read_w(rs, JN, q - TM, wn_);
+            }
+        }
+        if constexpr (rd && W4) {
+          // X fragments first; on a new pair the raw W chunks next, each
+          // unpacked in a later slot than its read (the slots issue reads
+          // before unpacks); otherwise the held chunks' second halves
+          constexpr bool new_pair = (JN % 2) == 0;
+          constexpr int NRD = TM + (new_pair ? TN : 0);
+  #pragma unroll
+          for (int q = 0; q < NRD; ++q)
+            if ((q < NMF ? q : NMF - 1) == idx) {
+              if (q < TM)
+                read_x(rs, JN, q, xn);
+              else
+                read_w(rs, JN, q - TM, raw);
+            }
+  #pragma unroll
+          for (int a2 = 0; a2 < TN; ++a2) {
+            constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
+            const int want = first_slot + a2 > TM + a2 || !new_pair ? first_slot + a2 : TM + a2;
+            if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
+          }
+        }
+        if constexpr (dma) {
+  #pragma unroll
+          for (int d = 0; d < PS; ++d)
+            if (d * NMF / PS == idx) dma_one(dst, dsl, d);
+          if (idx == 0 && wave == 0) dma_scales(dst);
+        }
+        if constexpr (pre) {
+          if (idx == 0) prefetch(pg);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+  #pragma unroll
+    for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
+  #pragma unroll
+    for (int a = 0; a < TN; ++a) {
+      if constexpr (W4) {
+        read_w(0, 0, a, raw);
+        unpack_half(a, 0, wf[0]);
+      } else {
+        read_w(0, 0, a, wf[0]);
       }
     }
-  }
-  __syncthreads();
-  constexpr int LPR = BN / 8, RPS = 64 / LPR;
-  const int cl = (lane % LPR) * 8;
-  const int n = n0 + cl;
-#pragma unroll 4
-  for (int rr = wave * RPS + lane / LPR; rr < BM; rr += NW * RPS) {
-    const int m = m0 + rr;
-    if (m < M && n < N)
-      *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
-          *reinterpret_cast<const i32x4*>(smem + rr * OUT_LD + cl * 2);
+    prefetch(-1);  // the first flush: zero sums, zero scales
+
+    // Stage kt at position HALF of a PER-stage period: sub-step J starts group
+    // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before;
+    // the sub-step before it reads that group's scales (PRE).
+    auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
+      constexpr int HALF = decltype(halfc)::value;
+      constexpr bool LAST = decltype(lastc)::value != 0;
+      const int sl = kt % NS;
+      if constexpr (LAST) {
+        sa_t = p.sa[min(m0 + tid % BM, M - 1)];
+        if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
+      }
+  #define PG1_SUB(J)                                                                              \
+    {                                                                                             \
+      constexpr bool FIRST = ((4 * HALF + (J)) % SUBG) == 0;                                      \
+      constexpr bool PRE = ((4 * HALF + (J) + 1) % SUBG) == 0;                                    \
+      const int pg = (4 * kt + (J) + 1) / SUBG - 1;                                               \
+      if constexpr ((J) < 3) {                                                                    \
+        step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, ic<PRE>{}, wf[(J) & 1], xf[(J) & 1],   \
+             sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, pg);                                 \
+      } else if constexpr (!LAST) {                                                               \
+        wait_stage();                                                                             \
+        __syncthreads();                                                                          \
+        step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], (kt + 1) % NS,      \
+             wf[0], xf[0], min(kt + NS, nk - 1), sl, pg);                                         \
+      } else {                                                                                    \
+        step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, \
+             0, pg);                                                                              \
+      }                                                                                           \
+    }
+      PG1_SUB(0)
+      PG1_SUB(1)
+      PG1_SUB(2)
+      PG1_SUB(3)
+  #undef PG1_SUB
+    };
+    int kt = 0;
+    if constexpr (PER == 1) {
+      for (; kt + 1 < nk; ++kt) stage(kt, ic<0>{}, ic<0>{});
+      stage(kt, ic<0>{}, ic<1>{});
+    } else {
+      // gs 256: K % 256 == 0, so nk is even
+      for (; kt + 2 < nk; kt += 2) {
+        stage(kt, ic<0>{}, ic<0>{});
+        stage(kt + 1, ic<1>{}, ic<0>{});
+      }
+      stage(kt, ic<0>{}, ic<0>{});
+      stage(kt + 1, ic<1>{}, ic<1>{});
+    }
+    // the last group (its scales were read in the last sub-step)
+  #pragma unroll
+    for (int a = 0; a < TN; ++a) flush_row(a);
+  };
+  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN].  Each
+  // flush path ends in its own copy, so the two k-loops never join with
+  // live accumulators (joined, the register allocator kept values of both
+  // alive and the int8 tiles spilled).
+  auto epilogue = [&]() __attribute__((always_inline)) {
+    wait_vmcnt<0>();  // reloads past the end land before LDS is reused
+    float* ssa = reinterpret_cast<float*>(smem + OUT);
+    uint16_t* sbias = reinterpret_cast<uint16_t*>(ssa + BM);
+    __syncthreads();  // every wave is done with the ring
+    if (tid < BM) ssa[tid] = sa_t;
+    if (tid < BN) sbias[tid] = b_t;
+    __syncthreads();
+  #pragma unroll
+    for (int a = 0; a < TN; ++a) {
+  #pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
+        const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+        const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
+                             h2f((uint16_t)((uint32_t)bb[0] >> 16)),
+                             h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
+                             h2f((uint16_t)((uint32_t)bb[1] >> 16))};
+  #pragma unroll
+        for (int b = 0; b < TM; ++b) {
+          const int ml = wm * WM + b * 32 + frow;
+          const float sam = ssa[ml];
+          float o[4];
+  #pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float v = facc[a][b][4 * q + r] * sam;
+            if (p.bias) v = v + bv[r];
+            o[r] = v;
+          }
+          *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
+              i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+        }
+      }
+    }
+    __syncthreads();
+    constexpr int LPR = BN / 8, RPS = 64 / LPR;
+    const int cl = (lane % LPR) * 8;
+    const int n = n0 + cl;
+  #pragma unroll 4
+    for (int rr = wave * RPS + lane / LPR; rr < BM; rr += NW * RPS) {
+      const int m = m0 + rr;
+      if (m < M && n < N)
+        *reinterpret_cast<i32x4*>(reinterpret_cast<uint16_t*>(p.y) + (int64_t)m * N + n) =
+            *reinterpret_cast<const i32x4*>(smem + rr * OUT_LD + cl * 2);
+    }
+  };
+  if constexpr (FL == 1) {
+    if (fma_tile) {
+      body(ic<1>{});
+      epilogue();
+    } else {
+      // Tiles with extreme scales: the exact chain from global memory (a
+      // second copy of the pipelined k-loop here made the register allocator
+      // keep values of both copies alive: spills at int8 gs 64, one wave per
+      // SIMD at int4).
+      wait_vmcnt<0>();  // the prologue's DMA lands before the workgroup ends
+      pg_exact_tile<BM, BN, GS, SWH, WF>(p, m0, n0, 64 * NW);
+    }
+  } else {
+    body(ic<0>{});
+    epilogue();
   }
 }
 
@@ -1009,11 +1216,95 @@ namespace {
 template <int GS, bool SWH, int WF>
 hipError_t run_pg64(const GemmArgs& a, hipStream_t s) {
   const int tiles = ((a.M + 63) / 64) * ((a.N + 63) / 64);
-  gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
+  gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
   return hipGetLastError();
 }
 
 }  // namespace
+
+// y[m, n..n+3] = h(f32((sum over s of part[s][m][n], in slice order) * sa[m])
+// [+ bias[n]]); N % 4 == 0, so a thread's four columns share a row.
+__global__ __launch_bounds__(256) void pg_splitk_sum_kernel(const GemmArgs p,
+                                                            const float* __restrict__ part,
+                                                            int S) {
+  const int64_t MN = (int64_t)p.M * p.N;
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= MN) return;
+  const int m = (int)(e / p.N), n = (int)(e % p.N);
+  f32x4 acc = *reinterpret_cast<const f32x4*>(part + e);
+  for (int sl = 1; sl < S; ++sl) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(part + sl * MN + e);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = acc[r] + v[r];
+  }
+  const float sam = p.sa[m];
+  float o[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = acc[r] * sam;
+    if (p.bias) v = v + h2f(p.bias[n + r]);
+    o[r] = v;
+  }
+  *reinterpret_cast<i32x2*>(reinterpret_cast<uint16_t*>(p.y) + e) =
+      i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+}
+
+// K slices of the per-group linear (1 = no split): at M > 64 (smaller M runs
+// the skinny kernels), where the 64 x 64 tiles (the mid-M grid below) would
+// fill at most half the CUs, the most slices,
+// in powers of two up to 8, that keep the grid within two workgroups per CU
+// and each slice at 8 k-stages or more, of whole groups.  The slices' fp32
+// chains are added in slice order, so the result follows the per-group
+// tolerance bar, not the sequential chain's bits.  The caller checks the DMA
+// conditions (K % 128 == 0, N % 8 == 0, aligned operands, K * 256 < 2^32).
+int pg_splitk_ways(int M, int N, int K, int gs) {
+  if (M <= 64 || N % 8 != 0 || K % 128 != 0) return 1;
+  if ((int64_t)K * 256 >= ((int64_t)1 << 32)) return 1;
+  const int cus = num_cus();
+  const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  if (2 * tiles > cus) return 1;
+  const int unit = gs > 128 ? gs : 128;
+  int S = 1;
+  while (S < 8 && tiles * 2 * S <= 2 * cus && K % (unit * 2 * S) == 0 && K / (2 * S) >= 1024)
+    S *= 2;
+  return S;
+}
+
+size_t pg_splitk_bytes(int M, int N, int K, int gs) {
+  const int S = pg_splitk_ways(M, N, K, gs);
+  return S > 1 ? (size_t)S * M * N * 4 : 0;
+}
+
+namespace {
+
+template <int GS, bool SWH, int WF>
+hipError_t run_pg64_splitk(const GemmArgs& a, int S, float* part, hipStream_t s) {
+  const dim3 grid(((a.M + 63) / 64) * ((a.N + 63) / 64), S);
+  gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<grid, 256, 0, s>>>(a, a.K / S, part);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm_pg_splitk(const GemmArgs& a, int gs, bool sw_half, int wf, int S,
+                                 float* part, hipStream_t s) {
+  hipError_t e;
+  if (wf == W_I4)
+    e = gs == 64 ? run_pg64_splitk<64, true, W_I4>(a, S, part, s)
+                 : run_pg64_splitk<128, true, W_I4>(a, S, part, s);
+  else if (sw_half)
+    e = gs == 64 ? run_pg64_splitk<64, true, W_I8>(a, S, part, s)
+        : gs == 128 ? run_pg64_splitk<128, true, W_I8>(a, S, part, s)
+                    : run_pg64_splitk<256, true, W_I8>(a, S, part, s);
+  else
+    e = gs == 64 ? run_pg64_splitk<64, false, W_I8>(a, S, part, s)
+        : gs == 128 ? run_pg64_splitk<128, false, W_I8>(a, S, part, s)
+                    : run_pg64_splitk<256, false, W_I8>(a, S, part, s);
+  if (e != hipSuccess) return e;
+  const int64_t quads = ((int64_t)a.M * a.N) / 4;
+  pg_splitk_sum_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>(a, part, S);
+  return hipGetLastError();
+}
 
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s) {
   {
@@ -1057,15 +1348,15 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
       const unsigned grid = (unsigned)tiles;
       if (wf == W_I4) {
         if (gs == 64)
-          gemm_dma_pg1_kernel<128, 128, 64, true, W_I4, 2, 2, 2><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg1_kernel<128, 128, 64, true, W_I4, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
         else
-          gemm_dma_pg1_kernel<128, 128, 128, true, W_I4, 2, 2, 2><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg1_kernel<128, 128, 128, true, W_I4, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
       } else if (gs == 64) {
-        gemm_dma_pg1_kernel<128, 128, 64, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 64, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
       } else if (gs == 128) {
-        gemm_dma_pg1_kernel<128, 128, 128, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 128, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
       } else {
-        gemm_dma_pg1_kernel<128, 128, 256, false, W_I8, 2, 2, 2><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg1_kernel<128, 128, 256, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
       }
       return hipGetLastError();
     }
@@ -1078,9 +1369,9 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
     constexpr int BM = 128, BN = 128;
     const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 256, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 256, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a, 0, nullptr);
     else
-      gemm_dma_pg_kernel<BM, BN, 256, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 256, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a, 0, nullptr);
     return hipGetLastError();
   }
   if (gs == 64 && a.M > 64) {
@@ -1091,11 +1382,11 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
     constexpr int BM = 128, BN = 128;
     const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
     if (wf == W_I4)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 4><<<tiles, 512, 0, s>>>(a, 0, nullptr);
     else if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a, 0, nullptr);
     else
-      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 4><<<tiles, 512, 0, s>>>(a, 0, nullptr);
     return hipGetLastError();
   }
   // 128 x 64 tiles, 4 waves of 64 x 32: gs 128 runs two workgroups per CU
@@ -1105,19 +1396,19 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
   if (wf == W_I4) {
     // int4 weights come with fp16 group scales ([K/gs, N])
     if (gs == 64)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I4, 1, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I4, 2, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
   } else if (gs == 64) {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, true, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
     else
-      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 64, false, W_I8, 1, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
   } else {
     if (sw_half)
-      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, true, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
     else
-      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a);
+      gemm_dma_pg_kernel<BM, BN, 128, false, W_I8, 2, 2, 2><<<tiles, 256, 0, s>>>(a, 0, nullptr);
   }
   return hipGetLastError();
 }

@@ -49,6 +49,13 @@ int splitk_ways(int M, int N, int K);
 size_t splitk_bytes(int M, int N, int K);
 hipError_t launch_gemm_splitk(const GemmArgs& a, int S, int32_t* part, hipStream_t s);
 hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, hipStream_t s);
+// Split-K per-group GEMM for mid-M shapes with few tiles (gemm_dma_pg.hip):
+// K slices (1 = no split), the fp32 partial bytes they need, and the launch
+// (slices into `part`, then their sum with the epilogue into a.y).
+int pg_splitk_ways(int M, int N, int K, int gs);
+size_t pg_splitk_bytes(int M, int N, int K, int gs);
+hipError_t launch_gemm_pg_splitk(const GemmArgs& a, int gs, bool sw_half, int wf, int S,
+                                 float* part, hipStream_t s);
 
 // Decode-sized GEMV on quantized activations (1 <= M <= 4), gemv_q.hip.
 bool gemv_q_supported(const GemmArgs& a, int wf, bool fused);

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import cider_oracle as O
-from tests.util import assert_bits_equal, assert_mv_close
+from tests.util import assert_bits_equal, assert_mv_close, assert_pergroup_linear_close
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -92,6 +92,10 @@ def test_config1_w8a8(M, N, K, mode):
             assert_mv_close(y, x, w, sw, None, gs, f"pg{gs} mv {N}x{K}")
             return
         exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, np.zeros(N, np.float16), gs)
+        assert y.shape == (M, N)
+        assert_pergroup_linear_close(y[rows], x[rows], w, sw, None, gs, exp,
+                                     f"config1 {mode} {M}x{N}x{K}")
+        return
     assert y.shape == (M, N)
     assert_bits_equal(y[rows], exp, f"config1 {mode} {M}x{N}x{K}")
 
@@ -107,8 +111,9 @@ def test_config2_w4a8_pergroup(M, N, K, gs):
     y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
     rows = rows_of(M, M + N + gs)
     assert y.shape == (M, N)
-    assert_bits_equal(y[rows], O.w4a8_pergroup_linear(x[rows], packed, sc, gs),
-                      f"config2 w4g{gs} {M}x{N}x{K}")
+    assert_pergroup_linear_close(y[rows], x[rows], w4_values(N, K), sc, None, gs,
+                                 O.w4a8_pergroup_linear(x[rows], packed, sc, gs),
+                                 f"config2 w4g{gs} {M}x{N}x{K}")
 
 
 def _w4a8_linear_ref_capi(x, packed, sw):

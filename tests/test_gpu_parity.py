@@ -18,7 +18,7 @@ import pytest
 
 from oracle import cider_oracle as O
 from tests.golden.make_golden import bitexact_inputs
-from tests.util import assert_bits_equal, assert_mv_close
+from tests.util import assert_pergroup_linear_close, assert_bits_equal, assert_mv_close
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -207,8 +207,8 @@ def test_w4_and_pergroup_midpoint_shapes(M, N, K):
     for gs in (64, 128):
         sc = (rng.random((K // gs, N)) * 0.01).astype(np.float32)
         y = H(C.pergroup_linear(T(x), T(w8), T(sc), gs))
-        assert_bits_equal(y, O.pergroup_linear(x, w8, sc, gs, None),
-                          f"pergroup gs{gs} midpoints {M}x{N}x{K}")
+        assert_pergroup_linear_close(y, x, w8, sc, None, gs, O.pergroup_linear(x, w8, sc, gs, None),
+                                     f"pergroup gs{gs} midpoints {M}x{N}x{K}")
 
 
 # K % 256 == 0 with 1024 <= K <= 16384 (in the streaming MV's table) runs the
@@ -302,8 +302,11 @@ def test_pergroup_linear(gs, M, N, K):
     if M == 1:
         assert_mv_close(y, x, w, sw, b, gs, f"pg mv gs{gs} {N}x{K}")
         return
-    # every M >= 2 keeps the reference's sequential group chain: bit-exact
-    assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"pg gs{gs} {M}x{N}x{K}")
+    # M >= 2: the per-group bar (the GEMM kernels flush with fma; the small-M
+    # kernels keep the sequential chain and are also checked bit for bit by
+    # the small-M tests)
+    assert_pergroup_linear_close(y, x, w, sw, b, gs, O.pergroup_linear(x, w, sw, gs, b),
+                                 f"pg gs{gs} {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128, 256])
@@ -329,7 +332,7 @@ def test_pergroup_full_size_rows(gs, M, N, K):
     y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
     rows = np.r_[0:16, M - 16:M]
     exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
-    assert_bits_equal(y[rows], exp, f"pg gs{gs} {M}x{N}x{K} rows")
+    assert_pergroup_linear_close(y[rows], x[rows], w, sw, b, gs, exp, f"pg gs{gs} {M}x{N}x{K} rows")
 
 
 # --------------------------------------------------------------------------
@@ -389,7 +392,14 @@ def test_w4a8_pergroup(gs, M, N, K):
     packed = O.pack_w4_lo_first(w4)
     sc = O.synth_scales((K // gs, N), 72 + K).astype(np.float16)
     y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
-    assert_bits_equal(y, O.w4a8_pergroup_linear(x, packed, sc, gs), f"w4g gs{gs} {M}x{N}x{K}")
+    exp = O.w4a8_pergroup_linear(x, packed, sc, gs)
+    if (M, N, K) == (512, 640, 2048):
+        # split K in two (fp32 chains of the slices, added): the per-group bar
+        assert_pergroup_linear_close(y, x, w4, sc, None, gs, exp, f"w4g gs{gs} {M}x{N}x{K}")
+    else:
+        # the small-M kernels and the two-set DMA kernel (exact fast flush of
+        # fp16 scales) keep the sequential chain
+        assert_bits_equal(y, exp, f"w4g gs{gs} {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gs", [64, 128])
@@ -402,7 +412,7 @@ def test_w4a8_pergroup_full_size_rows(gs):
     y = H(C.w4a8_pergroup_linear(T(x), T(packed), T(sc), gs))
     rows = np.r_[0:16, M - 16:M]
     exp = O.w4a8_pergroup_linear(x[rows], packed, sc, gs)
-    assert_bits_equal(y[rows], exp, f"w4g gs{gs} full-size rows")
+    assert_pergroup_linear_close(y[rows], x[rows], w4, sc, None, gs, exp, f"w4g gs{gs} full-size rows")
 
 
 # fp16 group scales take the fast flush (each group's int32 sum starts from
@@ -465,7 +475,8 @@ def test_pergroup_special_scales(gs, M, N, K):
     with np.errstate(invalid="ignore", over="ignore"):
         exp = O.pergroup_linear(x, w, sw, gs, b)
     assert np.isinf(exp).any() and np.isnan(exp).any()
-    assert_bits_equal(y, exp, f"pg special scales gs{gs} {M}x{N}x{K}")
+    # tiles with these scales take the exact chain, the others the fma flush
+    assert_pergroup_linear_close(y, x, w, sw, b, gs, exp, f"pg special scales gs{gs} {M}x{N}x{K}")
 
 
 # Grids of at least 512 tiles of 128 x 128 run the one-set per-group kernel
@@ -489,7 +500,8 @@ def test_pergroup_one_set_tiles(gs):
     with np.errstate(invalid="ignore", over="ignore"):
         exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
     assert np.isinf(exp).any() and np.isnan(exp).any()
-    assert_bits_equal(y[rows], exp, f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
+    assert_pergroup_linear_close(y[rows], x[rows], w, sw, b, gs, exp,
+                                 f"pg one-set tiles gs{gs} {M}x{N}x{K} rows")
 
 
 # Few rows on a very wide N also reach the one-set kernel (M <= 64 with N >= 8192
@@ -501,7 +513,8 @@ def test_pergroup_one_set_few_rows(gs):
     x, w, _, b = synth_pc(M, N, K, 98 + gs)
     sw = O.synth_scales((K // gs, N), 99 + gs)
     y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
-    assert_bits_equal(y, O.pergroup_linear(x, w, sw, gs, b), f"pg one-set few rows gs{gs}")
+    assert_pergroup_linear_close(y, x, w, sw, b, gs, O.pergroup_linear(x, w, sw, gs, b),
+                                 f"pg one-set few rows gs{gs}")
 
 
 # The one-set kernel at its shortest k-loops: one and two stages of 128 (the
@@ -515,7 +528,8 @@ def test_pergroup_one_set_short_k(gs, K):
     y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
     rows = np.r_[0:4, 1020:1030, M - 6:M]
     exp = O.pergroup_gemm(*O.quantize_per_token(x[rows]), w, sw, b, gs)
-    assert_bits_equal(y[rows], exp, f"pg one-set short K gs{gs} {M}x{N}x{K} rows")
+    assert_pergroup_linear_close(y[rows], x[rows], w, sw, b, gs, exp,
+                                 f"pg one-set short K gs{gs} {M}x{N}x{K} rows")
 
 
 # The same kernel with int4 weights and fp16 group scales.
@@ -537,7 +551,8 @@ def test_w4a8_pergroup_one_set_tiles(gs):
     with np.errstate(invalid="ignore", over="ignore"):
         exp = O.w4a8_pergroup_linear(x[rows], packed, sc, gs, b)
     assert np.isinf(exp).any() and np.isnan(exp).any()
-    assert_bits_equal(y[rows], exp, f"w4g one-set tiles gs{gs} {M}x{N}x{K} rows")
+    assert_pergroup_linear_close(y[rows], x[rows], w4, sc, b, gs, exp,
+                                 f"w4g one-set tiles gs{gs} {M}x{N}x{K} rows")
 
 
 # Decode-sized GEMV on quantized activations (M <= 4, K <= 16384, K % 16 == 0
@@ -690,25 +705,60 @@ def test_small_m_special_rows(M, N, K):
 
 
 # Per-group at mid M on small N: 64 x 64 tiles of four 32 x 32 waves, where the
-# 128-row tiles would fill at most half the CUs.  (65, 2560, 10240) leaves a
-# one-row tile, (200, 1032, 2048) a ragged row tile and N past the last
-# 64-column tile; every group size and both weight formats, bit-exact
-# against the oracle's sequential group chain.
+# 128-row tiles would fill at most half the CUs, and their split-K form
+# (K slices of fp32 chains, summed) where even those fill at most half the
+# CUs: (65, 2560, 10240) leaves a one-row tile (split in 4), (128, 2560,
+# 10240) splits in 4, (200, 1032, 2048) a ragged row tile and N past the
+# last 64-column tile; every group size and both weight formats, against
+# the per-group bar.
 @pytest.mark.parametrize("M,N,K", [(65, 2560, 10240), (128, 2560, 10240), (200, 1032, 2048),
                                    (512, 4096, 4096)])
-def test_pergroup_small_tiles_exact(M, N, K):
+def test_pergroup_small_tiles(M, N, K):
     x, w, _, b = synth_pc(M, N, K, 160 + M)
     for gs in (64, 128, 256):
         swg = O.synth_scales((K // gs, N), 161 + gs)
         y = H(C.pergroup_linear(T(x), T(w), T(swg), gs, T(b)))
-        assert_bits_equal(y, O.pergroup_linear(x, w, swg, gs, b), f"pg64 tiles gs{gs} {M}x{N}x{K}")
+        assert_pergroup_linear_close(y, x, w, swg, b, gs, O.pergroup_linear(x, w, swg, gs, b),
+                                     f"pg64 tiles gs{gs} {M}x{N}x{K}")
     w4 = np.random.default_rng(162).integers(-8, 8, (N, K), dtype=np.int8)
     pk = O.pack_w4_lo_first(w4)
     for gs in (64, 128):
         sc = O.synth_scales((K // gs, N), 163 + gs).astype(np.float16)
         y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b)))
-        assert_bits_equal(y, O.w4a8_pergroup_linear(x, pk, sc, gs, b),
-                          f"pg64 tiles w4g{gs} {M}x{N}x{K}")
+        assert_pergroup_linear_close(y, x, w4, sc, b, gs, O.w4a8_pergroup_linear(x, pk, sc, gs, b),
+                                     f"pg64 tiles w4g{gs} {M}x{N}x{K}")
+
+
+# Split-K per-group with special scales: the slices whose tiles hold
+# them take the exact chain from global memory (fp32 scales) or redo the
+# fast flush exactly (fp16 scales), the others flush with fma; the slices'
+# partial sums then carry the infinities and NaNs into the sum.
+@pytest.mark.parametrize("gs", [64, 128])
+def test_pergroup_splitk_special_scales(gs):
+    M, N, K = 128, 2560, 4096                      # 80 tiles of 64 x 64, 4 K slices
+    x, w, _, b = synth_pc(M, N, K, 164 + gs)
+    x[5, :] = 0
+    w[:, :gs] = -127
+    sw = O.synth_scales((K // gs, N), 165 + gs)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        sw[(g * 7) % (K // gs), n] = v              # spread over the slices
+    sw[20 % (K // gs), 6] = np.float32(3.0e38)
+    y = H(C.pergroup_linear(T(x), T(w), T(sw), gs, T(b)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.pergroup_linear(x, w, sw, gs, b)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_pergroup_linear_close(y, x, w, sw, b, gs, exp, f"pg split-K special gs{gs}")
+    w4 = np.random.default_rng(166).integers(-8, 8, (N, K), dtype=np.int8)
+    w4[:, :gs] = -8
+    pk = O.pack_w4_lo_first(w4)
+    sc = O.synth_scales((K // gs, N), 167 + gs).astype(np.float16)
+    for (g, n), v in _SPECIAL_SCALES.items():
+        sc[(g * 7) % (K // gs), n] = v
+    y = H(C.w4a8_pergroup_linear(T(x), T(pk), T(sc), gs, T(b)))
+    with np.errstate(invalid="ignore", over="ignore"):
+        exp = O.w4a8_pergroup_linear(x, pk, sc, gs, b)
+    assert np.isinf(exp).any() and np.isnan(exp).any()
+    assert_pergroup_linear_close(y, x, w4, sc, b, gs, exp, f"w4g split-K special gs{gs}")
 
 
 # Split-K per-channel GEMM (M from 17 to 512 where the tiles fill at most a

@@ -637,3 +637,66 @@ def test_sum_bar_compares_non_finite_outputs_per_element():
                       ("finite off", [1.0, np.inf, np.nan, -np.inf, 2.5])):
         with pytest.raises(AssertionError):
             assert_sum_close(np.array(bad, np.float16), ref, exact, mag, 8, name)
+
+
+def _fma_pergroup_chain(q, sa, w, sw, bias, gs, slices=1):
+    """The per-group GEMM as the fma-flush kernels evaluate it: per K slice a
+    chain acc = fma(f32(D_g), s, acc) (the fma's single rounding from the
+    exact float64 value, exact here since |D s| < 2^75 with 46-bit products
+    and the addend at most 2^64), the slices added in order, then the
+    reference's epilogue operations."""
+    M, K = q.shape
+    N = w.shape[0]
+    G = K // gs
+    s = sw.astype(np.float64).reshape(G, N)
+    per = G // slices
+    total = None
+    for sl in range(slices):
+        acc = np.zeros((M, N), F32)
+        for g in range(sl * per, (sl + 1) * per):
+            D = q[:, g * gs:(g + 1) * gs].astype(np.int64) @ w[:, g * gs:(g + 1) * gs].astype(np.int64).T
+            acc = (acc.astype(np.float64) + D.astype(np.float64) * s[g][None, :]).astype(F32)
+        total = acc if total is None else (total + acc).astype(F32)
+    v = (total * sa.astype(F32)[:, None]).astype(F32)
+    if bias is not None:
+        v = (v + bias.astype(F32)[None, :]).astype(F32)
+    return v.astype(np.float16)
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+def test_pergroup_bar_accepts_fma_chains_and_rejects_planted_mistakes(gs):
+    """The per-group tolerance bar (tests/util.py assert_pergroup_close)
+    passes the oracle's sequential chain, an fma chain and a 4-slice split
+    of it, and fails a dropped group, a group counted twice, the scales of
+    the next group, a column-shifted scale row and a scale off by 1 %."""
+    from tests.util import assert_pergroup_close
+    M, N, K = 24, 96, 1024
+    x = O.synth_activations(M, K, 171)
+    w = O.synth_weights_i8(N, K, 172)
+    sw = O.synth_scales((K // gs, N), 173)
+    b = (np.random.default_rng(174).standard_normal(N) * 0.1).astype(np.float16)
+    q, sa = O.quantize_per_token(x)
+    ref = O.pergroup_gemm(q, sa, w, sw, b, gs)
+
+    def bar(y, what):
+        assert_pergroup_close(y, q, sa, w, sw, b, gs, ref, what)
+
+    bar(ref, "oracle")
+    fma1 = _fma_pergroup_chain(q, sa, w, sw, b, gs)
+    fma4 = _fma_pergroup_chain(q, sa, w, sw, b, gs, slices=4)
+    bar(fma1, "fma chain")
+    bar(fma4, "4 slices")
+    G = K // gs
+    dropped = sw.copy()
+    dropped[3] = 0
+    doubled = sw.copy()
+    doubled[3] *= F32(2)
+    nextg = np.roll(sw, -1, axis=0)
+    shifted = np.roll(sw, 1, axis=1)
+    off = (sw * F32(1.01)).astype(F32)
+    for name, s_bad in (("dropped group", dropped), ("group twice", doubled),
+                        ("next group's scales", nextg), ("column-shifted scales", shifted),
+                        ("scale off by 1%", off)):
+        with pytest.raises(AssertionError):
+            bar(O.pergroup_gemm(q, sa, w, s_bad, b, gs), name)
+    assert G >= 8

@@ -141,3 +141,55 @@ def assert_sum_close(got, ref, exact, mag, depth, what="", bar="bar"):
         raise AssertionError(
             f"{what}: {np.count_nonzero(~ok)} of {ok.size} outputs outside the {bar}; "
             f"e.g. at {idx}: got {g[idx]} oracle {r[idx]} exact {exact[idx]} bound {bound[idx]}")
+
+
+def pergroup_exact(q, sa, w, sw_gn, bias, gs):
+    """float64 value and magnitude of the per-group GEMM from its definition:
+    y[m, n] = sa[m] * sum_g D_g[m, n] * s[g, n] + bias[n], D_g the exact
+    int dot product of group g; returns (exact [M, N], sum of |terms| with
+    the same factors, plus |bias|)."""
+    qf = np.asarray(q).astype(np.float64)
+    wf = np.asarray(w).astype(np.float64)
+    M, K = qf.shape
+    N = wf.shape[0]
+    G = K // gs
+    s = np.asarray(sw_gn, np.float32).astype(np.float64).reshape(G, N)
+    exact = np.zeros((M, N))
+    mag = np.zeros((M, N))
+    with np.errstate(invalid="ignore", over="ignore"):
+        for g in range(G):
+            D = qf[:, g * gs:(g + 1) * gs] @ wf[:, g * gs:(g + 1) * gs].T   # exact below 2^53
+            t = D * s[g][None, :]
+            exact += t
+            mag += np.abs(t)
+        sa64 = np.asarray(sa, np.float32).astype(np.float64).reshape(M, 1)
+        b = (np.zeros(N) if bias is None else
+             np.asarray(bias, np.float16).astype(np.float64)).reshape(1, N)
+        return exact * sa64 + b, mag * np.abs(sa64) + np.abs(b)
+
+
+def assert_pergroup_close(got, q, sa, w, sw_gn, bias, gs, ref, what=""):
+    """Bar for the per-group GEMM's fp16 outputs (M >= 2): the int32 group sums
+    D_g are exact, the fp32 chain over the groups may be evaluated in any
+    order and with fused multiply-adds (the kernels flush with
+    fma(f32(D_g), s, acc), and split-K adds the chains of K slices), so
+    every output is within 1e-3 relative / 1 fp16 ulp of the oracle's
+    sequential chain ``ref``, or within gamma_d * sum|terms| + 1 fp16 ulp of
+    the float64 value with d = 2 G + 8 (G groups: a product and an add each,
+    then the slice sums, the per-token scale and the bias).  Non-finite
+    outputs must match the oracle element by element.  ``q``, ``sa``: the
+    quantized activations; ``w``: int8 weights [N, K] (int4 values widened).
+    A dropped or duplicated group, a scale of the wrong group or column, or a
+    scale off by 1 % fails it (tests/test_oracle.py)."""
+    G = np.asarray(q).shape[1] // gs
+    exact, mag = pergroup_exact(q, sa, w, sw_gn, bias, gs)
+    assert_sum_close(got, ref, exact, mag, 2 * G + 8, what, "per-group bar")
+
+
+def assert_pergroup_linear_close(got, x, w, sw_gn, bias, gs, ref, what=""):
+    """assert_pergroup_close for fp16 activation rows x (quantized here with
+    the oracle's per-token quantization, which the kernels match bit for
+    bit)."""
+    from oracle import cider_oracle as O
+    q, sa = O.quantize_per_token(np.asarray(x, np.float16))
+    assert_pergroup_close(got, q, sa, w, sw_gn, bias, gs, ref, what)
