@@ -555,7 +555,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
       // (its first scale DMA comes stages later)
       static_assert(ROWB + 4 * NW <= PG_SSLOT, "vote words");
       uint32_t* vote = reinterpret_cast<uint32_t*>(smem + kZeroRow + ROWB);
-      if (lane == 0) vote[wave] = __builtin_amdgcn_ballot_w64(!tame) != 0 ? 1u : 0u;
+      const bool wbad = __builtin_amdgcn_ballot_w64(!tame) != 0;  // every lane votes
+      if (lane == 0) vote[wave] = wbad ? 1u : 0u;
       __syncthreads();
       uint32_t any = 0;
 #pragma unroll
