@@ -13,7 +13,13 @@ starts.
 
 Also reported, in the same run:
   * decode: the M == 1 MV (N=10240, K=2560), cycling over enough weight copies
-    (>= 2x the 256 MB Infinity Cache) that every launch streams from HBM;
+    (>= 2x the 256 MB Infinity Cache) that every launch streams from HBM, in a
+    HIP graph and as eager back-to-back launches, beside the read probe of
+    cider_amd/csrc/probe.hip (one launch reading the same bytes in the MV's
+    layout: the read ceiling of the M == 1 roofline);
+  * mfma_ceiling: the sustained int8 MFMA rate and shader clock of a probe
+    kernel with register-resident operands (random and zero bytes), the
+    ceiling of the GEMM roofline on this part;
   * sweep: the other configs[1] / configs[2] cases (per-group, W4A8, M = 1,
     16, 128, 1024, 8192 and the N=2560 K=10240 shape), each a HIP graph of
     back-to-back calls; up to M = 512 the weights rotate past the MALL;
@@ -62,6 +68,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the M=1 decode leg")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the compact sweep (per-group, W4A8, M=1 / 16 / 8192 cases)")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the sustained-MFMA probe (cider_amd/csrc/probe.hip)")
     ap.add_argument("--no-qwen3", action="store_true",
                     help="skip the compact configs[3] leg (Qwen3-8B prefill / decode)")
     ap.add_argument("--qwen3", action="store_true",
@@ -222,6 +230,9 @@ def main():
     if not args.no_sweep:
         result["sweep"] = compact_sweep(torch, lib, _lib, args, dev, stream)
 
+    if not args.no_ceiling:
+        result["mfma_ceiling"] = mfma_ceiling(torch, args, dev, stream)
+
     if not args.no_qwen3:
         result["qwen3"] = qwen3_summary(torch, args, dev)
 
@@ -285,6 +296,29 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
                                                None, 0, 1, N, K, cur()))
 
     us = graph_us(gcall, iters)
+    # The same calls launched one by one on the stream (no graph): the
+    # per-call time that a kernel trace of back-to-back launches pairs with.
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(iters):
+        call(i)
+    e0.record(stream)
+    for i in range(iters):
+        call(i)
+    e1.record(stream)
+    e1.synchronize()
+    us_eager = e0.elapsed_time(e1) / iters * 1e3
+    # The read probe (cider_amd/csrc/probe.hip) over the same weight copies in
+    # the same graph form: one launch reading N*K bytes in the MV's layout,
+    # with no x staging, arithmetic or output beyond 4 bytes per wave.
+    plib = load_probe()
+    rsink = torch.empty(N * K // 5120, dtype=torch.int32, device=dev)
+
+    def rcall(i):
+        rc = plib.cider_probe_read(vp(ws[i % copies]), N * K, vp(rsink), cur())
+        if rc != 0:
+            raise RuntimeError(f"cider_probe_read failed ({rc})")
+
+    read_us = graph_us(rcall, iters) if (N * K) % 20480 == 0 else None
     # The same call with 8 weight rows: the per-launch cost of the MV in the
     # graph (dispatch, x staging, drain) with almost no weight traffic.
     w8 = ws[0][:8].contiguous()
@@ -303,8 +337,91 @@ def bench_decode(torch, lib, _lib, N, K, args, dev, stream):
             "achieved_gbs": round(gbs, 1), "peak_gbs": HBM_PEAK_GBS,
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm",
             "kernel": "mv_stream_kernel<2, 5, per-channel> (cider_amd/csrc/mv_stream.hip)",
+            "us_per_call_eager": round(us_eager, 3),
             "launch_floor_us": round(floor_us, 3),
-            "streaming_gbs_above_floor": None if above is None else round(above, 1)}
+            "streaming_gbs_above_floor": None if above is None else round(above, 1),
+            "read_ceiling": None if read_us is None else {
+                "probe": "probe_read_kernel (cider_amd/csrc/probe.hip): one launch reading "
+                         "the N*K weight bytes in the MV's layout, same copies and graph",
+                "us_per_call": round(read_us, 3),
+                "gbs": round(N * K / (read_us * 1e-6) / 1e9, 1),
+                "frac_of_hbm_peak": round(N * K / (read_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "mv_frac_of_read": round(read_us / us, 4)}}
+
+
+_probe = None
+
+
+def load_probe():
+    """ctypes binding of cider_amd/lib/libcider_probe.so (the measurement
+    probes of cider_amd/csrc/probe.hip, not part of the linear's C ABI)."""
+    global _probe
+    if _probe is None:
+        path = os.path.join(ROOT, "cider_amd", "lib", "libcider_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: build with make -C cider_amd/csrc")
+        lib = ctypes.CDLL(path)
+        P, I, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+        lib.cider_probe_mfma.argtypes = [P, I, P, P, I, P]
+        lib.cider_probe_mfma.restype = I
+        lib.cider_probe_mfma_src_bytes.argtypes = []
+        lib.cider_probe_mfma_src_bytes.restype = LL
+        lib.cider_probe_read.argtypes = [P, LL, P, P]
+        lib.cider_probe_read.restype = I
+        _probe = lib
+    return _probe
+
+
+def mfma_ceiling(torch, args, dev, stream):
+    """The int8 MFMA rate the chip sustains with no memory traffic (probe
+    kernel probe_mfma_kernel, cider_amd/csrc/probe.hip): one 8-wave workgroup
+    per CU, 24 v_mfma_i32_32x32x32_i8 per wave and round from register-
+    resident operands, about 0.3 ms per launch; settled for 300 ms, then the
+    median of 10 timed launches.  Random operand bytes (as the GEMM's) and
+    all-zero operands; the shader clock is s_memtime over s_memrealtime
+    (100 MHz) of every wave, median."""
+    plib = load_probe()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nsrc = cus * int(plib.cider_probe_mfma_src_bytes())
+    g = torch.Generator(device="cpu").manual_seed(args.seed + 11)
+    rnd = torch.randint(-128, 128, (nsrc,), generator=g, dtype=torch.int8).to(dev)
+    clocks = torch.zeros(cus * 8 * 4, dtype=torch.int64, device=dev)
+    sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
+    iters = 400
+    ops = 2.0 * 32 * 32 * 32 * 24 * iters * cus * 8
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    out = {"probe": "probe_mfma_kernel (cider_amd/csrc/probe.hip): %d workgroups x 8 waves, "
+                    "%d rounds of 24 v_mfma_i32_32x32x32_i8 per wave" % (cus, iters)}
+    for name, src in (("random_int8", rnd), ("zeros", torch.zeros_like(rnd))):
+        def launch():
+            rc = plib.cider_probe_mfma(vp(src), iters, vp(clocks), vp(sink), cus, sp)
+            if rc != 0:
+                raise RuntimeError(f"cider_probe_mfma failed ({rc})")
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        while True:
+            for _ in range(20):
+                launch()
+            s1.record(stream)
+            s1.synchronize()
+            if s0.elapsed_time(s1) >= 300.0:
+                break
+        ts = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        ms = statistics.median(ts)
+        c = clocks.view(-1, 4).cpu().double()
+        ghz = ((c[:, 1] - c[:, 0]) / (c[:, 3] - c[:, 2]) * 0.1).median().item()
+        tops = ops / (ms * 1e-3) / 1e12
+        out[name] = {"ms_per_launch": round(ms, 4), "tops": round(tops, 1),
+                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                     "shader_clock_ghz": round(ghz, 3)}
+    return out
 
 
 def time_case(torch, stream, settle_ms, name, call_for, ncopies, M, N, K, nbytes_alg, ops,
