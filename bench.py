@@ -362,8 +362,10 @@ def load_probe():
             raise RuntimeError(f"{path} is missing: build with make -C cider_amd/csrc")
         lib = ctypes.CDLL(path)
         P, I, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
-        lib.cider_probe_mfma.argtypes = [P, I, P, P, I, P]
+        lib.cider_probe_mfma.argtypes = [P, I, I, P, P, I, P]
         lib.cider_probe_mfma.restype = I
+        lib.cider_probe_mfma_round_ops.argtypes = [I]
+        lib.cider_probe_mfma_round_ops.restype = LL
         lib.cider_probe_mfma_src_bytes.argtypes = []
         lib.cider_probe_mfma_src_bytes.restype = LL
         lib.cider_probe_read.argtypes = [P, LL, P, P]
@@ -375,52 +377,58 @@ def load_probe():
 def mfma_ceiling(torch, args, dev, stream):
     """The int8 MFMA rate the chip sustains with no memory traffic (probe
     kernel probe_mfma_kernel, cider_amd/csrc/probe.hip): one 8-wave workgroup
-    per CU, 24 v_mfma_i32_32x32x32_i8 per wave and round from register-
-    resident operands, about 0.3 ms per launch; settled for 300 ms, then the
-    median of 10 timed launches.  Random operand bytes (as the GEMM's) and
-    all-zero operands; the shader clock is s_memtime over s_memrealtime
-    (100 MHz) of every wave, median."""
+    per CU, the MFMAs of a 128 x 64 wave tile per round from register-
+    resident operands, about 0.3-0.5 ms per launch; settled for 300 ms, then
+    the median of 10 timed launches.  The GEMM's instruction
+    (v_mfma_i32_32x32x32_i8) and v_mfma_i32_16x16x64_i8, on random operand
+    bytes (the weights' statistics) and on all-zero operands; the shader clock
+    is s_memtime over s_memrealtime (100 MHz) of every wave, median."""
     plib = load_probe()
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     nsrc = cus * int(plib.cider_probe_mfma_src_bytes())
     g = torch.Generator(device="cpu").manual_seed(args.seed + 11)
     rnd = torch.randint(-128, 128, (nsrc,), generator=g, dtype=torch.int8).to(dev)
+    zeros = torch.zeros_like(rnd)
     clocks = torch.zeros(cus * 8 * 4, dtype=torch.int64, device=dev)
     sink = torch.empty(cus * 512, dtype=torch.int32, device=dev)
     iters = 400
-    ops = 2.0 * 32 * 32 * 32 * 24 * iters * cus * 8
     sp = ctypes.c_void_p(stream.cuda_stream)
     out = {"probe": "probe_mfma_kernel (cider_amd/csrc/probe.hip): %d workgroups x 8 waves, "
-                    "%d rounds of 24 v_mfma_i32_32x32x32_i8 per wave" % (cus, iters)}
-    for name, src in (("random_int8", rnd), ("zeros", torch.zeros_like(rnd))):
-        def launch():
-            rc = plib.cider_probe_mfma(vp(src), iters, vp(clocks), vp(sink), cus, sp)
-            if rc != 0:
-                raise RuntimeError(f"cider_probe_mfma failed ({rc})")
-        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s0.record(stream)
-        while True:
-            for _ in range(20):
+                    "%d rounds per wave" % (cus, iters)}
+    for form, fname in ((0, "mfma_i32_32x32x32_i8"), (1, "mfma_i32_16x16x64_i8")):
+        ops = float(plib.cider_probe_mfma_round_ops(form)) * iters * cus * 8
+        rec = {}
+        for name, src in (("random_int8", rnd), ("zeros", zeros)):
+            def launch():
+                rc = plib.cider_probe_mfma(vp(src), form, iters, vp(clocks), vp(sink), cus, sp)
+                if rc != 0:
+                    raise RuntimeError(f"cider_probe_mfma failed ({rc})")
+            s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s0.record(stream)
+            while True:
+                for _ in range(20):
+                    launch()
+                s1.record(stream)
+                s1.synchronize()
+                if s0.elapsed_time(s1) >= 300.0:
+                    break
+            ts = []
+            for _ in range(10):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
                 launch()
-            s1.record(stream)
-            s1.synchronize()
-            if s0.elapsed_time(s1) >= 300.0:
-                break
-        ts = []
-        for _ in range(10):
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            launch()
-            e1.record(stream)
-            e1.synchronize()
-            ts.append(e0.elapsed_time(e1))
-        ms = statistics.median(ts)
-        c = clocks.view(-1, 4).cpu().double()
-        ghz = ((c[:, 1] - c[:, 0]) / (c[:, 3] - c[:, 2]) * 0.1).median().item()
-        tops = ops / (ms * 1e-3) / 1e12
-        out[name] = {"ms_per_launch": round(ms, 4), "tops": round(tops, 1),
-                     "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
-                     "shader_clock_ghz": round(ghz, 3)}
+                e1.record(stream)
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            ms = statistics.median(ts)
+            c = clocks.view(-1, 4).cpu().double()
+            ghz = ((c[:, 1] - c[:, 0]) / (c[:, 3] - c[:, 2]) * 0.1).median().item()
+            tops = ops / (ms * 1e-3) / 1e12
+            rec[name] = {"ms_per_launch": round(ms, 4), "tops": round(tops, 1),
+                         "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                         "shader_clock_ghz": round(ghz, 3),
+                         "frac_of_peak_at_that_clock": round(tops / INT8_PEAK_TOPS * 2.4 / ghz, 4)}
+        out[fname] = rec
     return out
 
 

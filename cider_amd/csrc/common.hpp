@@ -91,6 +91,17 @@ __device__ __forceinline__ i32x2 ld8(const void* p) {
   return *reinterpret_cast<const i32x2*>(p);
 }
 
+// Non-temporal loads (the nt cache policy) for weight streams that every
+// launch reads once: a single-launch read of 26 MB in the MV's layout ran
+// 5.78 against 5.99 us with plain loads, the M == 1 MV 6.44 -> 6.00 us.
+__device__ __forceinline__ i32x4 ld16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+}
+
+__device__ __forceinline__ i32x2 ld8_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const i32x2*>(p));
+}
+
 // Maps a linear workgroup id to a tile index so that the workgroups one XCD
 // runs (the hardware deals workgroups to the 8 XCDs round-robin) receive a
 // contiguous range of tiles; neighbouring tiles share operand panels, which

@@ -47,6 +47,17 @@ __device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t 
       : "memory", "m0");
 }
 
+// As dma16s with the non-temporal cache policy, for weight streams read once
+// per launch.
+__device__ __forceinline__ void dma16s_nt(const void* base, uint32_t off, uint32_t lds_base) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "global_load_lds_dwordx4 %0, %1 nt"
+      :
+      : "v"(off), "s"(base), "s"(lds_base)
+      : "memory", "m0");
+}
+
 // Waits until at most N vector-memory loads of this wave are outstanding
 // (they complete in order).
 template <int N>

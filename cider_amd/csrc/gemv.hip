@@ -90,7 +90,7 @@ __global__ __launch_bounds__(256) void mv_kernel(
       // branch-free: a block index past the end re-reads the last block (its
       // value is never consumed), so every load is issued unconditionally and
       // the compiler can count outstanding loads exactly
-      v = ld16(wr + min(b, nb - 1) * 256 + 16 * j);
+      v = ld16_nt(wr + min(b, nb - 1) * 256 + 16 * j);
       return;
     }
     const int k = b * 256 + 16 * j;
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void mv_wide_kernel(
   const int8_t* wr = w + (int64_t)(live ? n : 0) * K + 8 * rl;
 
   // branch-free: a block past the end re-reads the last one (never consumed)
-  auto load_w = [&](int b) -> i32x2 { return ld8(wr + (int64_t)min(b, nb - 1) * 256); };
+  auto load_w = [&](int b) -> i32x2 { return ld8_nt(wr + (int64_t)min(b, nb - 1) * 256); };
 
   // ---- stage x as fp32 (and the group scales); x reads first, then the
   // first 2U weight blocks, then the conversions and LDS stores

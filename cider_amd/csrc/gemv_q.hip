@@ -70,7 +70,7 @@ __global__ __launch_bounds__(1024) void gemv_q_kernel(const GemmArgs p) {
   // ---- the whole row in flight (chunks past the end re-read the last one)
   i32x4 wv[JM];
 #pragma unroll
-  for (int j = 0; j < JM; ++j) wv[j] = ld16(wr + 16 * min(lane + 64 * j, nc - 1));
+  for (int j = 0; j < JM; ++j) wv[j] = ld16_nt(wr + 16 * min(lane + 64 * j, nc - 1));
 
   // ---- stage the quantized activations
   if constexpr (FQ) {
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4_kernel(const uint16_t* __res
 #pragma unroll
   for (int j = 0; j < C; ++j) {
     const int c = lane + 64 * j, r = c / CPR, kc = c % CPR;
-    wv[j] = ld16(w + (int64_t)min(n0 + r, N - 1) * RB + 16 * kc);
+    wv[j] = ld16_nt(w + (int64_t)min(n0 + r, N - 1) * RB + 16 * kc);
   }
   __builtin_amdgcn_sched_barrier(0);
 

@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     const int c = lane + 64 * j;
     const int r = c / CPR, kc = c - r * CPR;
     const int row = min(n0 + r, N - 1);
-    wv[j] = ld16(w + (int64_t)row * K + 16 * kc);
+    wv[j] = ld16_nt(w + (int64_t)row * K + 16 * kc);  // read once: non-temporal
     if constexpr (PG && !SS) sj[j] = sw[(int64_t)((16 * kc) / gs) * N + row];
   }
   // every load is issued before any arithmetic on x: keeps the scheduler from

@@ -91,7 +91,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_kernel(const GemmArgs p) {
         if (nb <= 0)
           wv[u] = i32x4{0, 0, 0, 0};
         else if (VEC)
-          wv[u] = ld16(W + (int64_t)nw * K + kk);
+          wv[u] = ld16_nt(W + (int64_t)nw * K + kk);
         else
           wv[u] = load_bytes_partial(W + (int64_t)nw * K + kk, nb < 16 ? nb : 16);
       }
@@ -255,7 +255,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_pg_kernel(const GemmArgs p) {
         if (nw >= N)
           wv[u] = i32x4{0, 0, 0, 0};
         else if (VEC)
-          wv[u] = ld16(W + (int64_t)nw * K + kk);
+          wv[u] = ld16_nt(W + (int64_t)nw * K + kk);
         else
           wv[u] = load_bytes_partial(W + (int64_t)nw * K + kk, 16);
       }

@@ -151,7 +151,7 @@ __global__ __launch_bounds__((EPI == EPI_PG ? kSdKW + kSdCW : kSdKW) * 64) void 
     for (int j = 0; j < PW; ++j) {
       const int i = wave + kSdKW * j;
       if (j < JW)
-        dma16s(wsrc, off[j], __builtin_amdgcn_readfirstlane(slot + i * 1024));
+        dma16s_nt(wsrc, off[j], __builtin_amdgcn_readfirstlane(slot + i * 1024));
       else
         dma16s(xsrc, off[j], __builtin_amdgcn_readfirstlane(slot + C::WS + (i - C::NWI) * 1024));
     }

@@ -113,7 +113,7 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
   auto load_k = [&](int k, i32x4 (&wv)[RB], i32x4 (&xv)[NX][TM]) {
     if constexpr (P2) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) wv[rb] = ld16(wrow[rb] + k * 64 + 16 * lq);
+      for (int rb = 0; rb < RB; ++rb) wv[rb] = ld16_nt(wrow[rb] + k * 64 + 16 * lq);
 #pragma unroll
       for (int b = 0; b < TM; ++b) {
         xv[0][b] = ld16(xrow[b] + k * 128 + 32 * lq);
@@ -123,10 +123,10 @@ __global__ __launch_bounds__(KW * 64) void skinny_stream_kernel(const GemmArgs p
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
         if constexpr (WF == W_I4) {
-          const i32x2 v = ld8(wrow[rb] + k * 32 + 8 * lq);
+          const i32x2 v = ld8_nt(wrow[rb] + k * 32 + 8 * lq);
           wv[rb] = i32x4{v[0], v[1], 0, 0};
         } else {
-          wv[rb] = ld16(wrow[rb] + k * 64 + 16 * lq);
+          wv[rb] = ld16_nt(wrow[rb] + k * 64 + 16 * lq);
         }
       }
 #pragma unroll
