@@ -70,6 +70,9 @@ def parse():
                     help="skip the compact sweep (per-group, W4A8, M=1 / 16 / 8192 cases)")
     ap.add_argument("--no-ceiling", action="store_true",
                     help="skip the sustained-MFMA probe (cider_amd/csrc/probe.hip)")
+    ap.add_argument("--only-decode", action="store_true",
+                    help="print only the decode leg (M=1 MV of N x K) as one JSON line, e.g. "
+                         "to pair it with a kernel trace of the same launches")
     ap.add_argument("--no-qwen3", action="store_true",
                     help="skip the compact configs[3] leg (Qwen3-8B prefill / decode)")
     ap.add_argument("--qwen3", action="store_true",
@@ -134,6 +137,11 @@ def main():
         return
     if args.qwen3vl:
         bench_qwen3vl(torch, args, dev)
+        return
+    if args.only_decode:
+        stream = torch.cuda.current_stream(dev)
+        print(json.dumps({"decode": bench_decode(torch, lib, _lib, args.N, args.K, args, dev,
+                                                 stream)}), flush=True)
         return
     M, N, K = args.M, args.N, args.K
     x, w, sw, bias = synth_inputs(torch, M, N, K, args.seed, dev)
