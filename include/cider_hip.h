@@ -51,11 +51,12 @@ const char* cider_last_error(void);
 
 /* Bytes of scratch the linear entry points need for the given problem
  * (quantized activations int8 [M,K] and per-token scales fp32 [M], each
- * 256-byte aligned; for CIDER_OP_PERCHANNEL also the int32 partial sums of
- * the split-K GEMM, S*M*N*4 bytes, on shapes with few output tiles, which
- * a smaller workspace of at least the first two parts runs in one pass over
- * K instead, with the same results). 0 when the call needs none (M <= 1 on
- * the W8 paths).
+ * 256-byte aligned; on shapes with few output tiles also the partial sums of
+ * the split-K GEMM, S*M*N*4 bytes: int32 for CIDER_OP_PERCHANNEL, fp32 for
+ * CIDER_OP_PERGROUP and CIDER_OP_W4A8_PERGROUP (group_size given). A smaller
+ * workspace of at least the first two parts runs one pass over K instead:
+ * per-channel with the same results, per-group within the same tolerance).
+ * 0 when the call needs none (M <= 1 on the W8 paths).
  * Replaces the per-call temporaries of csrc/src/w8a8_primitive.mm:184-188
  * and the global ScratchPool of csrc/src/w4a8_primitive.mm:40-76. */
 size_t cider_workspace_bytes(int op, int64_t M, int64_t N, int64_t K,
@@ -118,6 +119,14 @@ int cider_perchannel_gemm(const int8_t* q, const float* sa, const int8_t* w_nk,
  * {64,128,256}, K % group_size == 0.
  *   M == 1 : fp16 MV with per-group scales
  *   M >= 2 : acc = sum_g f32(f32(D_g) * sw[g,n]); y = h(f32(acc*sa[m]) + bias[n])
+ * D_g is the exact int32 sum of group g.  The M >= 2 GEMM kernels evaluate
+ * the fp32 chain over the groups with fused multiply-adds
+ * (acc = fma(f32(D_g), s, acc)) where every scale of a tile is finite and
+ * below 2^64 (else that tile runs the chain above as written), and split K
+ * into fp32 chains that are then added, on mid-M shapes with few tiles; the
+ * fp16 outputs are within 1e-3 relative / 1 fp16 ulp of the chain above, or
+ * within its fp32 error bound where the sum cancels.  The small-M kernels
+ * (M <= 16, and M <= 64 on N < 8192) keep the chain above bit for bit. */
  * Replaces _cider_prim.pergroup_linear (csrc/src/prim_bindings.cpp:21-27,
  * csrc/src/pergroup_primitive.mm:138-312). The reference's unused
  * `new_bias` argument has no counterpart. */
@@ -166,7 +175,9 @@ int cider_w4a8_linear_ref(const void* x_f16, const uint8_t* packed_kn,
  *   acc = sum_g f32(f32(D_g) * f32(scale[g,n])); y = h(f32(acc*sa[m]) [+ bias])
  * No reference counterpart: the reference has no per-group W4. This is the
  * per-group flush of cider/kernels/pergroup_int8_gemm.metal:152-189 applied
- * to int4 weights. */
+ * to int4 weights, with the tolerance of cider_pergroup_linear on the large
+ * grids (fma flush) and the split-K shapes; the other kernels keep the
+ * chain bit for bit. */
 int cider_w4a8_pergroup_linear(const void* x_f16, const uint8_t* w4_nk,
                                const void* scale_gn_f16, const void* bias_f16,
                                void* y_f16, void* ws, size_t ws_bytes,

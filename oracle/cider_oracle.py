@@ -252,9 +252,9 @@ def mv_pergroup(x: np.ndarray, w: np.ndarray, sw_gn: np.ndarray,
     """M == 1 per-group decode MV (fp16 activation).
 
     Follows ``cider/kernels/pergroup_int8_mv.metal:22-106``: per lane and
-    block, ``g = (256 b + 8 l) / gs`` (:129), ``dot`` over 8 exact products
-    left to right (:148-149), ``result += f32(sw[g, n] * dot)`` (:152-153),
-    ``simd_sum`` (:165) and ``y = h(f32(R + f32(bias)))`` (:173).
+    block, ``g = (256 b + 8 l) / gs`` (:58), ``dot`` over 8 exact products
+    left to right (:77-78), ``result += f32(sw[g, n] * dot)`` (:81-82),
+    ``simd_sum`` (:94) and ``y = h(f32(R + f32(bias)))`` (:102).
     """
     xv = np.asarray(x, np.float16).reshape(-1).astype(F32)
     w = np.asarray(w, np.int8)

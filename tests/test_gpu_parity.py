@@ -923,11 +923,26 @@ def test_cider_linear_from_float_and_convert():
         assert_bits_equal(H(y).reshape(-1, 96), exp)
     model = torch.nn.Sequential(torch.nn.Linear(128, 64), torch.nn.ReLU(),
                                 torch.nn.Sequential(torch.nn.Linear(64, 32))).to(DEV)
+    w0, b0 = (model[0].weight.detach().float().cpu().numpy(),
+              model[0].bias.detach().half().cpu().numpy())
+    w1, b1 = (model[2][0].weight.detach().float().cpu().numpy(),
+              model[2][0].bias.detach().half().cpu().numpy())
     stats = C.convert_model(model, verbose=False)
     assert stats["n_converted"] == 2
     assert isinstance(model[0], C.CiderLinear) and isinstance(model[2][0], C.CiderLinear)
-    out = model(torch.randn(4, 128, device=DEV, dtype=torch.float16))
+    # the converted weights are the reference quantizer's, and the converted
+    # model's output is the oracle's linear -> ReLU -> linear chain
+    q0, s0 = O.quantize_weight_int8(w0)
+    q1, s1 = O.quantize_weight_int8(w1)
+    assert_bits_equal(model[0].w_int8.cpu().numpy(), q0, "converted w0")
+    assert_bits_equal(model[0].scale_w.cpu().numpy(), s0, "converted scale 0")
+    assert_bits_equal(model[2][0].w_int8.cpu().numpy(), q1, "converted w1")
+    xm = torch.randn(4, 128, device=DEV, dtype=torch.float16)
+    out = model(xm)
     assert out.shape == (4, 32)
+    y0 = O.perchannel_linear(xm.cpu().numpy(), q0, s0, b0)
+    r0 = np.where(y0 > 0, y0, np.float16(0)).astype(np.float16)
+    assert_bits_equal(H(out), O.perchannel_linear(r0, q1, s1, b1), "converted model")
 
 
 def test_w4a8_module():
