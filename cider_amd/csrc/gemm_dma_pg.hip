@@ -1,11 +1,31 @@
 // Per-group int8 GEMM on the LDS-DMA pipeline (int8 or packed int4 weights,
 // gs 64 / 128, and gs 256 for int8 weights; K % 128 == 0, N % 8 == 0).
 //
-// Reference semantics (cider/kernels/pergroup_int8_gemm.metal:90-191), kept
-// operation for operation, so results are bit-identical to the restatement:
+// Reference semantics (cider/kernels/pergroup_int8_gemm.metal:90-191):
 //   D_g[m,n] = sum over the gs k of group g of qa[m,k] * w[n,k]   (exact int32)
-//   acc      = +0.0;  acc = acc + f32(f32(D_g) * sw[g,n])  for g = 0, 1, ...
+//   acc      = +0.0;  acc += float(D_g) * sw[g,n]  for g = 0, 1, ...
 //   y[m,n]   = h(f32(acc * sa[m]) [+ f32(bias[n])])
+// The reference compiles that flush under Metal's fast-math, which may
+// contract it into a fused multiply-add, so its fp32 chain is defined up to
+// the rounding of each product.  Here D_g is always exact, and the flush
+// takes one of three forms:
+//   * fma: acc = fma(f32(D_g), s, acc), 2 VALU ops per accumulator and group
+//     (int8 weights with fp32 scales in both kernels; every format in the
+//     one-set kernel), for tiles whose scales are all finite with |s| < 2^64
+//     (pg_scales_tame, a workgroup vote after the prologue).  The result
+//     differs from the two-rounding chain by the rounding of each product,
+//     within the per-group bar of the tests.
+//   * fast (fp16 scales in the two-set kernel): one fma per term from a
+//     biased sum (below) rounds D_g * s once, bit-identical to the exact
+//     chain, then the add: 2 VALU ops.
+//   * exact: acc = acc + f32(f32(D_g) * s), the reference's operation order
+//     with both roundings, 3 VALU ops: tiles with a non-finite or huge scale
+//     (pg_exact_tile, straight from global memory; real weights' scales never
+//     take it), and the two-set kernel where the fast flush's registers do
+//     not fit.
+// Split-K (mid M on small N): S K-slices of whole groups run the 64 x 64 tile
+// into fp32 partial chains, and pg_splitk_sum_kernel adds the slices in slice
+// order before the epilogue's fp32 operations.
 //
 // MI355X design
 //   * Waves of 64 x 32 (TM = 2 blocks of 32 x 32 along m, TN = 1 along n),
@@ -15,31 +35,30 @@
 //     (gemm_dma.hip).  Three launch shapes: 128 x 128 tiles of 8 waves (two
 //     per SIMD, 4 ring slots; gs 64 and 256 at M > 64), 128 x 64 tiles of
 //     4 waves (gs 128 at two workgroups per CU, gs 64 at M <= 64), and 64 x 64
-//     tiles of four 32 x 32 waves where those would leave most CUs idle.
+//     tiles of four 32 x 32 waves where those would leave most CUs idle (and
+//     for the split-K slices).  gemm_dma_pg1_kernel below (one group set,
+//     waves of 64 x 64) takes the grids of 512 tiles and more.
 //   * Group accumulators: two int32 sets alternate by group.  A group's first
 //     MFMA takes C = 0 (an inline constant), so starting a group costs
 //     nothing.  While group g accumulates, group g-1 is flushed into the fp32
 //     accumulators, a slice per sub-step interleaved with group g's MFMAs in
-//     the same fixed order: 3 VALU ops per accumulator (convert, multiply by
-//     the scale, add: the reference's two roundings rule out a fused
-//     multiply-add).  That flush is the kernel's bound: 12 VALU ops per MFMA
-//     at gs = 128, 24 at gs = 64, against the MFMA's 32 cycles and 4 per
-//     wave64 VALU op (6 at gs = 256).  A gs 256 group spans two k-stages, so
-//     the sets alternate over a period of 4 stages instead of 2.  Before the
-//     first group the other set is zero and its "scales" are a zero row, so
-//     the first flush adds +0.0; the last stage flushes the last group after
-//     its MFMAs.  fp16 scales (W4A8) take the fast flush below: the MFMA
-//     starts each group from a float bias, and one fma per accumulator
-//     replaces the conversion and the multiply (2 VALU ops).  Every register is
-//     architectural (no AGPR reads in the flush) and nothing spills: a spill
-//     reload is a vector-memory load the compiler tracks, and waiting for it
-//     would also wait for every LDS-DMA load in flight.
+//     the same fixed order.  The flush bounds the kernel: at 2 VALU ops per
+//     accumulator, 8 VALU ops per MFMA at gs = 128 and 16 at gs = 64, against
+//     the MFMA's 32 cycles and 4 per wave64 VALU op.  A gs 256 group spans two
+//     k-stages, so the sets alternate over a period of 4 stages instead of 2.
+//     Before the first group the other set is zero and its "scales" are a
+//     zero row, so the first flush adds +0.0; the last stage flushes the last
+//     group after its MFMAs.  Every register is architectural (no AGPR reads
+//     in the flush) and nothing spills: a spill reload is a vector-memory load
+//     the compiler tracks, and waiting for it would also wait for every
+//     LDS-DMA load in flight.
 //   * Scales: wave 0 DMAs the scale rows of a stage's groups (sw[g, n0..n0+BN))
 //     into an 8-slot LDS ring of its own, so a row stays in LDS until its
 //     group has been flushed during the next stage.  Wave 0 therefore moves one
 //     more load per stage than the others, and waits with its own count.
 //   * Epilogue: sa and bias are requested during the last stage; acc * sa
-//     (+ bias) is converted to fp16, staged in LDS and stored in whole rows.
+//     (+ bias) is converted to fp16, staged in LDS and stored in whole rows
+//     (a split-K slice stores its fp32 chains instead).
 #include "common.hpp"
 #include "dma_common.hpp"
 #include "kernels.hpp"
@@ -788,8 +807,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 // little there, and its registers are better spent on a wave tile twice as
 // large: per output and group 4 bytes of LDS fragment reads instead of 6.
 // Each group's sum D_g lives in one int32 set; the first sub-step of group g
-// flushes block row a of group g-1 (acc = acc + f32(f32(D) * s), in group
-// order, exactly as above) right before the MFMAs that start blocks (a, b) of
+// flushes block row a of group g-1 (in group order: the fma flush, or the
+// exact one with FL == 0) right before the MFMAs that start blocks (a, b) of
 // group g from C = 0, with scales read into registers during the sub-step
 // before.  Before the first group D is zero and the scales are the zero row;
 // the last group is flushed after the k-loop.
