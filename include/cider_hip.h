@@ -126,7 +126,7 @@ int cider_perchannel_gemm(const int8_t* q, const float* sa, const int8_t* w_nk,
  * into fp32 chains that are then added, on mid-M shapes with few tiles; the
  * fp16 outputs are within 1e-3 relative / 1 fp16 ulp of the chain above, or
  * within its fp32 error bound where the sum cancels.  The small-M kernels
- * (M <= 16, and M <= 64 on N < 8192) keep the chain above bit for bit. */
+ * (M <= 16, and M <= 64 on N < 8192) keep the chain above bit for bit.
  * Replaces _cider_prim.pergroup_linear (csrc/src/prim_bindings.cpp:21-27,
  * csrc/src/pergroup_primitive.mm:138-312). The reference's unused
  * `new_bias` argument has no counterpart. */

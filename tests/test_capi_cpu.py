@@ -34,6 +34,19 @@ def test_header_declares_entry_points():
     assert len(syms) == 20, syms
 
 
+@pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
+def test_header_compiles_as_c_and_cpp(lang, compiler, tmp_path):
+    """The header is what a binding (cgo, JNI, ctypes' C stub) includes: it
+    must compile on its own as C and as C++."""
+    import shutil
+    import subprocess
+    if shutil.which(compiler) is None:
+        pytest.skip(f"{compiler} not installed")
+    r = subprocess.run([compiler, "-fsyntax-only", "-Wall", "-Werror", "-x", lang, HEADER],
+                       capture_output=True, text=True, cwd=tmp_path)
+    assert r.returncode == 0, r.stderr
+
+
 def test_library_exports_every_header_symbol(lib):
     from cider_amd import _lib
     syms = header_symbols()
