@@ -55,6 +55,45 @@ __device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b, i32x4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// Lane moves within rows of 16 lanes by DPP (a VALU operand modifier, no LDS
+// round trip as with __shfl_xor): lane l reads lane l ^ 1, l ^ 2, the mirror
+// of l in its 8 lanes (7 - l) or in its 16 lanes (15 - l).
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_mov(int32_t v) {
+  return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppMirror8 = 0x141, kDppMirror16 = 0x140;
+
+// Every lane of each aligned group of G lanes (G = 1, 2, 4, 8 or 16) gets the
+// group's int32 sum (exact in any order).
+template <int G>
+__device__ __forceinline__ int32_t group_sum_i32(int32_t v) {
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "lane group");
+  if constexpr (G >= 2) v += dpp_mov<kDppXor1>(v);
+  if constexpr (G >= 4) v += dpp_mov<kDppXor2>(v);
+  if constexpr (G >= 8) v += dpp_mov<kDppMirror8>(v);
+  if constexpr (G >= 16) v += dpp_mov<kDppMirror16>(v);
+  return v;
+}
+
+// Sum over the 64 lanes, in every lane: int32 (exact), and fp32 in a fixed
+// order (pairs, quads, 8s and 16s by DPP, then the four rows of 16).
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+  v = group_sum_i32<16>(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppXor1>(__builtin_bit_cast(int32_t, v)));
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppXor2>(__builtin_bit_cast(int32_t, v)));
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppMirror8>(__builtin_bit_cast(int32_t, v)));
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppMirror16>(__builtin_bit_cast(int32_t, v)));
+  v = v + __shfl_xor(v, 16);
+  v = v + __shfl_xor(v, 32);
+  return v;
+}
+
 // Sign-extends the four two's-complement nibbles held in the low half of each
 // byte of t (t & 0xF0F0F0F0 == 0) to four int8 bytes, without carries between
 // bytes:  (n ^ 0x88) - 8  lies in [120, 135] for every nibble n, and xor 0x80

@@ -165,10 +165,7 @@ __global__ __launch_bounds__(1024) void gemv_q_kernel(const GemmArgs p) {
     if constexpr (EPI == EPI_PG) {
       // D_g over the CPG consecutive lanes of each group (exact int32)
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-#pragma unroll
-        for (int off = CPG / 2; off >= 1; off >>= 1) d[m] += __shfl_xor(d[m], off);
-      }
+      for (int m = 0; m < MT; ++m) d[m] = group_sum_i32<CPG>(d[m]);
       if (in && (lane % CPG) == 0) {
         const int g = c / CPG;
         const float sw = scale1<SWH>(p.sw, (int64_t)g * N + n);
@@ -207,10 +204,7 @@ __global__ __launch_bounds__(1024) void gemv_q_kernel(const GemmArgs p) {
     }
   } else {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) acc[m] += __shfl_xor(acc[m], off);
-    }
+    for (int m = 0; m < MT; ++m) acc[m] = wave_sum_i32(acc[m]);
     if (lane == 0) {
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
@@ -393,8 +387,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4_kernel(const uint16_t* __res
     int d = dot16(lo, *reinterpret_cast<const i32x4*>(xq + 32 * kc), 0);
     d = dot16(hi, *reinterpret_cast<const i32x4*>(xq + 32 * kc + 16), d);
     if constexpr (PG) {
-#pragma unroll
-      for (int off = CPG / 2; off >= 1; off >>= 1) d += __shfl_xor(d, off);
+      d = group_sum_i32<CPG>(d);
       if ((lane % CPG) == 0) {
         const int g = kc / CPG;
         terms[wave][r][g] = (float)d * h2f(ssc[g * WR + wave * R + r]);
@@ -409,8 +402,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_w4_kernel(const uint16_t* __res
   if constexpr (!PG) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off);
+      acc[r] = wave_sum_i32(acc[r]);
     if (lane < R && n0 + lane < N) {
       int av = acc[0];
 #pragma unroll

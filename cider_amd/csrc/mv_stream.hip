@@ -25,8 +25,8 @@
 // them by x and accumulate in fp32: 1.75 VALU operations per weight element.
 // The products are exact (8-bit by 11-bit significands); each lane sums its
 // chunks' products in chunk order (per group: each chunk's sum times its
-// scale), and the 64 lanes of a row are summed by an xor butterfly
-// (offsets 32 .. 1).
+// scale), and the 64 lanes of a row are summed in a fixed tree: pairs, quads,
+// 8s and 16s by DPP lane moves, then the four 16-lane rows.
 //
 // Producer modes (XM) stage x' = RMSNorm(x), RMSNorm(x + add) or SwiGLU in
 // the same way as the producer kernels (norm_common.hpp, thread t handling the
@@ -214,9 +214,10 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
     acc[rlo] = acc[rlo] + (r == rlo ? d : 0.0f);
     if (rhi != rlo) acc[rhi] = acc[rhi] + (r == rhi ? d : 0.0f);
   }
-  // ---- rows: xor butterfly over the 64 lanes
+  // ---- rows: sums over the 64 lanes (pairs, quads, 8s and 16s by DPP lane
+  // moves, then the four 16-lane rows)
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum_dpp(acc[r]);
   if (lane < R && n0 + lane < N) {
     float a = acc[0];
 #pragma unroll
