@@ -77,21 +77,24 @@ __device__ __forceinline__ int32_t group_sum_i32(int32_t v) {
 }
 
 // Sum over the 64 lanes, in every lane: int32 (exact), and fp32 in a fixed
-// order (pairs, quads, 8s and 16s by DPP, then the four rows of 16).
+// order (pairs, quads, 8s and 16s by DPP; then the four 16-lane row sums,
+// read into scalar registers, as (r0 + r1) + (r2 + r3)).
 __device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
   v = group_sum_i32<16>(v);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = v + __builtin_bit_cast(float, dpp_mov<kDppXor1>(__builtin_bit_cast(int32_t, v)));
   v = v + __builtin_bit_cast(float, dpp_mov<kDppXor2>(__builtin_bit_cast(int32_t, v)));
   v = v + __builtin_bit_cast(float, dpp_mov<kDppMirror8>(__builtin_bit_cast(int32_t, v)));
   v = v + __builtin_bit_cast(float, dpp_mov<kDppMirror16>(__builtin_bit_cast(int32_t, v)));
-  v = v + __shfl_xor(v, 16);
-  v = v + __shfl_xor(v, 32);
-  return v;
+  const int32_t b = __builtin_bit_cast(int32_t, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // Sign-extends the four two's-complement nibbles held in the low half of each
