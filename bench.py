@@ -776,13 +776,13 @@ def measure_qwen3(torch, args, dev, torch_producers=False):
     gen.manual_seed(args.seed)
     ids = torch.randint(0, cfg.vocab_size, (L,), device=dev, generator=gen)
     stream = torch.cuda.current_stream(dev)
-    m.prefill(ids)  # warm-up
+    m.prefill(ids, last_only=True)  # warm-up
     torch.cuda.synchronize()
     reps = 3
     e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     e[0].record(stream)
     for _ in range(reps):
-        logits = m.prefill(ids)
+        logits = m.prefill(ids, last_only=True)
     e[1].record(stream)
     torch.cuda.synchronize()
     prefill_ms = e[0].elapsed_time(e[1]) / reps

@@ -322,9 +322,12 @@ class Qwen3(torch.nn.Module):
 
     # ---- prefill ----------------------------------------------------------
     @torch.no_grad()
-    def prefill(self, ids: torch.Tensor) -> torch.Tensor:
+    def prefill(self, ids: torch.Tensor, last_only: bool = False) -> torch.Tensor:
         """ids [L] int64 on the device; fills the KV cache for positions
-        0..L-1 and returns the logits [L, vocab] (fp16)."""
+        0..L-1 and returns the logits [L, vocab] (fp16), or with last_only
+        those of the last position [1, vocab] -- what generation needs; the
+        reference's prefill evaluates only the cache, and the last token's
+        logits come from its first step (vlm_service/custom_qwen3vl.py:598-660)."""
         L = ids.shape[0]
         if L > self.max_len:
             raise ValueError(f"prompt of {L} tokens exceeds max_len={self.max_len}")
@@ -335,11 +338,15 @@ class Qwen3(torch.nn.Module):
             for i, layer in enumerate(self.layers):
                 x, pending = layer.prefill_fused(x, pending, (self.cos, self.sin), pos, pos,
                                                  self.k_cache[i], self.v_cache[i], L)
+            if last_only:
+                x, pending = x[-1:].clone(), pending[-1:].clone()
             return F.linear(self._final_norm(x, pending), self.lm_head)
         cos, sin = self.cos[:L, None, :], self.sin[:L, None, :]
         mask = torch.full((L, L), float("-inf"), device=self.device).triu_(1)
         for i, layer in enumerate(self.layers):
             x = layer.prefill(x, cos, sin, self.k_cache[i], self.v_cache[i], mask)
+        if last_only:
+            x = x[-1:]
         return F.linear(rms_norm(x, self.final_norm, self.cfg.rms_eps), self.lm_head)
 
     def _final_norm(self, x, pending):
@@ -390,7 +397,7 @@ class Qwen3(torch.nn.Module):
         L = ids.shape[0]
         if L + steps > self.max_len:
             raise ValueError("prompt + steps exceeds max_len")
-        logits = self.prefill(ids)
+        logits = self.prefill(ids, last_only=True)
         first = torch.argmax(logits[-1].float()).reshape(1)
         state = {"tok": first.clone(), "pos": torch.tensor([L], device=self.device),
                  "i": torch.zeros(1, dtype=torch.int64, device=self.device),

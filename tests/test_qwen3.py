@@ -119,6 +119,24 @@ def test_tiny_prefill_matches_fp32_model():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("fused", [True, False])
+def test_tiny_prefill_last_only(fused):
+    """prefill(last_only=True) fills the same cache and returns the last
+    position's logits: the final norm is per row, so only the lm_head
+    product (one row instead of L) may round differently."""
+    m = Q.Qwen3(TINY, max_len=256, seed=5, fused=fused)
+    ids = torch.randint(0, TINY.vocab_size, (77,), device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(6))
+    full = m.prefill(ids)
+    k_full = [k.clone() for k in m.k_cache]
+    last = m.prefill(ids, last_only=True)
+    assert last.shape == (1, TINY.vocab_size)
+    assert all(torch.equal(a, b) for a, b in zip(k_full, m.k_cache))
+    a, b = last[0].float(), full[-1].float()
+    assert (a - b).abs().max().item() <= 1e-2 * b.abs().max().item()
+
+
+@pytest.mark.gpu
 def test_tiny_decode_matches_prefill():
     m = Q.Qwen3(TINY, max_len=256, seed=3)
     ids = torch.randint(0, TINY.vocab_size, (65,), device="cuda",
