@@ -8,8 +8,10 @@ through the one-call C entry ``cider_w4a8_linear_ref``).  Each case runs the
 whole problem on the GPU (so the dispatcher picks the kernel and grid it
 picks in production) and compares rows against the CPU oracle: all rows at
 M <= 16, otherwise the first 16, the last 16 and 16 seeded random rows.
-Bar: bit-exact for every GEMM; the M == 1 MV within the bar stated where it
-is checked.
+Bar: bit-exact for the per-channel GEMMs and the reference W4 layout; the
+per-group formats within the per-group bar of tests/util.py (their DMA
+kernels flush with fused multiply-adds and split K at mid M); the M == 1 MV
+within the MV bar.
 """
 
 import ctypes
