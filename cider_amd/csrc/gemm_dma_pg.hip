@@ -1269,23 +1269,47 @@ __global__ __launch_bounds__(256) void pg_splitk_sum_kernel(const GemmArgs p,
       i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
 }
 
+// Tile of the split-K slices, with the workgroups one CU holds and the
+// shortest slice: 128 x 128 (eight 64 x 32 waves, one per CU, 2048 k) from
+// 256 rows; below that 128 x 64 (four 64 x 32 waves, two per CU, 2048 k), and
+// for gs 256 64 x 64 (four 32 x 32 waves, two per CU, 1024 k: 27.5 against
+// 29.7 us for 128 x 128 at M=128 N=2560 K=10240).
+namespace {
+struct PgSplitTile {
+  int bm, bn, per_cu, min_slice;
+};
+PgSplitTile pg_split_tile(int M, int gs) {
+  if (M >= 256) return {128, 128, 1, 2048};
+  if (gs == 256) return {64, 64, 2, 1024};
+  return {128, 64, 2, 2048};
+}
+}  // namespace
+
 // K slices of the per-group linear (1 = no split): at M > 64 (smaller M runs
-// the skinny kernels), where the 64 x 64 tiles (the mid-M grid below) would
-// fill at most half the CUs, the most slices,
-// in powers of two up to 8, that keep the grid within two workgroups per CU
-// and each slice at 8 k-stages or more, of whole groups.  The slices' fp32
-// chains are added in slice order, so the result follows the per-group
-// tolerance bar, not the sequential chain's bits.  The caller checks the DMA
-// conditions (K % 128 == 0, N % 8 == 0, aligned operands, K * 256 < 2^32).
+// the skinny kernels), the most slices, in powers of two up to 8, that keep
+// the slices' workgroups within what the CUs hold at once, each slice of
+// whole groups and no shorter than the tile's minimum.  Measured (kernels +
+// slice sum, weights from HBM, against the 64 x 64 tiles in up to eight
+// slices within two workgroups per CU that ran before, and the unsplit
+// dispatch at M >= 256): int8 M=128 N=2560 K=10240 gs 64 23.1 -> 21.6 us,
+// gs 128 22.3 -> 19.7 us; M=256 gs 64 37.8 -> 27.0 us, gs 128 30.2 -> 25.2
+// us; M=512 gs 128 42.0 -> 36.1 us; int4 M=512 N=4096 K=12288 gs 128 65.5 ->
+// 55.4 us, gs 64 84.8 -> 68.6 us; M=128 gs 128 25.7 -> 24.6 us.  Grids that
+// already fill the CUs, or short K (M=128 N=10240 K=2560: 16.8 against 20.0
+// us in two slices), do not split.  The slices' fp32 chains are added in
+// slice order, so the result follows the per-group tolerance bar, not the
+// sequential chain's bits.  The caller checks the DMA conditions
+// (K % 128 == 0, N % 8 == 0, aligned operands, K * 256 < 2^32).
 int pg_splitk_ways(int M, int N, int K, int gs) {
   if (M <= 64 || N % 8 != 0 || K % 128 != 0) return 1;
   if ((int64_t)K * 256 >= ((int64_t)1 << 32)) return 1;
-  const int cus = num_cus();
-  const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
-  if (2 * tiles > cus) return 1;
+  const PgSplitTile t = pg_split_tile(M, gs);
+  const int slots = t.per_cu * num_cus();
+  const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   const int unit = gs > 128 ? gs : 128;
   int S = 1;
-  while (S < 8 && tiles * 2 * S <= 2 * cus && K % (unit * 2 * S) == 0 && K / (2 * S) >= 1024)
+  while (S < 8 && tiles * 2 * S <= slots && K % (unit * 2 * S) == 0 &&
+         K / (2 * S) >= t.min_slice)
     S *= 2;
   return S;
 }
@@ -1298,9 +1322,18 @@ size_t pg_splitk_bytes(int M, int N, int K, int gs) {
 namespace {
 
 template <int GS, bool SWH, int WF>
-hipError_t run_pg64_splitk(const GemmArgs& a, int S, float* part, hipStream_t s) {
-  const dim3 grid(((a.M + 63) / 64) * ((a.N + 63) / 64), S);
-  gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<grid, 256, 0, s>>>(a, a.K / S, part);
+hipError_t run_pg_splitk(const GemmArgs& a, int S, float* part, hipStream_t s) {
+  const PgSplitTile t = pg_split_tile(a.M, GS);
+  const int bm = t.bm, bn = t.bn;
+  const dim3 grid(((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn), S);
+  if (bn == 128) {
+    gemm_dma_pg_kernel<128, 128, GS, SWH, WF, 1, 2, 4><<<grid, 512, 0, s>>>(a, a.K / S, part);
+  } else if (bm == 64) {
+    gemm_dma_pg_kernel<64, 64, GS, SWH, WF, 2, 2, 2><<<grid, 256, 0, s>>>(a, a.K / S, part);
+  } else {
+    if constexpr (GS != 256)
+      gemm_dma_pg_kernel<128, 64, GS, SWH, WF, 2, 2, 2><<<grid, 256, 0, s>>>(a, a.K / S, part);
+  }
   return hipGetLastError();
 }
 
@@ -1310,16 +1343,16 @@ hipError_t launch_gemm_pg_splitk(const GemmArgs& a, int gs, bool sw_half, int wf
                                  float* part, hipStream_t s) {
   hipError_t e;
   if (wf == W_I4)
-    e = gs == 64 ? run_pg64_splitk<64, true, W_I4>(a, S, part, s)
-                 : run_pg64_splitk<128, true, W_I4>(a, S, part, s);
+    e = gs == 64 ? run_pg_splitk<64, true, W_I4>(a, S, part, s)
+                 : run_pg_splitk<128, true, W_I4>(a, S, part, s);
   else if (sw_half)
-    e = gs == 64 ? run_pg64_splitk<64, true, W_I8>(a, S, part, s)
-        : gs == 128 ? run_pg64_splitk<128, true, W_I8>(a, S, part, s)
-                    : run_pg64_splitk<256, true, W_I8>(a, S, part, s);
+    e = gs == 64 ? run_pg_splitk<64, true, W_I8>(a, S, part, s)
+        : gs == 128 ? run_pg_splitk<128, true, W_I8>(a, S, part, s)
+                    : run_pg_splitk<256, true, W_I8>(a, S, part, s);
   else
-    e = gs == 64 ? run_pg64_splitk<64, false, W_I8>(a, S, part, s)
-        : gs == 128 ? run_pg64_splitk<128, false, W_I8>(a, S, part, s)
-                    : run_pg64_splitk<256, false, W_I8>(a, S, part, s);
+    e = gs == 64 ? run_pg_splitk<64, false, W_I8>(a, S, part, s)
+        : gs == 128 ? run_pg_splitk<128, false, W_I8>(a, S, part, s)
+                    : run_pg_splitk<256, false, W_I8>(a, S, part, s);
   if (e != hipSuccess) return e;
   const int64_t quads = ((int64_t)a.M * a.N) / 4;
   pg_splitk_sum_kernel<<<(unsigned)((quads + 255) / 256), 256, 0, s>>>(a, part, S);
@@ -1350,8 +1383,8 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
   {
     // The one-set kernel: 128 x 128 tiles of four 64 x 64 waves, two
     // workgroups per CU, for int8 weights with fp32 scales and int4 weights
-    // with fp16 scales, once its tiles fill the 512 workgroup slots (bit-
-    // identical to the kernels below).  Against the two-set kernel's tiles
+    // with fp16 scales, once its tiles fill the 512 workgroup slots (the fma
+    // chain of the kernels below for fp32 scales).  Against the two-set kernel's tiles
     // (weights from HBM where they exceed the MALL): M=4096 N=10240 K=2560 gs
     // 128 188.5 -> 153.9 us, gs 64 228.8 -> 197.4 us, gs 256 163.2 -> 136.5
     // us; M=4096 N=2560 K=10240 gs 128 171.1 -> 159.1 us; M=1024 N=10240

@@ -733,9 +733,11 @@ def test_pergroup_small_tiles(M, N, K):
 # them take the exact chain from global memory (fp32 scales) or redo the
 # fast flush exactly (fp16 scales), the others flush with fma; the slices'
 # partial sums then carry the infinities and NaNs into the sum.
-@pytest.mark.parametrize("gs", [64, 128])
-def test_pergroup_splitk_special_scales(gs):
-    M, N, K = 128, 2560, 4096                      # 80 tiles of 64 x 64, 4 K slices
+@pytest.mark.parametrize("M,gs", [(128, 64), (128, 128), (128, 256), (256, 64), (256, 128), (256, 256)])
+def test_pergroup_splitk_special_scales(M, gs):
+    # two K slices: 40 tiles of 128 x 64 at M=128, of 128 x 128 at M=256;
+    # gs 256 at M=128: four, of 80 tiles of 64 x 64
+    N, K = 2560, 4096
     x, w, _, b = synth_pc(M, N, K, 164 + gs)
     x[5, :] = 0
     w[:, :gs] = -127
@@ -747,7 +749,9 @@ def test_pergroup_splitk_special_scales(gs):
     with np.errstate(invalid="ignore", over="ignore"):
         exp = O.pergroup_linear(x, w, sw, gs, b)
     assert np.isinf(exp).any() and np.isnan(exp).any()
-    assert_pergroup_linear_close(y, x, w, sw, b, gs, exp, f"pg split-K special gs{gs}")
+    assert_pergroup_linear_close(y, x, w, sw, b, gs, exp, f"pg split-K special M={M} gs{gs}")
+    if gs == 256:
+        return                                     # the W4A8 formats define gs 64 / 128
     w4 = np.random.default_rng(166).integers(-8, 8, (N, K), dtype=np.int8)
     w4[:, :gs] = -8
     pk = O.pack_w4_lo_first(w4)
@@ -758,7 +762,7 @@ def test_pergroup_splitk_special_scales(gs):
     with np.errstate(invalid="ignore", over="ignore"):
         exp = O.w4a8_pergroup_linear(x, pk, sc, gs, b)
     assert np.isinf(exp).any() and np.isnan(exp).any()
-    assert_pergroup_linear_close(y, x, w4, sc, b, gs, exp, f"w4g split-K special gs{gs}")
+    assert_pergroup_linear_close(y, x, w4, sc, b, gs, exp, f"w4g split-K special M={M} gs{gs}")
 
 
 # Split-K per-channel GEMM (M from 17 to 512 where the tiles fill at most a
