@@ -36,7 +36,7 @@
 //     per SIMD, 4 ring slots; gs 64 and 256 at M > 64), 128 x 64 tiles of
 //     4 waves (gs 128 at two workgroups per CU, gs 64 at M <= 64), and 64 x 64
 //     tiles of four 32 x 32 waves where those would leave most CUs idle (and
-//     for the split-K slices).  gemm_dma_pg1_kernel below (one group set,
+//     for the split-K slices).  gemm_dma_pg16_kernel below (one group set,
 //     waves of 64 x 64) takes the grids of 512 tiles and more.
 //   * Group accumulators: two int32 sets alternate by group.  A group's first
 //     MFMA takes C = 0 (an inline constant), so starting a group costs
@@ -797,38 +797,52 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
   }
 }
 
-// One group set (int8 or int4 weights): the same pipeline with waves of 64 x 64
-// (TM = TN = 2) at two waves per SIMD (launched as 128 x 128 tiles of four
-// waves, two workgroups per CU).  Two waves on one SIMD do not overlap one
-// wave's MFMAs with the other's VALU work when both mix them (a
-// microbenchmark of 4 MFMAs + 48 flush-like VALU ops per wave and iteration:
-// 498 cycles per SIMD at two waves, against 244 for the MFMAs and 302 for the
-// VALU ops alone), so the alternating second set of gemm_dma_pg_kernel buys
-// little there, and its registers are better spent on a wave tile twice as
-// large: per output and group 4 bytes of LDS fragment reads instead of 6.
-// Each group's sum D_g lives in one int32 set; the first sub-step of group g
-// flushes block row a of group g-1 (in group order: the fma flush, or the
-// exact one with FL == 0) right before the MFMAs that start blocks (a, b) of
-// group g from C = 0, with scales read into registers during the sub-step
-// before.  Before the first group D is zero and the scales are the zero row;
-// the last group is flushed after the k-loop.
-template <int BM, int BN, int GS, bool SWH, int WF, int WGM, int WGN, int OCC = 1, int FL = 0>
-__global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const GemmArgs p) {
+// One group set (int8 or int4 weights) on v_mfma_i32_16x16x64_i8: 128 x 128
+// tiles of four 64 x 64 waves (4 x 4 blocks of 16 x 16, 4 int32 accumulators
+// per lane and block), two workgroups per CU (two waves per SIMD), the ring,
+// DMA issue, scale ring and fixed sub-step order of gemm_dma_pg_kernel.  Two
+// waves on one SIMD do not overlap one wave's MFMAs with the other's VALU
+// work when both mix them (a microbenchmark of 4 MFMAs + 48 flush-like VALU
+// ops per wave and iteration: 498 cycles per SIMD at two waves, against 244
+// for the MFMAs and 302 for the VALU ops alone), so the alternating second
+// set of gemm_dma_pg_kernel buys little here, and its registers are better
+// spent on a wave tile twice as large: per output and group 4 bytes of LDS
+// fragment reads instead of 6.
+// A 128-k stage is two sub-steps of 64 k; in sub-step j lane l holds k in
+// [64 j + 16 (l / 16), + 16) of row l % 16 of both operands, so a group of
+// gs >= 64 never splits a sub-step (int4 weights: the 8 bytes of nibbles of
+// that k range, unpacked in the last slots of the sub-step before).  Each
+// group's sum D_g lives in one int32 set; the first sub-step of group g
+// flushes each block's sum of group g-1 (in group order: the fma flush, or
+// the exact one with FL == 0) right before the MFMA that restarts the block
+// from C = 0, with scales read into registers during the sub-step before.
+// Before the first group D is zero and the scales are the zero row; the last
+// group is flushed after the k-loop.  The 16 x 16 x 64 form against the
+// 32 x 32 x 32 one on the same pipeline (bit-identical outputs; whole linears
+// under sustained load): M=4096 N=10240 K=2560 gs 128 155.4 -> 150.7 us, gs
+// 64 182.0 -> 172.7 us, gs 256 137.9 -> 133.4 us; M=8192 gs 128 300.6 ->
+// 290.4 us; N=2560 K=10240 gs 128 169.6 -> 161.9 us; int4 M=4096 N=12288
+// K=4096 gs 128 327.8 -> 309.5 us, gs 64 386.1 -> 367.1 us.
+template <int GS, bool SWH, int WF, int FL>
+__global__ __launch_bounds__(256, 2) void gemm_dma_pg16_kernel(const GemmArgs p) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
-  using C = PgCfg<BM, BN, WF, OCC, WGM, WGN>;
+  constexpr int BM = 128, BN = 128, WGM = 2, WGN = 2;
+  using C = PgCfg<BM, BN, WF, 2, WGM, WGN>;
   constexpr bool W4 = (WF == W_I4);
   constexpr int WB = C::WB;
-  constexpr int NW = C::NW, WM = C::WM, WN = C::WN, TM = C::TM, TN = C::TN;
+  constexpr int NW = C::NW, WM = C::WM, WN = C::WN;
+  constexpr int TM = WM / 16, TN = WN / 16;      // 16 x 16 blocks of the wave
   constexpr int BK = C::BK, CH = C::CH, RPI = C::RPI, CHW = C::CHW, RPIW = C::RPIW;
   constexpr int WI = C::WI, XI = C::XI, PS = C::PS, W_BYTES = C::W_BYTES, STAGE = C::STAGE;
   constexpr int NS = C::NS, RING = C::RING, SSLOT = C::SSLOT, SNS = C::SNS;
   constexpr int OUT_LD = C::OUT_LD, OUT = C::OUT;
-  constexpr int SUBG = GS / 32;                  // k sub-steps per group (a stage has 4)
-  constexpr int SRPS = SUBG < 4 ? 4 / SUBG : 1;  // scale rows a stage brings
-  constexpr int PER = SUBG < 8 ? 1 : 2;          // stages per period of group starts
+  constexpr int SUBG = GS / 64;                  // sub-steps per group (a stage has 2)
+  constexpr int SRPS = SUBG < 2 ? 2 / SUBG : 1;  // scale rows a stage brings
+  constexpr int PER = SUBG <= 2 ? 1 : 2;         // stages per period of group starts
   constexpr int ESZ = SWH ? 2 : 4;
   constexpr int CPR = BN * ESZ / 16, ROWB = BN * ESZ;
   constexpr int NMF = TN * TM, NR = TN + TM;
+  static_assert(NR <= NMF - TN, "int4: each block unpacked in a later slot than its read");
   static_assert(CPR * 16 * SRPS <= SSLOT && 64 / CPR >= SRPS, "scale rows per stage");
   constexpr int kZeroRow = RING + (SNS - 1) * SSLOT;
   static_assert(SNS - 1 - NS >= 2 && ROWB <= SSLOT, "zero row slot");
@@ -837,7 +851,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WGM, wn = wave / WGM;
-  const int h = lane >> 5, frow = lane & 31;
+  const int frow = lane & 15, fq = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
   const int G = K / GS, nk = K / BK;
   int m0, n0;
@@ -873,40 +887,47 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       dma16s(xbase + (int64_t)st * BK, xoff[d >= WI ? d - WI : 0],
              sb + W_BYTES + (wave * XI + d - WI) * 1024);
   };
+  // scale rows of stage st: its groups (gs 64: two), or the group it belongs
+  // to (gs 256: also on the group's second stage, whose slot is not read)
   auto dma_scales = [&](int st) __attribute__((always_inline)) {
-    const int g = min(st * 4 / SUBG + srow, G - 1);
+    const int g = min(st * 2 / SUBG + srow, G - 1);
     dma16(ssrc + (int64_t)g * N * ESZ, lds0 + RING + (uint32_t)((st % SNS) * SSLOT));
   };
-  // k mapping of sub-step j for lane half h (the same for both operands):
-  //   int8 weights: k in [32 j + 16 h, + 16)               (X chunk 2j + h)
-  //   int4 weights: k in [64 (j/2) + 32 h + 16 (j%2), + 16) (X chunk
-  //     4 (j/2) + 2h + j%2; the W4 chunk 2 (j/2) + h holds the pair's 32
-  //     nibbles, read once per pair, half j%2 unpacked per sub-step)
-  auto read_x = [&](int slot, int j, int b, i32x4 (&xfn)[TM]) __attribute__((always_inline)) {
+  auto read_x = [&](int slot, int j, int b, i32x4 (&dst)[TM]) __attribute__((always_inline)) {
     const int8_t* Xs = smem + slot * STAGE + W_BYTES;
-    const int row = wm * WM + b * 32 + frow;
-    const int c = W4 ? 4 * (j / 2) + 2 * h + (j % 2) : 2 * j + h;
-    xfn[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + ((c ^ swz<BK>(row)) << 4));
+    const int row = wm * WM + b * 16 + frow;
+    dst[b] = *reinterpret_cast<const i32x4*>(Xs + row * BK + (((4 * j + fq) ^ swz<BK>(row)) << 4));
   };
-  // int8: fragment of W block a for sub-step j;  int4: the raw 16-byte chunk
-  // of W block a for the sub-step pair j / 2
+  // int8: fragment of W block a for sub-step j;  int4: its 8 bytes of nibbles
+  // (raw), unpacked by unpack_w
   auto read_w = [&](int slot, int j, int a, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
     const int8_t* Ws = smem + slot * STAGE;
-    const int row = wn * WN + a * 32 + frow;
-    const int c = W4 ? 2 * (j / 2) + h : 2 * j + h;
-    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * WB + ((c ^ swz<WB>(row)) << 4));
+    const int row = wn * WN + a * 16 + frow;
+    dst[a] = *reinterpret_cast<const i32x4*>(Ws + row * BK + (((4 * j + fq) ^ swz<BK>(row)) << 4));
   };
-  i32x4 raw[TN];  // int4 only: packed chunks of the current sub-step pair
-  auto unpack_half = [&](int a, int half, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
-    dst[a] = half == 0 ? pg_unpack_w4_8((uint32_t)raw[a][0], (uint32_t)raw[a][1])
-                       : pg_unpack_w4_8((uint32_t)raw[a][2], (uint32_t)raw[a][3]);
+  i32x2 raw[TN];
+  auto read_w4 = [&](int slot, int j, int a) __attribute__((always_inline)) {
+    const int8_t* Ws = smem + slot * STAGE;
+    const int row = wn * WN + a * 16 + frow;
+    const int c = 2 * j + (fq >> 1);
+    raw[a] = *reinterpret_cast<const i32x2*>(Ws + row * WB + ((c ^ swz<WB>(row)) << 4) +
+                                             8 * (fq & 1));
   };
-  // the 4 scales of group g (g < 0: the zero row) for quad q of block a:
-  // n = wn*WN + 32a + 8q + 4h + [0..3]
-  auto read_scales = [&](int g, int a, int q, float (&s4)[4]) __attribute__((always_inline)) {
+  auto unpack_w = [&](int a, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
+    dst[a] = pg_unpack_w4_8((uint32_t)raw[a][0], (uint32_t)raw[a][1]);
+  };
+  auto read_wk = [&](int slot, int j, int a, i32x4 (&dst)[TN]) __attribute__((always_inline)) {
+    if constexpr (W4)
+      read_w4(slot, j, a);
+    else
+      read_w(slot, j, a, dst);
+  };
+  // the 4 scales of group g (g < 0: the zero row) for n-block a:
+  // n = wn*WN + 16a + 4fq + [0..3]
+  auto read_scales = [&](int g, int a, float (&s4)[4]) __attribute__((always_inline)) {
     const int8_t* base = g < 0 ? smem + kZeroRow
-                               : smem + RING + ((g * SUBG / 4) % SNS) * SSLOT + (g % SRPS) * ROWB;
-    const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
+                               : smem + RING + ((g * SUBG / 2) % SNS) * SSLOT + (g % SRPS) * ROWB;
+    const int nl = wn * WN + a * 16 + 4 * fq;
     if constexpr (SWH) {
       const i32x2 v = *reinterpret_cast<const i32x2*>(base + nl * 2);
       s4[0] = h2f((uint16_t)((uint32_t)v[0] & 0xffffu));
@@ -922,21 +943,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
     }
   };
 
-  float facc[TN][TM][16];
-  i32x16 zero16;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) zero16[r] = 0;
-  // The scales of the next flush, read from LDS one sub-step ahead (read
-  // next to the flush, each quad's LDS latency stood exposed before its
-  // terms).
-  float svp[TN][4][4];
+  float facc[TN][TM][4];
+  const i32x4 zero4 = {0, 0, 0, 0};
+  // the scales of the next flush, read one sub-step ahead
+  float svp[TN][4];
   auto prefetch = [&](int g) __attribute__((always_inline)) {
 #pragma unroll
-    for (int a = 0; a < TN; ++a)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) read_scales(g, a, q, svp[a][q]);
+    for (int a = 0; a < TN; ++a) read_scales(g, a, svp[a]);
   };
-
   auto wait_stage = [&]() __attribute__((always_inline)) {
     if (wave == 0)
       wait_vmcnt<(NS - 2) * (PS + 1)>();
@@ -959,9 +973,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       dma16s(xbase + (int64_t)s2 * BK, xoff[i], sb + W_BYTES + (wave * XI + i) * 1024);
     if (wave == 0) dma_scales(s2);
   }
-  // FL == 1: the fma flush for tiles whose scales are all finite with
-  // |s| < 2^64, the exact flush otherwise (a workgroup-uniform choice).  The
-  // scan's loads go out behind the prologue's, so their latency overlaps it.
   bool tame = true;
   if constexpr (FL == 1) tame = pg_scales_tame<BN, SWH>(p, n0, G, 64 * NW);
   if (wave == 0)
@@ -970,9 +981,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
     wait_vmcnt<(NS - 1) * PS>();
   bool fma_tile = false;
   if constexpr (FL == 1) {
-    // workgroup vote in the unused upper half of the zero row's scale slot
-    // (no extra LDS: at int4, 256 more bytes stopped two workgroups from
-    // sharing a CU); that slot's first scale DMA comes stages later
     static_assert(ROWB + 4 * NW <= SSLOT, "vote words");
     uint32_t* vote = reinterpret_cast<uint32_t*>(smem + kZeroRow + ROWB);
     const bool wbad = __builtin_amdgcn_ballot_w64(!tame) != 0;
@@ -987,50 +995,36 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
   }
   float sa_t = 0.0f;
   uint16_t b_t = 0;
-  // The k-loop with the flush of FMAc (1: fma, 0: exact): fragment reads of
-  // stage 0, the stages, and the last group's flush.
   auto body = [&](auto fmac) __attribute__((always_inline)) {
     constexpr bool FMA = decltype(fmac)::value != 0;
-    i32x16 D[TN][TM];
+    i32x4 D[TN][TM];
 #pragma unroll
     for (int a = 0; a < TN; ++a)
 #pragma unroll
-      for (int b = 0; b < TM; ++b)
+      for (int b = 0; b < TM; ++b) {
+        D[a][b] = zero4;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          D[a][b][r] = 0;
-          facc[a][b][r] = 0.0f;
+        for (int r = 0; r < 4; ++r) facc[a][b][r] = 0.0f;
+      }
+    // flush of block (a, b), each element pinned after its update so the
+    // compiler keeps the conversions next to their use
+    auto flush_blk = [&](int a, int b) __attribute__((always_inline)) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if constexpr (FMA) {
+          facc[a][b][r] = __builtin_fmaf((float)D[a][b][r], svp[a][r], facc[a][b][r]);
+        } else {
+          const float t = (float)D[a][b][r] * svp[a][r];
+          facc[a][b][r] = facc[a][b][r] + t;
         }
-    // flush of block row a (blocks (a, 0 .. TM-1)), each element pinned after
-    // its update so the compiler keeps the conversions next to their use.
-    // FMA: facc = fma(f32(D), s, facc), 2 VALU ops per accumulator (the
-    // product is not rounded on its own); exact: facc = facc + f32(f32(D) * s),
-    // the reference's two roundings, 3 ops.  (A bit-exact fast flush of fp16
-    // scales, one fma per term from a biased sum plus the add, measured slower
-    // here: int4 gs 64 M=4096 N=12288 K=4096 495.6 against 466.9 us.)
-    auto flush_row = [&](int a) __attribute__((always_inline)) {
-  #pragma unroll
-      for (int q = 0; q < 4; ++q)
-  #pragma unroll
-        for (int b = 0; b < TM; ++b)
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if constexpr (FMA) {
-              facc[a][b][4 * q + r] =
-                  __builtin_fmaf((float)D[a][b][4 * q + r], svp[a][q][r], facc[a][b][4 * q + r]);
-            } else {
-              const float t = (float)D[a][b][4 * q + r] * svp[a][q][r];
-              facc[a][b][4 * q + r] = facc[a][b][4 * q + r] + t;
-            }
-            asm volatile("" : "+v"(facc[a][b][4 * q + r]));
-          }
+        asm volatile("" : "+v"(facc[a][b][r]));
+      }
     };
-
-    // One k sub-step in a fixed order: per MFMA slot (block a, b), the flush of
-    // the block's previous group (first sub-step of a group), the MFMA, one of
-    // the next sub-step's fragment reads (rd) and a share of the DMA loads of
-    // stage dst into slot dsl (dma); before a sub-step that flushes (pre), the
-    // scales of group pg after the first MFMA.
+    // One 64-k sub-step in a fixed order: per MFMA slot (block a, b), the
+    // flush of the block's previous group (first sub-step of a group), the
+    // MFMA, one of the next sub-step's fragment reads (rd) and a share of the
+    // DMA loads of stage dst into slot dsl (dma); before a sub-step that
+    // flushes (pre), the scales of group pg after the first MFMA.
     auto step = [&](auto firstc, auto rdc, auto dmac, auto JNc, auto prec, const i32x4 (&wc)[TN],
                     const i32x4 (&xc)[TM], int rs, i32x4 (&wn_)[TN], i32x4 (&xn)[TM], int dst,
                     int dsl, int pg) __attribute__((always_inline)) {
@@ -1039,76 +1033,58 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       constexpr bool rd = decltype(rdc)::value != 0;
       constexpr bool dma = decltype(dmac)::value != 0;
       constexpr int JN = decltype(JNc)::value;
-  #pragma unroll
+#pragma unroll
       for (int idx = 0; idx < NMF; ++idx) {
         const int a = idx / TM, b = idx % TM;
         if constexpr (first) {
-          if (b == 0) flush_row(a);
-          D[a][b] = mfma32(wc[a], xc[b], zero16);
+          flush_blk(a, b);
+          D[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[a], xc[b], zero4, 0, 0, 0);
         } else {
-          D[a][b] = mfma32(wc[a], xc[b], D[a][b]);
+          D[a][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wc[a], xc[b], D[a][b], 0, 0, 0);
         }
-        if constexpr (rd && !W4) {
-  #pragma unroll
+        if constexpr (rd) {
+#pragma unroll
           for (int q = 0; q < NR; ++q)
-            if ((q < NMF ? q : NMF - 1) == idx) {
+            if (q == idx) {
               if (q == 0)
-                read_w(rs, JN, 0, wn_);
+                read_wk(rs, JN, 0, wn_);
               else if (q <= TM)
                 read_x(rs, JN, q - 1, xn);
               else
-                read_w(rs, JN, q - TM, wn_);
+                read_wk(rs, JN, q - TM, wn_);
             }
-        }
-        if constexpr (rd && W4) {
-          // X fragments first; on a new pair the raw W chunks next, each
-          // unpacked in a later slot than its read (the slots issue reads
-          // before unpacks); otherwise the held chunks' second halves
-          constexpr bool new_pair = (JN % 2) == 0;
-          constexpr int NRD = TM + (new_pair ? TN : 0);
-  #pragma unroll
-          for (int q = 0; q < NRD; ++q)
-            if ((q < NMF ? q : NMF - 1) == idx) {
-              if (q < TM)
-                read_x(rs, JN, q, xn);
-              else
-                read_w(rs, JN, q - TM, raw);
-            }
-  #pragma unroll
-          for (int a2 = 0; a2 < TN; ++a2) {
-            constexpr int first_slot = new_pair ? (NMF > TN ? NMF - TN : 0) : 0;
-            const int want = first_slot + a2 > TM + a2 || !new_pair ? first_slot + a2 : TM + a2;
-            if ((want < NMF ? want : NMF - 1) == idx) unpack_half(a2, JN % 2, wn_);
+          // int4: block a's nibbles, read in slot 0 or TM + a, unpacked in
+          // slot NMF - TN + a
+          if constexpr (W4) {
+#pragma unroll
+            for (int a2 = 0; a2 < TN; ++a2)
+              if (NMF - TN + a2 == idx) unpack_w(a2, wn_);
           }
         }
         if constexpr (dma) {
-  #pragma unroll
+#pragma unroll
           for (int d = 0; d < PS; ++d)
             if (d * NMF / PS == idx) dma_one(dst, dsl, d);
           if (idx == 0 && wave == 0) dma_scales(dst);
         }
         if constexpr (pre) {
-          if (idx == 0) prefetch(pg);
+          if (idx == NMF - 1) prefetch(pg);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-  #pragma unroll
+#pragma unroll
     for (int b = 0; b < TM; ++b) read_x(0, 0, b, xf[0]);
-  #pragma unroll
+#pragma unroll
     for (int a = 0; a < TN; ++a) {
-      if constexpr (W4) {
-        read_w(0, 0, a, raw);
-        unpack_half(a, 0, wf[0]);
-      } else {
-        read_w(0, 0, a, wf[0]);
-      }
+      read_wk(0, 0, a, wf[0]);
+      if constexpr (W4) unpack_w(a, wf[0]);
     }
     prefetch(-1);  // the first flush: zero sums, zero scales
 
     // Stage kt at position HALF of a PER-stage period: sub-step J starts group
-    // (4 kt + J) / SUBG when (4 HALF + J) % SUBG == 0, flushing the group before;
-    // the sub-step before it reads that group's scales (PRE).
+    // (2 kt + J) / SUBG when (2 HALF + J) % SUBG == 0, flushing the group
+    // before; the sub-step before it reads that group's scales (PRE).
     auto stage = [&](int kt, auto halfc, auto lastc) __attribute__((always_inline)) {
       constexpr int HALF = decltype(halfc)::value;
       constexpr bool LAST = decltype(lastc)::value != 0;
@@ -1117,29 +1093,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
         sa_t = p.sa[min(m0 + tid % BM, M - 1)];
         if (p.bias) b_t = p.bias[min(n0 + tid % BN, N - 1)];
       }
-  #define PG1_SUB(J)                                                                              \
-    {                                                                                             \
-      constexpr bool FIRST = ((4 * HALF + (J)) % SUBG) == 0;                                      \
-      constexpr bool PRE = ((4 * HALF + (J) + 1) % SUBG) == 0;                                    \
-      const int pg = (4 * kt + (J) + 1) / SUBG - 1;                                               \
-      if constexpr ((J) < 3) {                                                                    \
-        step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<(J) + 1>{}, ic<PRE>{}, wf[(J) & 1], xf[(J) & 1],   \
-             sl, wf[((J) + 1) & 1], xf[((J) + 1) & 1], 0, 0, pg);                                 \
-      } else if constexpr (!LAST) {                                                               \
-        wait_stage();                                                                             \
-        __syncthreads();                                                                          \
-        step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], (kt + 1) % NS,      \
-             wf[0], xf[0], min(kt + NS, nk - 1), sl, pg);                                         \
-      } else {                                                                                    \
-        step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], 0, wf[0], xf[0], 0, \
-             0, pg);                                                                              \
-      }                                                                                           \
-    }
-      PG1_SUB(0)
-      PG1_SUB(1)
-      PG1_SUB(2)
-      PG1_SUB(3)
-  #undef PG1_SUB
+      {
+        constexpr bool FIRST = ((2 * HALF) % SUBG) == 0;
+        constexpr bool PRE = ((2 * HALF + 1) % SUBG) == 0;
+        const int pg = (2 * kt + 1) / SUBG - 1;
+        step(ic<FIRST>{}, ic<1>{}, ic<0>{}, ic<1>{}, ic<PRE>{}, wf[0], xf[0], sl, wf[1], xf[1], 0,
+             0, pg);
+      }
+      {
+        constexpr bool FIRST = ((2 * HALF + 1) % SUBG) == 0;
+        constexpr bool PRE = ((2 * HALF + 2) % SUBG) == 0;
+        const int pg = (2 * kt + 2) / SUBG - 1;
+        if constexpr (!LAST) {
+          wait_stage();
+          __syncthreads();
+          step(ic<FIRST>{}, ic<1>{}, ic<1>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], (kt + 1) % NS,
+               wf[0], xf[0], min(kt + NS, nk - 1), sl, pg);
+        } else {
+          step(ic<FIRST>{}, ic<0>{}, ic<0>{}, ic<0>{}, ic<PRE>{}, wf[1], xf[1], 0, wf[0], xf[0],
+               0, 0, pg);
+        }
+      }
     };
     int kt = 0;
     if constexpr (PER == 1) {
@@ -1155,13 +1129,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       stage(kt + 1, ic<1>{}, ic<1>{});
     }
     // the last group (its scales were read in the last sub-step)
-  #pragma unroll
-    for (int a = 0; a < TN; ++a) flush_row(a);
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) flush_blk(a, b);
   };
-  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN].  Each
-  // flush path ends in its own copy, so the two k-loops never join with
-  // live accumulators (joined, the register allocator kept values of both
-  // alive and the int8 tiles spilled).
+  // ---- epilogue: LDS [0, OUT) fp16 tile, then sa [BM] and bias [BN]
   auto epilogue = [&]() __attribute__((always_inline)) {
     wait_vmcnt<0>();  // reloads past the end land before LDS is reused
     float* ssa = reinterpret_cast<float*>(smem + OUT);
@@ -1170,37 +1143,34 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
     if (tid < BM) ssa[tid] = sa_t;
     if (tid < BN) sbias[tid] = b_t;
     __syncthreads();
-  #pragma unroll
+#pragma unroll
     for (int a = 0; a < TN; ++a) {
-  #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nl = wn * WN + a * 32 + 8 * q + 4 * h;
-        const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
-        const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
-                             h2f((uint16_t)((uint32_t)bb[0] >> 16)),
-                             h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
-                             h2f((uint16_t)((uint32_t)bb[1] >> 16))};
-  #pragma unroll
-        for (int b = 0; b < TM; ++b) {
-          const int ml = wm * WM + b * 32 + frow;
-          const float sam = ssa[ml];
-          float o[4];
-  #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float v = facc[a][b][4 * q + r] * sam;
-            if (p.bias) v = v + bv[r];
-            o[r] = v;
-          }
-          *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
-              i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
+      const int nl = wn * WN + a * 16 + 4 * fq;
+      const i32x2 bb = *reinterpret_cast<const i32x2*>(sbias + nl);
+      const float bv[4] = {h2f((uint16_t)((uint32_t)bb[0] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[0] >> 16)),
+                           h2f((uint16_t)((uint32_t)bb[1] & 0xffffu)),
+                           h2f((uint16_t)((uint32_t)bb[1] >> 16))};
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int ml = wm * WM + b * 16 + frow;
+        const float sam = ssa[ml];
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = facc[a][b][r] * sam;
+          if (p.bias) v = v + bv[r];
+          o[r] = v;
         }
+        *reinterpret_cast<i32x2*>(smem + ml * OUT_LD + nl * 2) =
+            i32x2{(int)f2h2(o[0], o[1]), (int)f2h2(o[2], o[3])};
       }
     }
     __syncthreads();
     constexpr int LPR = BN / 8, RPS = 64 / LPR;
     const int cl = (lane % LPR) * 8;
     const int n = n0 + cl;
-  #pragma unroll 4
+#pragma unroll 4
     for (int rr = wave * RPS + lane / LPR; rr < BM; rr += NW * RPS) {
       const int m = m0 + rr;
       if (m < M && n < N)
@@ -1213,10 +1183,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg1_kernel(const
       body(ic<1>{});
       epilogue();
     } else {
-      // Tiles with extreme scales: the exact chain from global memory (a
-      // second copy of the pipelined k-loop here made the register allocator
-      // keep values of both copies alive: spills at int8 gs 64, one wave per
-      // SIMD at int4).
       wait_vmcnt<0>();  // the prologue's DMA lands before the workgroup ends
       pg_exact_tile<BM, BN, GS, SWH, WF>(p, m0, n0, 64 * NW);
     }
@@ -1384,8 +1350,10 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
     // The one-set kernel: 128 x 128 tiles of four 64 x 64 waves, two
     // workgroups per CU, for int8 weights with fp32 scales and int4 weights
     // with fp16 scales, once its tiles fill the 512 workgroup slots (the fma
-    // chain of the kernels below for fp32 scales).  Against the two-set kernel's tiles
-    // (weights from HBM where they exceed the MALL): M=4096 N=10240 K=2560 gs
+    // chain of the kernels below for fp32 scales).  Against the two-set
+    // kernel's tiles, measured on its 32 x 32 x 32 form (the 16 x 16 x 64
+    // form it runs now is 3-6 % faster again; weights from HBM where they
+    // exceed the MALL): M=4096 N=10240 K=2560 gs
     // 128 188.5 -> 153.9 us, gs 64 228.8 -> 197.4 us, gs 256 163.2 -> 136.5
     // us; M=4096 N=2560 K=10240 gs 128 171.1 -> 159.1 us; M=1024 N=10240
     // K=2560 gs 128 49.4 -> 46.7 us; M=2048 95.3 -> 79.7 us; int4 M=4096
@@ -1401,15 +1369,15 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
       const unsigned grid = (unsigned)tiles;
       if (wf == W_I4) {
         if (gs == 64)
-          gemm_dma_pg1_kernel<128, 128, 64, true, W_I4, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg16_kernel<64, true, W_I4, 1><<<grid, 256, 0, s>>>(a);
         else
-          gemm_dma_pg1_kernel<128, 128, 128, true, W_I4, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg16_kernel<128, true, W_I4, 1><<<grid, 256, 0, s>>>(a);
       } else if (gs == 64) {
-        gemm_dma_pg1_kernel<128, 128, 64, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<64, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
       } else if (gs == 128) {
-        gemm_dma_pg1_kernel<128, 128, 128, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<128, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
       } else {
-        gemm_dma_pg1_kernel<128, 128, 256, false, W_I8, 2, 2, 2, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<256, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
       }
       return hipGetLastError();
     }
