@@ -823,8 +823,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, OCC) void gemm_dma_pg_kernel(const 
 // 64 182.0 -> 172.7 us, gs 256 137.9 -> 133.4 us; M=8192 gs 128 300.6 ->
 // 290.4 us; N=2560 K=10240 gs 128 169.6 -> 161.9 us; int4 M=4096 N=12288
 // K=4096 gs 128 327.8 -> 309.5 us, gs 64 386.1 -> 367.1 us.
+// ks > 0: split-K.  Workgroup (t, s) runs tile t over k in [s ks, (s+1) ks)
+// (whole groups and k-stages) and writes its fp32 group chain, before the
+// per-token scale, to part + s M N; pg_splitk_sum_kernel adds the slices.
 template <int GS, bool SWH, int WF, int FL>
-__global__ __launch_bounds__(256, 2) void gemm_dma_pg16_kernel(const GemmArgs p) {
+__global__ __launch_bounds__(256, 2) void gemm_dma_pg16_kernel(const GemmArgs pin, int ks,
+                                                               float* part) {
   static_assert(GS == 64 || GS == 128 || GS == 256, "group size");
   constexpr int BM = 128, BN = 128, WGM = 2, WGN = 2;
   using C = PgCfg<BM, BN, WF, 2, WGM, WGN>;
@@ -852,8 +856,20 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_pg16_kernel(const GemmArgs p)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave % WGM, wn = wave / WGM;
   const int frow = lane & 15, fq = lane >> 4;
+  // K is the row pitch; the k-loop covers KL of it (a split-K slice: the
+  // operands and scales start at the slice, and the partial sums go to pp)
+  GemmArgs p = pin;
+  float* pp = nullptr;
+  if (ks > 0) {
+    const int sl = blockIdx.y;
+    p.x = pin.x + (int64_t)sl * ks;
+    p.w = reinterpret_cast<const int8_t*>(pin.w) + (int64_t)sl * (W4 ? ks / 2 : ks);
+    p.sw = reinterpret_cast<const int8_t*>(pin.sw) + (int64_t)(sl * (ks / GS)) * pin.N * ESZ;
+    pp = part + (int64_t)sl * pin.M * pin.N;
+  }
   const int M = p.M, N = p.N, K = p.K;
-  const int G = K / GS, nk = K / BK;
+  const int KL = ks > 0 ? ks : K;
+  const int G = KL / GS, nk = KL / BK;
   int m0, n0;
   tile_coords<BM, BN>(xcd_remap(blockIdx.x, gridDim.x), M, 0, N, m0, n0);
 
@@ -1178,17 +1194,37 @@ __global__ __launch_bounds__(256, 2) void gemm_dma_pg16_kernel(const GemmArgs p)
             *reinterpret_cast<const i32x4*>(smem + rr * OUT_LD + cl * 2);
     }
   };
+  // split-K slice: the chain's fp32 sums, 4 consecutive columns per store
+  auto store_part = [&]() __attribute__((always_inline)) {
+    wait_vmcnt<0>();  // reloads past the end land before the workgroup ends
+#pragma unroll
+    for (int a = 0; a < TN; ++a)
+#pragma unroll
+      for (int b = 0; b < TM; ++b) {
+        const int m = m0 + wm * WM + b * 16 + frow;
+        const int n = n0 + wn * WN + a * 16 + 4 * fq;
+        if (m < M && n < N)
+          *reinterpret_cast<f32x4*>(pp + (int64_t)m * N + n) =
+              f32x4{facc[a][b][0], facc[a][b][1], facc[a][b][2], facc[a][b][3]};
+      }
+  };
   if constexpr (FL == 1) {
     if (fma_tile) {
       body(ic<1>{});
-      epilogue();
+      if (pp)
+        store_part();
+      else
+        epilogue();
     } else {
       wait_vmcnt<0>();  // the prologue's DMA lands before the workgroup ends
-      pg_exact_tile<BM, BN, GS, SWH, WF>(p, m0, n0, 64 * NW);
+      pg_exact_tile<BM, BN, GS, SWH, WF>(p, m0, n0, 64 * NW, 0, KL, pp);
     }
   } else {
     body(ic<0>{});
-    epilogue();
+    if (pp)
+      store_part();
+    else
+      epilogue();
   }
 }
 
@@ -1249,10 +1285,8 @@ PgSplitTile pg_split_tile(int M, int gs) {
   if (gs == 256) return {64, 64, 2, 1024};
   return {128, 64, 2, 2048};
 }
-}  // namespace
 
-// K slices of the per-group linear (1 = no split): at M > 64 (smaller M runs
-// the skinny kernels), the most slices, in powers of two up to 8, that keep
+// Slices of the two-set kernel: the most, in powers of two up to 8, that keep
 // the slices' workgroups within what the CUs hold at once, each slice of
 // whole groups and no shorter than the tile's minimum.  Measured (kernels +
 // slice sum, weights from HBM, against the 64 x 64 tiles in up to eight
@@ -1266,9 +1300,7 @@ PgSplitTile pg_split_tile(int M, int gs) {
 // slice order, so the result follows the per-group tolerance bar, not the
 // sequential chain's bits.  The caller checks the DMA conditions
 // (K % 128 == 0, N % 8 == 0, aligned operands, K * 256 < 2^32).
-int pg_splitk_ways(int M, int N, int K, int gs) {
-  if (M <= 64 || N % 8 != 0 || K % 128 != 0) return 1;
-  if ((int64_t)K * 256 >= ((int64_t)1 << 32)) return 1;
+int pg_splitk_ways_two_set(int M, int N, int K, int gs) {
   const PgSplitTile t = pg_split_tile(M, gs);
   const int slots = t.per_cu * num_cus();
   const int tiles = ((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
@@ -1280,6 +1312,40 @@ int pg_splitk_ways(int M, int N, int K, int gs) {
   return S;
 }
 
+struct PgSplit {
+  int S;         // K slices (1: no split)
+  bool one_set;  // slices of gemm_dma_pg16_kernel, else of gemm_dma_pg_kernel
+};
+
+// K slices of the per-group linear (1 = no split) at M > 64 (smaller M runs
+// the skinny kernels), and whether the one-set kernel runs them.  Grids of
+// the one-set kernel's 128 x 128 tiles that fill one and a half of its two
+// workgroups per CU run unsplit.  Below that, its slices where the most of
+// them (powers of two up to 8, within two workgroups per CU, at least 1024 k
+// each, whole groups) fill one and a half workgroups per CU again: W4A8 M=512
+// N=4096 K=12288 gs 64 75.9 -> 68.1 us, gs 128 61.0 -> 59.4 us (four slices
+// against two of the two-set kernel).  With fewer of its slices the one-set
+// kernel lost (int8 gs 64 M=1024 N=2560 K=10240: 76.0 against 69.9 us
+// unsplit; M=128 N=2560 K=10240 gs 128: 26.5 against 24.8 us), so the other
+// shapes keep the two-set kernel's slices above.
+PgSplit pg_split_plan(int M, int N, int K, int gs) {
+  if (M <= 64 || N % 8 != 0 || K % 128 != 0) return {1, false};
+  if ((int64_t)K * 256 >= ((int64_t)1 << 32)) return {1, false};
+  const int cus = num_cus();
+  const int tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (2 * tiles >= 3 * cus) return {1, false};
+  const int unit = gs > 128 ? gs : 128;
+  int S = 1;
+  while (S < 8 && tiles * 2 * S <= 2 * cus && K % (unit * 2 * S) == 0 && K / (2 * S) >= 1024)
+    S *= 2;
+  if (S > 1 && 2 * tiles * S >= 3 * cus) return {S, true};
+  return {pg_splitk_ways_two_set(M, N, K, gs), false};
+}
+
+}  // namespace
+
+int pg_splitk_ways(int M, int N, int K, int gs) { return pg_split_plan(M, N, K, gs).S; }
+
 size_t pg_splitk_bytes(int M, int N, int K, int gs) {
   const int S = pg_splitk_ways(M, N, K, gs);
   return S > 1 ? (size_t)S * M * N * 4 : 0;
@@ -1289,6 +1355,13 @@ namespace {
 
 template <int GS, bool SWH, int WF>
 hipError_t run_pg_splitk(const GemmArgs& a, int S, float* part, hipStream_t s) {
+  if constexpr (!(WF == W_I4 && GS == 256)) {
+    if (pg_split_plan(a.M, a.N, a.K, GS).one_set) {
+      const dim3 grid(((a.M + 127) / 128) * ((a.N + 127) / 128), S);
+      gemm_dma_pg16_kernel<GS, SWH, WF, 1><<<grid, 256, 0, s>>>(a, a.K / S, part);
+      return hipGetLastError();
+    }
+  }
   const PgSplitTile t = pg_split_tile(a.M, GS);
   const int bm = t.bm, bn = t.bn;
   const dim3 grid(((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn), S);
@@ -1349,8 +1422,10 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
   {
     // The one-set kernel: 128 x 128 tiles of four 64 x 64 waves, two
     // workgroups per CU, for int8 weights with fp32 scales and int4 weights
-    // with fp16 scales, once its tiles fill the 512 workgroup slots (the fma
-    // chain of the kernels below for fp32 scales).  Against the two-set
+    // with fp16 scales, once its tiles fill 384 of the 512 workgroup slots
+    // (the fma chain of the kernels below for fp32 scales; from 384 instead
+    // of 512: W4A8 gs 64 M=512 N=12288 K=4096 87.8 -> 71.6 us, gs 128 60.2
+    // -> 58.8 us).  Against the two-set
     // kernel's tiles, measured on its 32 x 32 x 32 form (the 16 x 16 x 64
     // form it runs now is 3-6 % faster again; weights from HBM where they
     // exceed the MALL): M=4096 N=10240 K=2560 gs
@@ -1365,19 +1440,19 @@ hipError_t launch_gemm_dma_pg(const GemmArgs& a, int gs, bool sw_half, int wf, h
     // M=512 N=12288 K=4096 gs 128: 52.3 against 55.8 us).
     const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.N + 127) / 128);
     const bool fmt = (wf == W_I8 && !sw_half) || (wf == W_I4 && sw_half && gs != 256);
-    if (fmt && tiles >= 2 * (int64_t)num_cus()) {
+    if (fmt && 2 * tiles >= 3 * (int64_t)num_cus()) {
       const unsigned grid = (unsigned)tiles;
       if (wf == W_I4) {
         if (gs == 64)
-          gemm_dma_pg16_kernel<64, true, W_I4, 1><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg16_kernel<64, true, W_I4, 1><<<grid, 256, 0, s>>>(a, 0, nullptr);
         else
-          gemm_dma_pg16_kernel<128, true, W_I4, 1><<<grid, 256, 0, s>>>(a);
+          gemm_dma_pg16_kernel<128, true, W_I4, 1><<<grid, 256, 0, s>>>(a, 0, nullptr);
       } else if (gs == 64) {
-        gemm_dma_pg16_kernel<64, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<64, false, W_I8, 1><<<grid, 256, 0, s>>>(a, 0, nullptr);
       } else if (gs == 128) {
-        gemm_dma_pg16_kernel<128, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<128, false, W_I8, 1><<<grid, 256, 0, s>>>(a, 0, nullptr);
       } else {
-        gemm_dma_pg16_kernel<256, false, W_I8, 1><<<grid, 256, 0, s>>>(a);
+        gemm_dma_pg16_kernel<256, false, W_I8, 1><<<grid, 256, 0, s>>>(a, 0, nullptr);
       }
       return hipGetLastError();
     }

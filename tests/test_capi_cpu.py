@@ -96,9 +96,9 @@ def test_splitk_workspace_respects_32bit_tile_offsets(lib):
 def test_pergroup_splitk_workspace(lib):
     """The per-group linears size fp32 partial chains of their K slices (256
     CUs assumed without a GPU): 40 tiles of 128 x 64 at M=128 N=2560 K=10240
-    take 4 slices, and so do its 80 tiles of 64 x 64 at gs 256; 128 tiles of
-    128 x 128 at M=512 N=4096 K=12288 take 2; grids that fill the CUs, short
-    K and M <= 64 take none."""
+    take 4 slices, and so do its 80 tiles of 64 x 64 at gs 256; the 128 tiles
+    of 128 x 128 at M=512 N=4096 K=12288 take 4 (512 workgroups of the
+    one-set kernel); grids that fill the CUs, short K and M <= 64 take none."""
     from cider_amd import _lib
     ws = _lib.workspace_bytes
 
@@ -111,7 +111,7 @@ def test_pergroup_splitk_workspace(lib):
     assert ws(_lib.CIDER_OP_PERGROUP, 128, 2560, 10240, 256) == \
         quant(128, 10240) + 4 * 128 * 2560 * 4
     assert ws(_lib.CIDER_OP_W4A8_PERGROUP, 512, 4096, 12288, 64) == \
-        quant(512, 12288) + 2 * 512 * 4096 * 4
+        quant(512, 12288) + 4 * 512 * 4096 * 4
     assert ws(_lib.CIDER_OP_PERGROUP, 128, 10240, 2560, 128) == quant(128, 2560)
     assert ws(_lib.CIDER_OP_W4A8_PERGROUP, 512, 12288, 4096, 128) == quant(512, 4096)
     assert ws(_lib.CIDER_OP_PERGROUP, 64, 2560, 10240, 64) == quant(64, 10240)

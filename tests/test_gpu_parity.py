@@ -733,11 +733,14 @@ def test_pergroup_small_tiles(M, N, K):
 # them take the exact chain from global memory (fp32 scales) or redo the
 # fast flush exactly (fp16 scales), the others flush with fma; the slices'
 # partial sums then carry the infinities and NaNs into the sum.
-@pytest.mark.parametrize("M,gs", [(128, 64), (128, 128), (128, 256), (256, 64), (256, 128), (256, 256)])
-def test_pergroup_splitk_special_scales(M, gs):
-    # two K slices: 40 tiles of 128 x 64 at M=128, of 128 x 128 at M=256;
-    # gs 256 at M=128: four, of 80 tiles of 64 x 64
-    N, K = 2560, 4096
+@pytest.mark.parametrize("M,N,gs", [(128, 2560, 64), (128, 2560, 128), (128, 2560, 256),
+                                    (256, 2560, 64), (256, 2560, 128), (256, 2560, 256),
+                                    (512, 4096, 64), (512, 4096, 128), (512, 4096, 256)])
+def test_pergroup_splitk_special_scales(M, N, gs):
+    # two K slices of the two-set kernel: 40 tiles of 128 x 64 at M=128, of
+    # 128 x 128 at M=256; gs 256 at M=128: four, of 80 tiles of 64 x 64.
+    # M=512 N=4096: four slices of the one-set kernel's 128 tiles.
+    K = 4096
     x, w, _, b = synth_pc(M, N, K, 164 + gs)
     x[5, :] = 0
     w[:, :gs] = -127
