@@ -33,6 +33,7 @@
 // 8-element chunks t, t + 256, ...), so a fused launch is bit-identical to
 // the producer launch followed by the plain MV.
 #include "common.hpp"
+#include "dma_common.hpp"
 #include "kernels.hpp"
 #include "norm_common.hpp"
 
@@ -228,6 +229,159 @@ __global__ __launch_bounds__(kWpg * 64) void mv_stream_kernel(
   }
 }
 
+
+// Long rows (per-channel; K from 10240 to 16384, K % 1024 == 0): the k range
+// splits over the workgroup's KS waves instead of its rows.  Wave v handles k
+// in [v K / KS, (v + 1) K / KS) of all KS rows: it loads and stages only that
+// part of x (or of the producer's output), into LDS of its own, so no
+// workgroup barrier stands before its first product (the RMSNorm producers
+// keep one: their row statistic); the waves' partial row sums meet in LDS at
+// the end and are added in wave order.  Lane l's chunks are l, l + 64, ... of
+// the wave's KS row slices of K / KS bytes (every wave instruction still reads
+// 1 KB of consecutive weight bytes within a row, or two runs at a row
+// boundary).  Measured against the one-row-per-wave stream (weights from HBM,
+// back-to-back launches): N=2560 K=10240 6.95 -> 6.45 us at KS = 5 (512
+// workgroups, two per CU; 6.78 us at KS = 4), N=2048 K=12288 6.66 -> 6.27 us;
+// at K = 4096 and 8192 it ran level or slower, and the per-group MV level or
+// slower, so those keep the stream above.  Producer modes compute x' exactly
+// as the producer kernels: SwiGLU per element; RMSNorm's sum of squares by
+// threads 0..255 over the 8-element chunks t, t + 256, ... and the 4-wave
+// reduction of norm_common.hpp, then each wave normalizes its own range.
+template <int K, int KS, int XM>
+__global__ __launch_bounds__(KS * 64) void mv_ksplit_kernel(const uint16_t* __restrict__ x,
+                                                            const int8_t* __restrict__ w,
+                                                            const float* __restrict__ sw,
+                                                            const uint16_t* __restrict__ bias,
+                                                            uint16_t* __restrict__ y, int N,
+                                                            MvProducer pp) {
+  constexpr int KQ = K / KS;        // k of one wave
+  constexpr int CPQ = KQ / 16;      // 16-byte weight chunks per row and wave
+  constexpr int C = KS * CPQ / 64;  // chunks per lane
+  static_assert(KQ * KS == K && KS * CPQ == 64 * C && CPQ >= 64, "whole wave loads");
+  static_assert(KS >= 4, "the RMSNorm statistic takes threads 0..255");
+  constexpr int XCH = KQ / 8;       // 8-element x chunks of the wave's k range
+  constexpr int XR = (XCH + 63) / 64;
+  constexpr bool kNorm = XM == XM_NORM || XM == XM_ADDNORM;
+  constexpr int NCH = K / 8, XRN = (NCH + 255) / 256;  // the statistic's chunks per thread
+  __shared__ __attribute__((aligned(16))) uint16_t xs[KS][KQ];
+  __shared__ float part[KS][KS];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * KS;
+  const int e0 = wave * XCH;  // the wave's first 8-element chunk
+
+  // x (the producer's inputs of the wave's range) first, then the RMSNorm
+  // statistic's chunks, the per-row operands and every weight chunk (clamped
+  // rows past N re-read row N - 1 and are never stored)
+  i32x4 xr[XR], xu[XM == XM_SWIGLU || XM == XM_ADDNORM ? XR : 1], xn[kNorm ? XR : 1];
+#pragma unroll
+  for (int q = 0; q < XR; ++q) {
+    const int e = e0 + min(lane + 64 * q, XCH - 1);
+    xr[q] = ld16(x + 8 * e);
+    if constexpr (XM == XM_SWIGLU) xu[q] = ld16(x + K + 8 * e);
+    if constexpr (XM == XM_ADDNORM) xu[q] = ld16(pp.add + 8 * e);
+    if constexpr (kNorm) xn[q] = ld16(pp.nw + 8 * e);
+  }
+  i32x4 sr[kNorm ? XRN : 1], su[XM == XM_ADDNORM ? XRN : 1];
+  if constexpr (kNorm) {
+#pragma unroll
+    for (int q = 0; q < XRN; ++q) {
+      const int e = min(min(tid, 255) + 256 * q, NCH - 1);
+      sr[q] = ld16(x + 8 * e);
+      if constexpr (XM == XM_ADDNORM) su[q] = ld16(pp.add + 8 * e);
+    }
+  }
+  const int wrow = min(n0 + min(lane, KS - 1), N - 1);
+  const float s_row = sw[wrow];
+  const float b_row = h2f(bias ? bias[wrow] : x[0]);
+  i32x4 wv[C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = lane + 64 * j;
+    const int r = c / CPQ, kc = c - r * CPQ;
+    wv[j] = ld16_nt(w + (int64_t)min(n0 + r, N - 1) * K + wave * KQ + 16 * kc);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if constexpr (XM == XM_SWIGLU) {
+#pragma unroll
+    for (int q = 0; q < XR; ++q) xr[q] = swiglu8(xr[q], xu[q]);
+  }
+  if constexpr (kNorm) {
+    // the statistic as the producer kernels take it: thread t's chunks t,
+    // t + 256, ... (threads 0..255), then the sum over waves 0..3
+    float ss = 0.0f;
+    if (tid < 256) {
+#pragma unroll
+      for (int q = 0; q < XRN; ++q) {
+        const int e = tid + 256 * q;
+        if (e < NCH) {
+          i32x4 h = sr[q];
+          if constexpr (XM == XM_ADDNORM) {
+            h = add8(h, su[q]);
+            if (blockIdx.x == 0) *reinterpret_cast<i32x4*>(pp.hsum + 8 * e) = h;
+          }
+          ss = sumsq8(h, ss);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0 && wave < 4) red[wave] = ss;
+    __syncthreads();
+    const float tot = ((red[0] + red[1]) + red[2]) + red[3];
+    const float rn = 1.0f / sqrtf(tot / (float)K + pp.eps);
+#pragma unroll
+    for (int q = 0; q < XR; ++q) {
+      i32x4 h = xr[q];
+      if constexpr (XM == XM_ADDNORM) h = add8(h, xu[q]);
+      xr[q] = norm8(h, xn[q], rn);
+    }
+  }
+  // the wave's x' range, visible to its own lanes after the fence (copies of
+  // the last chunk past the end)
+#pragma unroll
+  for (int q = 0; q < XR; ++q)
+    *reinterpret_cast<i32x4*>(&xs[wave][8 * min(lane + 64 * q, XCH - 1)]) = xr[q];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  float acc[KS];
+#pragma unroll
+  for (int r = 0; r < KS; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < C; ++j) {
+    const int c = lane + 64 * j;
+    const int r = c / CPQ, kc = c - r * CPQ;
+    const i32x4 xa = *reinterpret_cast<const i32x4*>(&xs[wave][16 * kc]);
+    const i32x4 xb = *reinterpret_cast<const i32x4*>(&xs[wave][16 * kc + 8]);
+    const float d = dot16(wv[j], xa, xb, 0.0f);
+    const int rlo = (64 * j) / CPQ, rhi = (64 * j + 63) / CPQ;  // constants once unrolled
+    acc[rlo] = acc[rlo] + (r == rlo ? d : 0.0f);
+    if (rhi != rlo && rhi < KS) acc[rhi] = acc[rhi] + (r == rhi ? d : 0.0f);
+  }
+  // the wave's partial row sums (the stream's lane tree), then the rows over
+  // the waves in wave order
+#pragma unroll
+  for (int r = 0; r < KS; ++r) acc[r] = wave_sum_dpp(acc[r]);
+  if (lane < KS) {
+    float a = acc[0];
+#pragma unroll
+    for (int r = 1; r < KS; ++r) a = lane == r ? acc[r] : a;
+    part[wave][lane] = a;
+  }
+  __syncthreads();
+  if (wave == 0 && lane < KS && n0 + lane < N) {
+    float a = part[0][lane];
+#pragma unroll
+    for (int v = 1; v < KS; ++v) a = a + part[v][lane];
+    float o = s_row * a;
+    if (bias) o = o + b_row;
+    y[n0 + lane] = f2h(o);
+  }
+}
+
 namespace {
 
 template <int R, int C, bool PG, int XM>
@@ -295,6 +449,49 @@ hipError_t pick_stream(int K, const uint16_t* x, const int8_t* w, const float* s
 #undef CIDER_MV
 }
 
+// KS of the k-split MV for K (0: not taken): 4 or 5 waves, whichever leaves
+// fewer workgroup slots idle in the last round over the CUs (5 needs
+// K % 80 == 0).
+int ksplit_ways(int N, int K) {
+  if (K < 10240 || K > 16384 || K % 1024 != 0) return 0;
+  const int cus = num_cus();
+  auto idle = [&](int ks) {
+    const int wgs = (N + ks - 1) / ks, rounds = (wgs + cus - 1) / cus;
+    return (double)(rounds * cus - wgs) / wgs;
+  };
+  return (K % 80 == 0 && idle(5) < idle(4)) ? 5 : 4;
+}
+
+template <int K, int XM>
+hipError_t run_ksplit(int ks, const uint16_t* x, const int8_t* w, const float* sw,
+                      const uint16_t* bias, uint16_t* y, int N, const MvProducer& pp,
+                      hipStream_t s) {
+  if constexpr (K % 80 == 0) {
+    if (ks == 5) {
+      mv_ksplit_kernel<K, 5, XM><<<(N + 4) / 5, 320, 0, s>>>(x, w, sw, bias, y, N, pp);
+      return hipGetLastError();
+    }
+  }
+  mv_ksplit_kernel<K, 4, XM><<<(N + 3) / 4, 256, 0, s>>>(x, w, sw, bias, y, N, pp);
+  return hipGetLastError();
+}
+
+template <int XM>
+hipError_t launch_ksplit(int ks, const uint16_t* x, const int8_t* w, const float* sw,
+                         const uint16_t* bias, uint16_t* y, int N, int K, const MvProducer& pp,
+                         hipStream_t s) {
+  switch (K) {
+    case 10240: return run_ksplit<10240, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 11264: return run_ksplit<11264, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 12288: return run_ksplit<12288, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 13312: return run_ksplit<13312, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 14336: return run_ksplit<14336, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 15360: return run_ksplit<15360, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    case 16384: return run_ksplit<16384, XM>(ks, x, w, sw, bias, y, N, pp, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
 bool stream_k(int K) {
   if (K < 1024 || K > 16384 || K % 256 != 0) return false;
   const int m = K / 256;
@@ -316,6 +513,17 @@ hipError_t launch_mv_stream(int xm, const uint16_t* x, const int8_t* w, const fl
   if (gs > 0) {
     if (xm != XM_PLAIN) return hipErrorInvalidValue;
     return pick_stream<true, XM_PLAIN>(K, x, w, sw, bias, y, N, gs, pp, s);
+  }
+  // the k-split MV for every producer mode alike, so a fused launch still
+  // equals the producer launch followed by the plain MV bit for bit
+  if (const int ks = ksplit_ways(N, K)) {
+    switch (xm) {
+      case XM_PLAIN: return launch_ksplit<XM_PLAIN>(ks, x, w, sw, bias, y, N, K, pp, s);
+      case XM_NORM: return launch_ksplit<XM_NORM>(ks, x, w, sw, bias, y, N, K, pp, s);
+      case XM_ADDNORM: return launch_ksplit<XM_ADDNORM>(ks, x, w, sw, bias, y, N, K, pp, s);
+      case XM_SWIGLU: return launch_ksplit<XM_SWIGLU>(ks, x, w, sw, bias, y, N, K, pp, s);
+      default: return hipErrorInvalidValue;
+    }
   }
   switch (xm) {
     case XM_PLAIN: return pick_stream<false, XM_PLAIN>(K, x, w, sw, bias, y, N, 0, pp, s);

@@ -294,7 +294,9 @@ def _pc_linear(N, K, seed):
 
 @pytest.mark.parametrize("N,K,with_add", [(6144, 4096, True), (24576, 4096, True),
                                           (4096, 2048, False), (33, 16384, True),
-                                          (40, 256, False), (3000, 2560, True)])
+                                          (40, 256, False), (3000, 2560, True),
+                                          (2560, 10240, False), (2560, 10240, True),
+                                          (4096, 12288, True)])
 def test_rmsnorm_mv_equals_two_launches(N, K, with_add):
     g = torch.Generator(device="cuda").manual_seed(N + K)
     x = (torch.randn(1, K, device="cuda", generator=g) * 3).half()
@@ -309,7 +311,8 @@ def test_rmsnorm_mv_equals_two_launches(N, K, with_add):
     assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), f"rmsnorm_mv {N}x{K}"
 
 
-@pytest.mark.parametrize("N,I", [(4096, 12288), (2048, 6144), (33, 512), (4096, 16384)])
+@pytest.mark.parametrize("N,I", [(4096, 12288), (2048, 6144), (33, 512), (4096, 16384),
+                                 (2560, 10240), (7, 15360)])
 def test_swiglu_mv_equals_two_launches(N, I):
     g = torch.Generator(device="cuda").manual_seed(N + I)
     gu = (torch.randn(1, 2 * I, device="cuda", generator=g) * 3).half()

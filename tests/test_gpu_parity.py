@@ -213,12 +213,16 @@ def test_w4_and_pergroup_midpoint_shapes(M, N, K):
 
 # K % 256 == 0 with 1024 <= K <= 16384 (in the streaming MV's table) runs the
 # streaming MV: R rows per wave, 16-byte chunks, v_dot2 products; N=9 and
-# N=130 leave the last wave partly past N.  K=256 / 8 / 300 / 16640 run the
-# lane-order MV (bounds-checked tail for K=300 and K=8).
+# N=130 leave the last wave partly past N.  Of those, K from 10240 to 16384
+# with K % 1024 == 0 runs the k-split MV (KS = 4 or 5 waves share each row's
+# k range; N=9, 3 and 1001 leave the last workgroup partly past N, N=2560
+# takes KS = 5).  K=256 / 8 / 300 / 16640 run the lane-order MV
+# (bounds-checked tail for K=300 and K=8).
 @pytest.mark.parametrize("N,K", [(40, 256), (130, 1024), (10240, 2560), (2560, 10240),
                                  (100, 300), (7, 8), (8, 1280), (9, 1536), (100, 16384),
                                  (33, 16640), (4096, 12288), (12288, 4096), (1000, 3584),
-                                 (50, 7680), (70, 3840)])
+                                 (50, 7680), (70, 3840), (9, 11264), (3, 10240),
+                                 (1001, 13312), (64, 14336), (255, 15360)])
 def test_perchannel_mv(N, K):
     x, w, sw, b = synth_pc(1, N, K, 500 + N + K)
     y = H(C.perchannel_linear(T(x), T(w), T(sw), T(b)))
