@@ -69,11 +69,34 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
 
   float ss = 0.0f, amax = 0.0f;
   if constexpr (NV > 0) {
-    i32x4 v[NV];
+    // up to 12 vectors per lane every load first, unconditional (clamped: a
+    // lane past the row re-reads its last vector): a load under a lane mask
+    // made the compiler wait for each before the next.  hsum may alias x:
+    // each element's h is stored after all of the row's x loads, by the lane
+    // that loaded it.  From 16 on the three register copies would not fit.
+    constexpr bool HOIST = NV <= 12;
+    i32x4 v[NV], av[HOIST && ADD ? NV : 1], wv[HOIST ? NV : 1];
+    if constexpr (HOIST) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = min(lane + i * kWave, nvec - 1);
+        v[i] = ld16(xr + 8 * e);
+        if constexpr (ADD) av[i] = ld16(add + row * K + 8 * e);
+        wv[i] = ld16(w + 8 * e);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + i * kWave;
-      v[i] = e < nvec ? first_h(e) : i32x4{0, 0, 0, 0};
+      if constexpr (HOIST) {
+        if constexpr (ADD) {
+          v[i] = add8(v[i], av[i]);
+          if (e < nvec) *reinterpret_cast<i32x4*>(hsum + row * K + 8 * e) = v[i];
+        }
+        if (e >= nvec) v[i] = i32x4{0, 0, 0, 0};
+      } else {
+        v[i] = e < nvec ? first_h(e) : i32x4{0, 0, 0, 0};
+      }
       ss = sumsq8(v[i], ss);
     }
     ss = wave_sum(ss);
@@ -82,7 +105,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
     for (int i = 0; i < NV; ++i) {
       const int e = lane + i * kWave;
       if (e < nvec) {
-        v[i] = norm8(v[i], ld16(w + 8 * e), r);
+        if constexpr (HOIST)
+          v[i] = norm8(v[i], wv[i], r);
+        else
+          v[i] = norm8(v[i], ld16(w + 8 * e), r);
         if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * K + 8 * e) = v[i];
         amax = absmax8(v[i], amax);
       }
@@ -134,12 +160,28 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(
   const uint16_t* u = g + I;
   float amax = 0.0f;
   if constexpr (NV > 0) {
-    i32x4 v[NV];
+    // up to 24 vectors per lane every load first, unconditional (clamped: a
+    // lane past the row re-reads its last vector): a load under a lane mask
+    // made the compiler wait for each before the next (2048 x 12288: 47 ->
+    // 24 us).  At 32 the two register copies would leave one wave per SIMD.
+    constexpr bool HOIST = NV <= 24;
+    i32x4 v[NV], uv[HOIST ? NV : 1];
+    if constexpr (HOIST) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int e = min(lane + i * kWave, nvec - 1);
+        v[i] = ld16(g + 8 * e);
+        uv[i] = ld16(u + 8 * e);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int e = lane + i * kWave;
       if (e < nvec) {
-        v[i] = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
+        if constexpr (HOIST)
+          v[i] = swiglu8(v[i], uv[i]);
+        else
+          v[i] = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
         if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v[i];
         amax = absmax8(v[i], amax);
       }
@@ -286,9 +328,22 @@ __global__ __launch_bounds__(256) void silu_mul_ew_kernel(const uint16_t* __rest
 // ---------------------------------------------------------------------------
 // per-head q/k RMSNorm + RoPE + KV-cache write (head_dim 128)
 // ---------------------------------------------------------------------------
-// One wave per (token, head) of the fused projection row [q heads | k heads |
-// v heads]; lane l holds elements l and l + 64, which is exactly the pair the
-// rotate-half RoPE mixes.
+// Eight lanes per (token, head) of the fused projection row [q heads | k
+// heads | v heads], eight heads per wave: lane j of a head holds elements
+// [8j, 8j + 8) and [64 + 8j, 64 + 8j + 8), which are the pairs the
+// rotate-half RoPE mixes, so every access is 16 bytes.  The head's sum of
+// squares: each lane's 16 squares in order, then pairs, quads and the 8-lane
+// group by DPP moves.  Per element: n = h(w * h(x * r)), out = h(h(n * cos) +
+// h(-n' * sin)) for the first half (n' its partner) and h(h(n * cos) +
+// h(n' * sin)) for the second.  (One wave per head with 2-byte lanes ran the
+// 2048-token prefill's 2048 x 48 heads in 29 us.)
+__device__ __forceinline__ float group8_sum(float v) {
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppXor1>(__builtin_bit_cast(int32_t, v)));
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppXor2>(__builtin_bit_cast(int32_t, v)));
+  v = v + __builtin_bit_cast(float, dpp_mov<kDppMirror8>(__builtin_bit_cast(int32_t, v)));
+  return v;
+}
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
     const uint16_t* __restrict__ kw, float eps, const uint16_t* __restrict__ cos_t,
@@ -296,58 +351,77 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(
     const int64_t* __restrict__ slot, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int L, int H, int KV, int64_t T) {
   constexpr int D = 128;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, j = lane & 7;
   const int heads = H + 2 * KV;
+  const int groups = (heads + 7) / 8;  // waves per token
   const int64_t gw = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int64_t t = gw / heads;
-  const int hh = (int)(gw % heads);
-  if (t >= L) return;
+  const int64_t t = gw / groups;
+  if (t >= L) return;  // uniform per wave
+  const int hh = (int)(gw % groups) * 8 + (lane >> 3);
+  if (hh >= heads) return;
   const uint16_t* src = qkv + (t * heads + hh) * D;
-  const uint16_t x0 = src[lane], x1 = src[lane + 64];
+  const i32x4 x0 = ld16(src + 8 * j), x1 = ld16(src + 64 + 8 * j);
+  const int64_t p = slot[t];
   if (hh >= H + KV) {  // v: copy into the cache
-    const int64_t p = slot[t];
     if (p < 0 || p >= T) return;
     uint16_t* dst = vc + ((int64_t)(hh - H - KV) * T + p) * D;
-    dst[lane] = x0;
-    dst[lane + 64] = x1;
+    *reinterpret_cast<i32x4*>(dst + 8 * j) = x0;
+    *reinterpret_cast<i32x4*>(dst + 64 + 8 * j) = x1;
     return;
   }
   const int64_t rr = rope_row[t];
-  if (rr < 0 || rr >= P) {
+  const bool has_row = rr >= 0 && rr < P;
+  const uint16_t* wn = hh < H ? qw : kw;
+  const int64_t rrc = has_row ? rr : 0;
+  const i32x4 w0 = ld16(wn + 8 * j), w1 = ld16(wn + 64 + 8 * j);
+  const i32x4 c0 = ld16(cos_t + rrc * D + 8 * j), c1 = ld16(cos_t + rrc * D + 64 + 8 * j);
+  const i32x4 s0 = ld16(sin_t + rrc * D + 8 * j), s1 = ld16(sin_t + rrc * D + 64 + 8 * j);
+  float ss = 0.0f;
+  ss = sumsq8(x0, ss);
+  ss = sumsq8(x1, ss);
+  ss = group8_sum(ss);  // every lane of the head's group
+  if (!has_row) {
     // No RoPE row: the k cache is left alone, and the q heads get a quiet
     // NaN, so a caller that feeds them on sees the error instead of stale
     // memory.
     if (hh < H) {
       uint16_t* dst = q_out + (t * H + hh) * D;
-      dst[lane] = 0x7E00;
-      dst[lane + 64] = 0x7E00;
+      const i32x4 nan4 = {0x7E007E00, 0x7E007E00, 0x7E007E00, 0x7E007E00};
+      *reinterpret_cast<i32x4*>(dst + 8 * j) = nan4;
+      *reinterpret_cast<i32x4*>(dst + 64 + 8 * j) = nan4;
     }
     return;
   }
-  const float a = h2f(x0), b = h2f(x1);
-  float ss = a * a;
-  ss = ss + b * b;
-  ss = wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / (float)D + eps);
-  const uint16_t* wn = hh < H ? qw : kw;
-  const float n0 = h2f(norm1(x0, wn[lane], r)), n1 = h2f(norm1(x1, wn[lane + 64], r));
-  const uint16_t* cr = cos_t + rr * D;
-  const uint16_t* sr = sin_t + rr * D;
-  // out = x * cos + rotate_half(x) * sin, rotate_half(x) = [-x[64:], x[:64]]
-  const uint16_t o0 = f2h(h2f(f2h(n0 * h2f(cr[lane]))) + h2f(f2h(-(n1 * h2f(sr[lane])))));
-  const uint16_t o1 =
-      f2h(h2f(f2h(n1 * h2f(cr[lane + 64]))) + h2f(f2h(n0 * h2f(sr[lane + 64]))));
-  if (hh < H) {
-    uint16_t* dst = q_out + (t * H + hh) * D;
-    dst[lane] = o0;
-    dst[lane + 64] = o1;
-  } else {
-    const int64_t p = slot[t];
-    if (p < 0 || p >= T) return;
-    uint16_t* dst = kc + ((int64_t)(hh - H) * T + p) * D;
-    dst[lane] = o0;
-    dst[lane + 64] = o1;
+  const i32x4 n0 = norm8(x0, w0, r), n1 = norm8(x1, w1, r);
+  i32x4 o0, o1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t lo[2], hi[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float a = h2f(h ? hi16(n0[e]) : lo16(n0[e]));
+      const float b = h2f(h ? hi16(n1[e]) : lo16(n1[e]));
+      const float ca = h2f(h ? hi16(c0[e]) : lo16(c0[e]));
+      const float sa = h2f(h ? hi16(s0[e]) : lo16(s0[e]));
+      const float cb = h2f(h ? hi16(c1[e]) : lo16(c1[e]));
+      const float sb = h2f(h ? hi16(s1[e]) : lo16(s1[e]));
+      // out = x * cos + rotate_half(x) * sin, rotate_half(x) = [-x[64:], x[:64]]
+      lo[h] = f2h(h2f(f2h(a * ca)) + h2f(f2h(-(b * sa))));
+      hi[h] = f2h(h2f(f2h(b * cb)) + h2f(f2h(a * sb)));
+    }
+    o0[e] = pack2(lo[0], lo[1]);
+    o1[e] = pack2(hi[0], hi[1]);
   }
+  uint16_t* dst;
+  if (hh < H) {
+    dst = q_out + (t * H + hh) * D;
+  } else {
+    if (p < 0 || p >= T) return;
+    dst = kc + ((int64_t)(hh - H) * T + p) * D;
+  }
+  *reinterpret_cast<i32x4*>(dst + 8 * j) = o0;
+  *reinterpret_cast<i32x4*>(dst + 64 + 8 * j) = o1;
 }
 
 template <template <int> class F, typename... A>
@@ -357,7 +431,9 @@ hipError_t by_nv(int nvec, A... args) {
   if (per_lane <= 2) return F<2>::run(args...);
   if (per_lane <= 4) return F<4>::run(args...);
   if (per_lane <= 8) return F<8>::run(args...);
+  if (per_lane <= 12) return F<12>::run(args...);
   if (per_lane <= 16) return F<16>::run(args...);
+  if (per_lane <= 24) return F<24>::run(args...);
   if (per_lane <= 32) return F<32>::run(args...);
   return F<0>::run(args...);
 }
@@ -482,7 +558,7 @@ hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const ui
                                const int64_t* rope_row, const int64_t* slot, uint16_t* q_out,
                                uint16_t* kc, uint16_t* vc, int L, int H, int KV, int64_t T,
                                hipStream_t s) {
-  const int64_t waves = (int64_t)L * (H + 2 * KV);
+  const int64_t waves = (int64_t)L * ((H + 2 * KV + 7) / 8);
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
   qk_norm_rope_kernel<<<grid, block, 0, s>>>(qkv, qw, kw, eps, cos_t, sin_t, P, rope_row, slot,
                                              q_out, kc, vc, L, H, KV, T);

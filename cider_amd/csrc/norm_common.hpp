@@ -54,9 +54,20 @@ __device__ __forceinline__ i32x4 norm8(i32x4 v, i32x4 w, float r) {
   return o;
 }
 
+// SwiGLU of one element: h(f32(h(silu(g))) * f32(u)), silu(g) = g / (1 + e^-g)
+// in fp32 from the hardware exp2 (v_exp_f32, 2^x) and reciprocal
+// (v_rcp_f32), each within about one ulp of binary32: the fp32 silu lands
+// within a few ulps of the exact quotient, so its fp16 rounding h(silu(g))
+// is the exact one or a neighbour only for values within those few ulps of
+// a rounding boundary.  (The correctly rounded expf and division took about
+// 30 VALU operations per element and bound the SwiGLU kernels.)  Infinities
+// map as in the exact expression: g = -inf gives NaN, +inf gives +inf, and
+// e^-g overflowing to +inf gives a signed zero.
 __device__ __forceinline__ uint16_t swiglu1(uint16_t g, uint16_t u) {
   const float gf = h2f(g);
-  const uint16_t a = f2h(gf / (1.0f + expf(-gf)));
+  constexpr float kLog2e = 1.4426950408889634f;  // 1 / ln 2
+  const float e = __builtin_amdgcn_exp2f(-gf * kLog2e);
+  const uint16_t a = f2h(gf * __builtin_amdgcn_rcpf(1.0f + e));
   return f2h(h2f(a) * h2f(u));
 }
 
