@@ -33,13 +33,15 @@ __global__ __launch_bounds__(256) void quantize_vec_kernel(
   const int nvec = K >> 3;
   float amax = 0.0f;
   if constexpr (NV > 0) {
+    // every load first, unconditional (clamped: a lane past the row re-reads
+    // its last vector, which leaves the max unchanged), as a load under a
+    // lane mask makes the compiler wait for each before the next: M=4096
+    // K=2560 5.99 -> 5.79 us, M=2048 K=4096 5.37 -> 4.98 us (M=8192 level)
     i32x4 v[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + i * kWave;
-      v[i] = e < nvec ? ld16(xr + 8 * e) : i32x4{0, 0, 0, 0};
-      amax = absmax8(v[i], amax);
-    }
+    for (int i = 0; i < NV; ++i) v[i] = ld16(xr + 8 * min(lane + i * kWave, nvec - 1));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) amax = absmax8(v[i], amax);
     amax = wave_max(amax);
     const float s = row_scale(amax);
     const float inv = 1.0f / s;
