@@ -1,7 +1,7 @@
 """Producers of the W8A8 linear's input, with the per-token quantization fused
-in, and single-query decode attention (HIP kernels behind the C ABI of
+in, prefill-chunk and single-query decode attention (HIP kernels behind the C ABI of
 ``include/cider_hip.h``: ``cider_rmsnorm_quantize``, ``cider_silu_mul_quantize``,
-``cider_qk_norm_rope``, ``cider_attn_decode``).
+``cider_qk_norm_rope``, ``cider_attn_decode``, ``cider_attn_prefill``).
 
 The reference library quantizes a linear's fp16 input inside the linear
 (``cider/kernels/w8a8_quantize.metal:17-87``); its models produce that input
@@ -166,6 +166,36 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         _lib.check(lib.cider_attn_decode(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(n_valid),
                                          float(scale), _ptr(ws), ws.numel(), _ptr(out), H, KV, d,
                                          T, _stream_ptr(dev, stream)))
+    return out
+
+
+def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, n: int,
+                 scale: float, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Causal grouped-query attention of a prefill chunk: q [c, H, 128] holds
+    the queries of cache slots n - c .. n - 1, whose keys and values are
+    already in k_cache / v_cache [KV, T, 128]; query i attends slots
+    0 .. n - c + i.  Returns fp16 [c, H * 128] (the reference hands this to
+    MLX's fused SDPA, ``cider/fused_hybrid.py:179-196``)."""
+    fn = "attn_prefill"
+    dev = _require_gpu(fn, q, k_cache, v_cache, out)
+    _f16(fn, "q", q)
+    _f16(fn, "k_cache", k_cache)
+    _f16(fn, "v_cache", v_cache)
+    if q.dim() != 3:
+        raise ValueError(f"{fn}: q must be [c, H, D]")
+    c, H, D = q.shape
+    KV, T, d = k_cache.shape
+    if tuple(v_cache.shape) != (KV, T, d) or d != D:
+        raise ValueError(f"{fn}: the caches must be [KV, T, {D}]")
+    lib = _lib.load()
+    with _on_stream(dev, stream):
+        if out is None:
+            out = torch.empty(c, H * D, dtype=torch.float16, device=dev)
+        elif out.dtype != torch.float16 or not out.is_contiguous() or out.numel() != c * H * D:
+            raise ValueError(f"{fn}: out must be a contiguous float16 tensor of c x H x {D}")
+        _lib.check(lib.cider_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), float(scale),
+                                          _ptr(out), c, int(n), H, KV, D, T,
+                                          _stream_ptr(dev, stream)))
     return out
 
 

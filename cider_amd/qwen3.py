@@ -21,9 +21,9 @@ RMSNorm before q/k/v and gate/up, and the SwiGLU before down_proj, end in the
 per-token quantization, so prefill hands (q, scale_a) straight to the int8
 GEMM; the per-head q/k RMSNorm and RoPE write k and v into the cache in the
 same kernel; decode attention is a single-query split-K kernel over the
-cache; prefill attention is PyTorch's fused causal SDPA over the cache
-(grouped query heads, lower-right causal alignment for a chunk that follows
-earlier cache slots).  ``fused=False`` runs those steps as plain PyTorch ops
+cache; prefill attention is this library's causal flash-attention kernel over
+the cache (grouped query heads; a chunk that follows earlier cache slots
+attends them all).  ``fused=False`` runs those steps as plain PyTorch ops
 instead (the A/B reference; its attention is batched matmuls with the 4 query
 heads of each KV head grouped along rows).  The embedding lookup and the fp16
 lm_head are PyTorch on the GPU in both modes.  Both caches are [KV, T, 128]
@@ -43,8 +43,6 @@ from typing import Optional
 
 import torch
 import torch.nn.functional as F
-
-from torch.nn.attention.bias import causal_lower_right
 
 from . import fused as FK
 from .nn import CiderLinear
@@ -183,20 +181,6 @@ class Qwen3Layer(torch.nn.Module):
         x = x + self.o(self._attend(q, k_cache, v_cache, mask))
         return x + self._mlp(x)
 
-    def _attend_sdpa(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
-        """Causal attention of the chunk q [c, heads, d] (cache slots n - c ..
-        n - 1) over k, v [kv, n, d] with PyTorch's fused SDPA (grouped heads,
-        lower-right causal alignment when the chunk follows earlier slots)."""
-        c, n = q.shape[0], k.shape[1]
-        qq = q.permute(1, 0, 2).unsqueeze(0)
-        kk, vv = k.unsqueeze(0), v.unsqueeze(0)
-        if c == n:
-            o = F.scaled_dot_product_attention(qq, kk, vv, is_causal=True, enable_gqa=True)
-        else:
-            o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=causal_lower_right(c, n),
-                                               enable_gqa=True)
-        return o[0].permute(1, 0, 2).reshape(c, self.cfg.num_heads * self.cfg.head_dim)
-
     # ---- fused producers (HIP kernels) -------------------------------------
     # The residual stream is carried as (x, pending): the layer's true input is
     # h(x + pending); the add happens inside the next RMSNorm kernel, which
@@ -215,7 +199,7 @@ class Qwen3Layer(torch.nn.Module):
         qkv = self.qkv.forward_quantized(a.q, a.scale_a)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
                             rope_row, slot, k_cache, v_cache, c.num_heads, c.num_kv_heads)
-        attn = self._attend_sdpa(q, k_cache[:, :n, :], v_cache[:, :n, :])
+        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim))
         b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
         gu = self.gate_up.forward_quantized(b.q, b.scale_a)
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)

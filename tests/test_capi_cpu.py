@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 20, syms
+    assert len(syms) == 21, syms
 
 
 @pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
@@ -210,6 +210,18 @@ def test_producer_and_attention_validation_without_gpu(lib):
     assert lib.cider_attn_decode(p, p, p, p, 0.1, p, 16, p, 32, 8, 128, 4096, n) == E
     assert "workspace" in _err(lib)
     assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 32, 8, 64, 4096, n) == E
+    # prefill attention: head_dim, grouping, 1 <= c <= n <= T, pointers, alignment
+    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 32, 32, 8, 64, 64, n) == E
+    assert "head_dim" in _err(lib)
+    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 32, 30, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 33, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 0, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 65, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(n, p, p, 0.1, p, 16, 32, 32, 8, 128, 64, n) == E
+    assert "q is NULL" in _err(lib)
+    assert lib.cider_attn_prefill(p, p, p, 0.1, ctypes.c_void_p(0x1008), 16, 32, 32, 8, 128,
+                                  64, n) == E
+    assert "aligned" in _err(lib)
     # empty problems succeed
     assert lib.cider_rmsnorm_quantize(n, n, n, n, 1e-6, p, n, n, 0, 16, n) == _lib.CIDER_OK
     assert lib.cider_qk_norm_rope(*(args[:12] + [0] + args[13:])) == _lib.CIDER_OK

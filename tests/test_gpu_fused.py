@@ -1,6 +1,6 @@
 """GPU parity of the producer kernels (RMSNorm / SwiGLU with the per-token
 quantization fused in, per-head q/k norm + RoPE + cache write) and of the
-single-query decode attention.
+single-query decode and prefill-chunk attention.
 
 Bars:
   * quantization: q and scale_a bit-identical to the oracle's
@@ -13,8 +13,11 @@ Bars:
     chain's first fp16 intermediate by one step: the output must equal the
     chain's for that intermediate or a neighbour (RoPE: within the error bound
     that step propagates to), and almost all elements must be identical;
-  * attention: float64 softmax attention on the CPU, within fp16 output
-    rounding plus fp32 accumulation error (rtol 4e-3, atol 2e-3).
+  * decode attention: float64 softmax attention on the CPU, within fp16
+    output rounding plus fp32 accumulation error (rtol 4e-3, atol 2e-3);
+  * prefill attention: float64 causal softmax attention, within 3e-3 + 5e-3
+    |ref| (the kernel rounds the probabilities to fp16 for the P.V product, as
+    fused SDPA kernels do; PyTorch's SDPA lands at the same error).
 """
 
 import math
@@ -279,6 +282,72 @@ def test_attn_decode_graph_replays_follow_device_length():
         gr.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"n={n}"
+
+
+def _prefill_ref(q, kc, vc, c, n, scale):
+    """float64 causal attention of the chunk q [c, H, D] (cache slots
+    n - c .. n - 1) over kc / vc [KV, >= n, D], on the GPU in float64."""
+    H, D = q.shape[1], q.shape[2]
+    KV = kc.shape[0]
+    G = H // KV
+    allowed = torch.ones(c, n, dtype=torch.bool, device=q.device).tril(diagonal=n - c)
+    out = torch.empty(c, H, D, dtype=torch.float64, device=q.device)
+    for h in range(H):
+        j = h // G
+        k = kc[j, :n].double()
+        s = scale * (q[:, h].double() @ k.T.contiguous())
+        s = s.masked_fill(~allowed, float("-inf"))
+        out[:, h] = torch.softmax(s, dim=-1) @ vc[j, :n].double()
+    return out
+
+
+# (c, n, H, KV, T, q scale): the Qwen3-8B 2048-token prefill, Qwen3-VL chunks
+# after earlier slots, ragged lengths and capacities (the last stage past n),
+# one query, every grouping 1..8, KV not a multiple of 8 (the plain item
+# order), and peaked softmaxes (large logits exercise the running-max slack).
+PREFILL_CASES = [
+    (2048, 2048, 32, 8, 2048, 1.0), (512, 2048, 16, 8, 2304, 1.0), (777, 777, 32, 8, 800, 1.0),
+    (100, 1000, 16, 8, 1024, 1.0), (1, 37, 32, 8, 64, 1.0), (130, 130, 8, 8, 136, 1.0),
+    (64, 200, 64, 8, 256, 1.0), (300, 300, 12, 4, 320, 1.0), (257, 513, 5, 1, 520, 1.0),
+    (640, 1280, 32, 8, 1280, 6.0), (300, 1500, 16, 8, 1536, 10.0), (129, 129, 16, 8, 4096, 1.0),
+]
+
+
+@pytest.mark.parametrize("c,n,H,KV,T,qs", PREFILL_CASES)
+def test_attn_prefill(c, n, H, KV, T, qs):
+    D = 128
+    g = torch.Generator(device="cuda").manual_seed(c * 7 + n + H)
+    q = (torch.randn(c, H, D, device="cuda", generator=g) * qs).half()
+    kc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    # slots >= n hold garbage that must not leak into the result
+    kc[:, n:, :] = float("nan")
+    vc[:, n:, :] = float("nan")
+    scale = 1.0 / math.sqrt(D)
+    out = F.attn_prefill(q, kc, vc, n, scale)
+    torch.cuda.synchronize()
+    exp = _prefill_ref(q, kc, vc, c, n, scale)
+    got = out.double().reshape(c, H, D)
+    assert torch.isfinite(got).all()
+    err = (got - exp).abs()
+    tol = 3e-3 + 5e-3 * exp.abs()
+    assert bool((err <= tol).all()), f"max err {err.max().item():.3e}"
+
+
+def test_attn_prefill_chunks_match_one_shot():
+    """Chunks of 512 after earlier slots (the Qwen3-VL prefill) give what one
+    launch over the whole prompt gives, within the same bar."""
+    c, H, KV, D, T = 1500, 16, 8, 128, 1536
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randn(c, H, D, device="cuda", generator=g).half()
+    kc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    one = F.attn_prefill(q, kc, vc, c, 0.09).double()
+    parts = [F.attn_prefill(q[s:s + 512].contiguous(), kc, vc, min(s + 512, c), 0.09).double()
+             for s in range(0, c, 512)]
+    torch.cuda.synchronize()
+    err = (torch.cat(parts) - one).abs()
+    assert bool((err <= 3e-3 + 5e-3 * one.abs()).all()), f"max err {err.max().item():.3e}"
 
 
 # Decode producers run inside the consuming M == 1 linear: bit-identical to
