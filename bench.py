@@ -83,6 +83,11 @@ def parse():
                     help="instead of the default line, print one JSON line for configs[4]: "
                          "Qwen3-VL-2B-shaped W8A8 text decoder, chunked prefill (512) of "
                          "1334 / 2393 / 3455-token multimodal prompts, then graph decode")
+    ap.add_argument("--attn", action="store_true",
+                    help="instead of the default line, print one JSON line for the prefill "
+                         "attention kernel (cider_attn_prefill) at the configs[3] shape "
+                         "(2048 queries, 32 / 8 heads) and a configs[4] chunk (512 queries "
+                         "after 1536 cached, 16 / 8 heads), with PyTorch's SDPA beside it")
     ap.add_argument("--torch-producers", action="store_true",
                     help="with --qwen3: run RMSNorm, SwiGLU, q/k norm + RoPE and decode "
                          "attention as PyTorch ops instead of the fused HIP kernels (A/B)")
@@ -137,6 +142,9 @@ def main():
         return
     if args.qwen3vl:
         bench_qwen3vl(torch, args, dev)
+        return
+    if args.attn:
+        bench_attn(torch, args, dev)
         return
     if args.only_decode:
         stream = torch.cuda.current_stream(dev)
@@ -801,6 +809,66 @@ def measure_qwen3(torch, args, dev, torch_producers=False):
     del g, m, logits
     torch.cuda.empty_cache()
     return prefill_ms, decode_ms, distinct, build_s, cfg
+
+
+def bench_attn(torch, args, dev):
+    """--attn: the causal prefill attention kernel per launch (HIP events on the
+    launch stream), against the 2.5 PFLOP/s dense fp16 MFMA peak, with
+    PyTorch's fused SDPA at the same shapes (the path the models used before)."""
+    import math
+
+    import torch.nn.functional as TF
+    from torch.nn.attention.bias import causal_lower_right
+
+    from cider_amd import fused as FK
+    D, reps = 128, 20
+    stream = torch.cuda.current_stream(dev)
+    cases = []
+    for name, c, n, H, KV in (("configs[3] Qwen3-8B prefill, 2048 tokens", 2048, 2048, 32, 8),
+                              ("configs[4] Qwen3-VL chunk of 512 after 1536 cached", 512, 2048,
+                               16, 8)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(args.seed + c + n)
+        q = torch.randn(c, H, D, device=dev, generator=g).half()
+        kc = torch.randn(KV, n, D, device=dev, generator=g).half()
+        vc = torch.randn(KV, n, D, device=dev, generator=g).half()
+        scale = 1.0 / math.sqrt(D)
+        out = torch.empty(c, H * D, dtype=torch.float16, device=dev)
+        qq, kk, vv = q.permute(1, 0, 2).unsqueeze(0), kc.unsqueeze(0), vc.unsqueeze(0)
+        mask = None if c == n else causal_lower_right(c, n)
+
+        def ours():
+            FK.attn_prefill(q, kc, vc, n, scale, out=out)
+
+        def sdpa():
+            if mask is None:
+                return TF.scaled_dot_product_attention(qq, kk, vv, is_causal=True, enable_gqa=True)
+            return TF.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask, enable_gqa=True)
+
+        times = {}
+        for key, fn in (("kernel", ours), ("sdpa", sdpa)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            times[key] = e0.elapsed_time(e1) / reps * 1e3  # us per launch
+        # causal flops: 2 products of 2 D flops per (query, allowed key) pair
+        flops = 4.0 * H * D * (c * (n - c) + c * (c + 1) / 2)
+        tf = flops / times["kernel"] / 1e6
+        cases.append({"case": name, "c": c, "n": n, "heads": H, "kv_heads": KV,
+                      "kernel_us": round(times["kernel"], 2), "tflops": round(tf, 1),
+                      "frac_fp16_peak": round(tf / 2500.0, 4),
+                      "sdpa_us": round(times["sdpa"], 2),
+                      "speedup_vs_sdpa": round(times["sdpa"] / times["kernel"], 2)})
+    print(json.dumps({"metric": "causal prefill attention (cider_attn_prefill) per launch",
+                      "unit": "us", "higher_is_better": False, "dtype": "fp16 (fp32 softmax)",
+                      "data": "synthetic N(0,1) q/k/v", "peak_tflops_fp16_dense": 2500.0,
+                      "cases": cases}), flush=True)
 
 
 def qwen3_summary(torch, args, dev):
