@@ -820,6 +820,7 @@ def bench_attn(torch, args, dev):
     import torch.nn.functional as TF
     from torch.nn.attention.bias import causal_lower_right
 
+    from cider_amd import _lib
     from cider_amd import fused as FK
     D, reps = 128, 20
     stream = torch.cuda.current_stream(dev)
@@ -834,11 +835,12 @@ def bench_attn(torch, args, dev):
         vc = torch.randn(KV, n, D, device=dev, generator=g).half()
         scale = 1.0 / math.sqrt(D)
         out = torch.empty(c, H * D, dtype=torch.float16, device=dev)
+        ws = FK.attn_prefill_workspace(c, n, H, dev)
         qq, kk, vv = q.permute(1, 0, 2).unsqueeze(0), kc.unsqueeze(0), vc.unsqueeze(0)
         mask = None if c == n else causal_lower_right(c, n)
 
         def ours():
-            FK.attn_prefill(q, kc, vc, n, scale, out=out)
+            FK.attn_prefill(q, kc, vc, n, scale, out=out, ws=ws)
 
         def sdpa():
             if mask is None:
@@ -861,6 +863,8 @@ def bench_attn(torch, args, dev):
         flops = 4.0 * H * D * (c * (n - c) + c * (c + 1) / 2)
         tf = flops / times["kernel"] / 1e6
         cases.append({"case": name, "c": c, "n": n, "heads": H, "kv_heads": KV,
+                      "key_parts": _lib.load().cider_attn_prefill_workspace_bytes(c, n, H)
+                      // max(1, c * H * 130 * 4) or 1,
                       "kernel_us": round(times["kernel"], 2), "tflops": round(tf, 1),
                       "frac_fp16_peak": round(tf / 2500.0, 4),
                       "sdpa_us": round(times["sdpa"], 2),

@@ -82,24 +82,31 @@ __device__ __forceinline__ f32x16 mfma_f16(i32x4 a, i32x4 b, f32x16 c) {
                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// One workgroup = one item (query block qb, query head h) and one part of its
+// keys: with P > 1 parts, part p takes stages [p * nst / P, (p + 1) * nst / P)
+// of the item's nst stages and writes its unnormalised (o, m, l) to ws; the
+// merge kernel combines the parts.  With P == 1 it writes the output.
 __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
-    const uint16_t* __restrict__ vc, uint16_t* __restrict__ o, int c, int n, int H, int KV,
-    int T, float sc) {
+    const uint16_t* __restrict__ vc, uint16_t* __restrict__ o, float* __restrict__ ws, int c,
+    int n, int H, int KV, int T, int P, float sc) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * kTile];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
   const int nqb = (c + kBQ - 1) / kBQ;
-  int qb, h;
+  int qb, h, part;
   if (KV % 8 == 0) {
     // XCD x = blockIdx.x % 8 takes KV heads j % 8 == x, longest items first.
     const int x = blockIdx.x & 7, s = blockIdx.x >> 3, per = H / 8, G = H / KV;
-    qb = nqb - 1 - s / per;
-    const int r = s % per;
+    qb = nqb - 1 - s / (per * P);
+    const int r = (s / P) % per;
+    part = s % P;
     h = ((r / G) * 8 + x) * G + r % G;
-  } else {  // item i, longest first: query block nqb - 1 - i / H of head i % H
-    qb = nqb - 1 - (int)blockIdx.x / H;
-    h = (int)blockIdx.x % H;
+  } else {  // item i = blockIdx.x / P, longest first: query block nqb - 1 - i / H of head i % H
+    const int i = (int)blockIdx.x / P;
+    part = (int)blockIdx.x % P;
+    qb = nqb - 1 - i / H;
+    h = i % H;
   }
   const int j = h / (H / KV);
   const int tid = threadIdx.x, lane = tid & 63, hl = lane >> 5, l32 = lane & 31;
@@ -112,22 +119,13 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
   const int qa_hi = n - c + min(wq0 + 31, c - 1);
   const bool wave_live = wq0 < c;
 
-  // Q as the B operand: lane (query l32, half hl) holds dims 16s + 8hl .. +7.
-  const int qlc = ql < c ? ql : c - 1;
-  i32x4 qf[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qf[s] = *reinterpret_cast<const i32x4*>(q + ((int64_t)qlc * H + h) * kD + 16 * s + 8 * hl);
-  // Use the Q registers here: the compiler cannot see the DMA loads in its
-  // wait bookkeeping and would otherwise wait for every load in flight before
-  // the first MFMA of each block.
-#pragma unroll
-  for (int s = 0; s < 8; ++s) asm volatile("" ::"v"(qf[s]));
-
-  const int kend = n - c + min(qb * kBQ + kBQ, c);  // keys the workgroup needs
-  const int nst = (kend + kStage - 1) / kStage;
+  const int kend = n - c + min(qb * kBQ + kBQ, c);  // keys the item needs
+  const int nst_item = (kend + kStage - 1) / kStage;
+  const int st0 = part * nst_item / P, st1 = (part + 1) * nst_item / P;  // this part's stages
   const uint16_t* kbase = kc + (int64_t)j * T * kD;
   const uint16_t* vbase = vc + (int64_t)j * T * kD;
+
+  i32x4 qf[8];  // Q fragments, loaded once the first stage's DMA is out
 
   // DMA: wave w fills rows 16w .. 16w + 15 of a stage, 4 rows per
   // instruction; the lane of LDS slot (row r, chunk p) fetches the global
@@ -194,7 +192,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
 
   auto stage = [&](auto bufc, int st) {
     constexpr int buf = decltype(bufc)::value;  // compile-time: LDS offsets become immediates
-    const bool more = st + 1 < nst;
+    const bool more = st + 1 < st1;
     if (more) issue(st + 1, buf ^ 1);
     const int key0 = st * kStage + set * kBKey;  // this wave's block
     if (wave_live && key0 <= qa_hi) {
@@ -282,12 +280,23 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
     __syncthreads();
   };
 
-  issue(0, 0);
+  // The first stage's DMA goes out before the Q loads, so the two latencies overlap.
+  if (st0 < st1) issue(st0, 0);
+  // Q as the B operand: lane (query l32, half hl) holds dims 16s + 8hl .. +7.
+  const int qlc = ql < c ? ql : c - 1;
+#pragma unroll
+  for (int s = 0; s < 8; ++s)
+    qf[s] = *reinterpret_cast<const i32x4*>(q + ((int64_t)qlc * H + h) * kD + 16 * s + 8 * hl);
+  // Use the Q registers here (the loads complete in order, after the DMA): the
+  // compiler cannot see the DMA loads in its wait bookkeeping and would
+  // otherwise wait for every load in flight before the first MFMA of each block.
+#pragma unroll
+  for (int s = 0; s < 8; ++s) asm volatile("" ::"v"(qf[s]));
   wait_vmcnt<0>();
   __syncthreads();
-  for (int st = 0; st < nst; st += 2) {
+  for (int st = st0; st < st1; st += 2) {
     stage(std::integral_constant<int, 0>{}, st);
-    if (st + 1 < nst) stage(std::integral_constant<int, 1>{}, st + 1);
+    if (st + 1 < st1) stage(std::integral_constant<int, 1>{}, st + 1);
   }
   const float l_i = lacc[0];  // every row of the ones tile holds the query's sum
 
@@ -303,7 +312,35 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
     ml[(qw * 2 + 1) * 64 + lane] = l_i;
   }
   __syncthreads();
-  if (set == 0 && ql < c) {
+  if (set == 0 && ql < c && P > 1) {
+    // partial of this part: o = o0 a0 + o1 a1 and l = l0 a0 + l1 a1 relative to m; a part in
+    // which neither set saw a key of this query writes m = -inf, l = 0, o = 0.
+    const float m1 = ml[(qw * 2) * 64 + lane], l1 = ml[(qw * 2 + 1) * 64 + lane];
+    const float m = fmaxf(m_i, m1);
+    const bool none = m == -INFINITY;
+    const float a0 = none ? 0.0f : __builtin_amdgcn_exp2f((m_i - m) * sc);
+    const float a1 = none ? 0.0f : __builtin_amdgcn_exp2f((m1 - m) * sc);
+    const int64_t row = ((int64_t)part * c + ql) * H + h;
+    float* wo = ws + row * kD;
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 v;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int r = 4 * g + t;
+          v[t] = oacc[a][r] * a0 + mo[(qw * 64 + a * 16 + r) * 64 + lane] * a1;
+        }
+        *reinterpret_cast<f32x4*>(wo + a * 32 + 8 * g + 4 * hl) = v;
+      }
+    if (hl == 0) {
+      float* wml = ws + (int64_t)P * c * H * kD + row * 2;
+      wml[0] = m;
+      wml[1] = l_i * a0 + l1 * a1;
+    }
+  }
+  if (set == 0 && ql < c && P == 1) {
     const float m1 = ml[(qw * 2) * 64 + lane], l1 = ml[(qw * 2 + 1) * 64 + lane];
     const float m = fmaxf(m_i, m1);  // finite: set 0 always sees key 0
     const float a0 = __builtin_amdgcn_exp2f((m_i - m) * sc);
@@ -326,14 +363,69 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
   }
 }
 
+// out[i, h, :] = sum_p o_p 2^((m_p - M) sc) / sum_p l_p 2^((m_p - M) sc), M = max_p m_p:
+// 16 threads per (query, head), 8 dimensions each, parts in order.
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ ws,
+                                                                 uint16_t* __restrict__ out,
+                                                                 int64_t rows, int P, float sc) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int d0 = 8 * (threadIdx.x & 15);
+  if (row >= rows) return;
+  const float* ml = ws + (int64_t)P * rows * kD;
+  float M = -INFINITY;
+  for (int p = 0; p < P; ++p) M = fmaxf(M, ml[((int64_t)p * rows + row) * 2]);
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0}, L = 0.0f;
+  for (int p = 0; p < P; ++p) {
+    const int64_t pr = (int64_t)p * rows + row;
+    const float mp = ml[pr * 2];
+    const float w = mp == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((mp - M) * sc);
+    L += ml[pr * 2 + 1] * w;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(ws + pr * kD + d0);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(ws + pr * kD + d0 + 4);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] += a[t] * w;
+      acc[4 + t] += b[t] * w;
+    }
+  }
+  const float inv = 1.0f / L;
+  i32x4 v;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) v[t] = (int32_t)f2h2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
+  *reinterpret_cast<i32x4*>(out + row * kD + d0) = v;
+}
+
 }  // namespace
 
-hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                               uint16_t* out, float scale, int c, int n, int H, int KV,
-                               int64_t T, hipStream_t s) {
+int attn_prefill_parts(int c, int n, int H) {
   const int items = ((c + kBQ - 1) / kBQ) * H;
-  attn_prefill_kernel<<<items, kThreads, 0, s>>>(q, kc, vc, out, c, n, H, KV, (int)T,
-                                                  scale * 1.4426950408889634f);
+  const int cus = num_cus();
+  if (items >= cus) return 1;
+  const int nst_max = (n + kStage - 1) / kStage;  // the longest item's stages
+  int P = cus / items;
+  P = P < 8 ? P : 8;
+  P = P < nst_max / 4 ? P : nst_max / 4;  // at least four stages per part
+  return P > 1 ? P : 1;
+}
+
+size_t attn_prefill_ws_floats(int c, int n, int H) {
+  const int P = attn_prefill_parts(c, n, H);
+  return P > 1 ? (size_t)P * c * H * (kD + 2) : 0;
+}
+
+hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                               uint16_t* out, float scale, float* ws, size_t ws_floats, int c,
+                               int n, int H, int KV, int64_t T, hipStream_t s) {
+  const float sc = scale * 1.4426950408889634f;
+  int P = attn_prefill_parts(c, n, H);
+  if (ws == nullptr || ws_floats < (size_t)P * c * H * (kD + 2)) P = 1;
+  const int items = ((c + kBQ - 1) / kBQ) * H;
+  attn_prefill_kernel<<<items * P, kThreads, 0, s>>>(q, kc, vc, out, ws, c, n, H, KV, (int)T, P,
+                                                      sc);
+  if (P > 1) {
+    const int64_t rows = (int64_t)c * H;
+    attn_prefill_merge_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(ws, out, rows, P, sc);
+  }
   return hipGetLastError();
 }
 

@@ -651,15 +651,22 @@ int cider_attn_decode(const void* q_f16, const void* k_cache_f16, const void* v_
       fn);
 }
 
+size_t cider_attn_prefill_workspace_bytes(int64_t c, int64_t n, int64_t H) {
+  if (H <= 0 || H > 4096 || c < 1 || n < c || n > ((int64_t)1 << 24) || c * H > kMaxDim)
+    return 0;
+  const size_t f = cider::attn_prefill_ws_floats((int)c, (int)n, (int)H);
+  return f ? align256(f * sizeof(float)) : 0;
+}
+
 int cider_attn_prefill(const void* q_f16, const void* k_cache_f16, const void* v_cache_f16,
-                       float scale, void* out_f16, int64_t c, int64_t n, int64_t H, int64_t KV,
-                       int64_t D, int64_t T, void* stream) {
+                       float scale, void* ws, size_t ws_bytes, void* out_f16, int64_t c,
+                       int64_t n, int64_t H, int64_t KV, int64_t D, int64_t T, void* stream) {
   static const char* fn = "cider_attn_prefill";
   if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
   if (H <= 0 || KV <= 0 || H > 4096 || H % KV != 0)
     return fail(CIDER_E_INVALID, "%s: H=%lld must be a positive multiple of KV=%lld (H <= 4096)",
                 fn, (long long)H, (long long)KV);
-  if (T <= 0 || T > ((int64_t)1 << 24) || n < 1 || n > T || c < 1 || c > n)
+  if (T <= 0 || T > ((int64_t)1 << 24) || n < 1 || n > T || c < 1 || c > n || c * H > kMaxDim)
     return fail(CIDER_E_INVALID, "%s: need 1 <= c <= n <= T <= 2^24 (c=%lld n=%lld T=%lld)", fn,
                 (long long)c, (long long)n, (long long)T);
   CIDER_TRY(need(fn, q_f16, "q", true));
@@ -669,12 +676,15 @@ int cider_attn_prefill(const void* q_f16, const void* k_cache_f16, const void* v
   if (!aligned16(q_f16) || !aligned16(k_cache_f16) || !aligned16(v_cache_f16) ||
       !aligned16(out_f16))
     return fail(CIDER_E_INVALID, "%s: q, the caches and out must be 16-byte aligned", fn);
+  if (ws != nullptr && ((uintptr_t)ws & 255) != 0)
+    return fail(CIDER_E_INVALID, "%s: ws must be 256-byte aligned", fn);
   return hip_status(
       cider::launch_attn_prefill(reinterpret_cast<const uint16_t*>(q_f16),
                                  reinterpret_cast<const uint16_t*>(k_cache_f16),
                                  reinterpret_cast<const uint16_t*>(v_cache_f16),
-                                 reinterpret_cast<uint16_t*>(out_f16), scale, (int)c, (int)n,
-                                 (int)H, (int)KV, T, (hipStream_t)stream),
+                                 reinterpret_cast<uint16_t*>(out_f16), scale,
+                                 reinterpret_cast<float*>(ws), ws ? ws_bytes / sizeof(float) : 0,
+                                 (int)c, (int)n, (int)H, (int)KV, T, (hipStream_t)stream),
       fn);
 }
 

@@ -169,15 +169,26 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+def attn_prefill_workspace(c: int, n: int, num_heads: int, device) -> Optional[torch.Tensor]:
+    """The workspace a chunk of c queries over n slots splits its keys into
+    (None when the launch does not split)."""
+    nbytes = _lib.load().cider_attn_prefill_workspace_bytes(c, n, num_heads)
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, n: int,
-                 scale: float, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+                 scale: float, out: Optional[torch.Tensor] = None,
+                 ws: Optional[torch.Tensor] = None, split: bool = True,
+                 stream=None) -> torch.Tensor:
     """Causal grouped-query attention of a prefill chunk: q [c, H, 128] holds
     the queries of cache slots n - c .. n - 1, whose keys and values are
     already in k_cache / v_cache [KV, T, 128]; query i attends slots
     0 .. n - c + i.  Returns fp16 [c, H * 128] (the reference hands this to
-    MLX's fused SDPA, ``cider/fused_hybrid.py:179-196``)."""
+    MLX's fused SDPA, ``cider/fused_hybrid.py:179-196``).  A launch with few
+    query blocks splits its keys over several workgroups into a workspace
+    (allocated here unless ``ws`` is given); ``split=False`` runs unsplit."""
     fn = "attn_prefill"
-    dev = _require_gpu(fn, q, k_cache, v_cache, out)
+    dev = _require_gpu(fn, q, k_cache, v_cache, out, ws)
     _f16(fn, "q", q)
     _f16(fn, "k_cache", k_cache)
     _f16(fn, "v_cache", v_cache)
@@ -193,8 +204,11 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
             out = torch.empty(c, H * D, dtype=torch.float16, device=dev)
         elif out.dtype != torch.float16 or not out.is_contiguous() or out.numel() != c * H * D:
             raise ValueError(f"{fn}: out must be a contiguous float16 tensor of c x H x {D}")
+        if ws is None and split:
+            ws = attn_prefill_workspace(c, int(n), H, dev)
+        wsp, wsb = (_ptr(ws), ws.numel()) if (ws is not None and split) else (None, 0)
         _lib.check(lib.cider_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), float(scale),
-                                          _ptr(out), c, int(n), H, KV, D, T,
+                                          wsp, wsb, _ptr(out), c, int(n), H, KV, D, T,
                                           _stream_ptr(dev, stream)))
     return out
 

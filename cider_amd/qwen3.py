@@ -191,15 +191,18 @@ class Qwen3Layer(torch.nn.Module):
                                    sum_out=x if pending is not None else None,
                                    want_y=want_y, want_q=want_q)
 
-    def prefill_fused(self, x, pending, tables, rope_row, slot, k_cache, v_cache, n):
+    def prefill_fused(self, x, pending, tables, rope_row, slot, k_cache, v_cache, n,
+                      attn_ws=None):
         """x [L, hidden] (+ pending) at cache slots n - L .. n - 1 (`slot`);
-        attends causally over cache slots 0..n-1.  Returns (x, pending)."""
+        attends causally over cache slots 0..n-1 (``attn_ws``: the attention's
+        split workspace for this (L, n), shared by the layers).  Returns
+        (x, pending)."""
         c = self.cfg
         a = self._norm(x, pending, self.input_norm, False, True)
         qkv = self.qkv.forward_quantized(a.q, a.scale_a)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
                             rope_row, slot, k_cache, v_cache, c.num_heads, c.num_kv_heads)
-        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim))
+        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim), ws=attn_ws)
         b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
         gu = self.gate_up.forward_quantized(b.q, b.scale_a)
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
@@ -319,9 +322,10 @@ class Qwen3(torch.nn.Module):
         if self.fused:
             pos = torch.arange(L, device=self.device)
             pending = None
+            ws = FK.attn_prefill_workspace(L, L, self.cfg.num_heads, self.device)
             for i, layer in enumerate(self.layers):
                 x, pending = layer.prefill_fused(x, pending, (self.cos, self.sin), pos, pos,
-                                                 self.k_cache[i], self.v_cache[i], L)
+                                                 self.k_cache[i], self.v_cache[i], L, ws)
             if last_only:
                 x, pending = x[-1:].clone(), pending[-1:].clone()
             return F.linear(self._final_norm(x, pending), self.lm_head)

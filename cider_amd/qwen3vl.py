@@ -38,6 +38,7 @@ from typing import List, Sequence, Tuple
 import torch
 import torch.nn.functional as F
 
+from . import fused as FK
 from .qwen3 import Qwen3, Qwen3Config
 
 QWEN3_VL_2B = Qwen3Config(hidden_size=2048, intermediate_size=6144, num_layers=28, num_heads=16,
@@ -163,10 +164,11 @@ class Qwen3VL(Qwen3):
             xc = x[s:e].clone()
             rows = torch.arange(c, device=self.device)
             pc = None
+            ws = FK.attn_prefill_workspace(e - s, e, self.cfg.num_heads, self.device)
             for i, layer in enumerate(self.layers):
                 # query i (slot s + i) sees slots 0 .. s + i
                 xc, pc = layer.prefill_fused(xc, pc, (cos[s:e], sin[s:e]), rows,
-                                             slots[s:e], self.k_cache[i], self.v_cache[i], e)
+                                             slots[s:e], self.k_cache[i], self.v_cache[i], e, ws)
             out = (xc, pc)
         xl, pl = out
         logits = F.linear(self._final_norm(xl[-1:].clone(), pl[-1:].clone()), self.lm_head)

@@ -265,6 +265,12 @@ int cider_attn_decode(const void* q_f16, const void* k_cache_f16,
                       void* ws, size_t ws_bytes, void* out_f16, int64_t H,
                       int64_t KV, int64_t D, int64_t T, void* stream);
 
+/* Bytes of workspace cider_attn_prefill uses for a chunk of c queries over n
+ * cache slots with H query heads: the fp32 partials of a launch that splits
+ * its keys over several workgroups per query block (when the query blocks
+ * alone would fill few CUs); 0 when it does not split. */
+size_t cider_attn_prefill_workspace_bytes(int64_t c, int64_t n, int64_t H);
+
 /* Causal grouped-query attention of a prefill chunk over the caches written
  * by cider_qk_norm_rope: the chunk's c queries q [c, H, D] sit at cache slots
  * n - c .. n - 1 (their keys already written), and for query i, head h of KV
@@ -272,13 +278,15 @@ int cider_attn_decode(const void* q_f16, const void* k_cache_f16,
  *   out[i, h] = sum_{t <= n - c + i} softmax_t(scale * q[i,h] . K[j,t,:]) V[j,t,:]
  * rounded to fp16 [c, H, D].  Replaces the reference's prefill call of MLX's
  * fused SDPA (cider/fused_hybrid.py:179-196); fp32 scores and accumulation,
- * probabilities rounded to fp16 for the P.V product.  D == 128,
- * 1 <= c <= n <= T, H % KV == 0; q, the caches and out 16-byte aligned; out
- * must not overlap the inputs. */
+ * probabilities rounded to fp16 for the P.V product.  ws (256-byte aligned)
+ * of cider_attn_prefill_workspace_bytes lets a launch with few query blocks
+ * split its keys; NULL or a smaller ws runs unsplit (results within the same
+ * bar, not bit-identical).  D == 128, 1 <= c <= n <= T, H % KV == 0; q, the
+ * caches and out 16-byte aligned; out and ws must not overlap the inputs. */
 int cider_attn_prefill(const void* q_f16, const void* k_cache_f16,
-                       const void* v_cache_f16, float scale, void* out_f16,
-                       int64_t c, int64_t n, int64_t H, int64_t KV, int64_t D,
-                       int64_t T, void* stream);
+                       const void* v_cache_f16, float scale, void* ws,
+                       size_t ws_bytes, void* out_f16, int64_t c, int64_t n,
+                       int64_t H, int64_t KV, int64_t D, int64_t T, void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 21, syms
+    assert len(syms) == 22, syms
 
 
 @pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
@@ -211,17 +211,25 @@ def test_producer_and_attention_validation_without_gpu(lib):
     assert "workspace" in _err(lib)
     assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 32, 8, 64, 4096, n) == E
     # prefill attention: head_dim, grouping, 1 <= c <= n <= T, pointers, alignment
-    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 32, 32, 8, 64, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, 32, 8, 64, 64, n) == E
     assert "head_dim" in _err(lib)
-    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 32, 30, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 33, 32, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 0, 32, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, p, 16, 65, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(n, p, p, 0.1, p, 16, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, 30, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 33, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 0, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 65, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(n, p, p, 0.1, n, 0, p, 16, 32, 32, 8, 128, 64, n) == E
     assert "q is NULL" in _err(lib)
-    assert lib.cider_attn_prefill(p, p, p, 0.1, ctypes.c_void_p(0x1008), 16, 32, 32, 8, 128,
-                                  64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, ctypes.c_void_p(0x1008), 16, 32, 32, 8,
+                                  128, 64, n) == E
     assert "aligned" in _err(lib)
+    assert lib.cider_attn_prefill(p, p, p, 0.1, ctypes.c_void_p(0x1010), 4096, p, 16, 32, 32, 8,
+                                  128, 64, n) == E
+    assert "256-byte" in _err(lib)
+    # the workspace is what a split launch needs: none for a launch that fills the GPU
+    assert lib.cider_attn_prefill_workspace_bytes(2048, 2048, 32) == 0
+    assert lib.cider_attn_prefill_workspace_bytes(0, 2048, 32) == 0
+    # a 512-query chunk over 2048 slots with 16 heads (64 query blocks): 4 parts of fp32 partials
+    assert lib.cider_attn_prefill_workspace_bytes(512, 2048, 16) == 4 * 512 * 16 * 130 * 4
     # empty problems succeed
     assert lib.cider_rmsnorm_quantize(n, n, n, n, 1e-6, p, n, n, 0, 16, n) == _lib.CIDER_OK
     assert lib.cider_qk_norm_rope(*(args[:12] + [0] + args[13:])) == _lib.CIDER_OK

@@ -334,6 +334,38 @@ def test_attn_prefill(c, n, H, KV, T, qs):
     assert bool((err <= tol).all()), f"max err {err.max().item():.3e}"
 
 
+# chunks whose query blocks fill few CUs split their keys over parts (a first
+# chunk of 1024: the first query block's first part holds no stage at all;
+# later chunks: 2-8 parts); the unsplit launch is held to the same bar
+SPLIT_CASES = [(1024, 1024, 8, 8, 1024), (512, 2048, 16, 8, 2048), (383, 3455, 16, 8, 3584),
+               (100, 1000, 32, 8, 1024), (128, 4096, 8, 8, 4096)]
+
+
+@pytest.mark.parametrize("c,n,H,KV,T", SPLIT_CASES)
+def test_attn_prefill_split_and_unsplit(c, n, H, KV, T):
+    from cider_amd import _lib
+    D = 128
+    assert _lib.load().cider_attn_prefill_workspace_bytes(c, n, H) > 0, "expected a split launch"
+    g = torch.Generator(device="cuda").manual_seed(c + 3 * n)
+    q = torch.randn(c, H, D, device="cuda", generator=g).half()
+    kc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    kc[:, n:, :] = float("nan")
+    vc[:, n:, :] = float("nan")
+    scale = 1.0 / math.sqrt(D)
+    ws = F.attn_prefill_workspace(c, n, H, "cuda")
+    ws.fill_(0xFF)  # stale partials must not matter
+    split = F.attn_prefill(q, kc, vc, n, scale, ws=ws)
+    plain = F.attn_prefill(q, kc, vc, n, scale, split=False)
+    torch.cuda.synchronize()
+    exp = _prefill_ref(q, kc, vc, c, n, scale)
+    for got in (split, plain):
+        got = got.double().reshape(c, H, D)
+        assert torch.isfinite(got).all()
+        err = (got - exp).abs()
+        assert bool((err <= 3e-3 + 5e-3 * exp.abs()).all()), f"max err {err.max().item():.3e}"
+
+
 def test_attn_prefill_chunks_match_one_shot():
     """Chunks of 512 after earlier slots (the Qwen3-VL prefill) give what one
     launch over the whole prompt gives, within the same bar."""
