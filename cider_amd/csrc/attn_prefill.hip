@@ -89,7 +89,11 @@ __device__ __forceinline__ f32x16 mfma_f16(i32x4 a, i32x4 b, f32x16 c) {
 __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, uint16_t* __restrict__ o, float* __restrict__ ws, int c,
-    int n, int H, int KV, int T, int P, float sc) {
+    int n, const int64_t* __restrict__ n_dev, int H, int KV, int T, int P, float sc) {
+  if (n_dev != nullptr) {  // the valid length from the device, within [c, the host bound]
+    const int64_t nd = *n_dev;
+    n = (int)(nd < c ? c : (nd > n ? n : nd));
+  }
   __shared__ __attribute__((aligned(1024))) uint8_t smem[4 * kTile];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
@@ -238,8 +242,11 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
         for (int r = 0; r < 16; ++r) mb = fmaxf(mb, sacc[kb][r]);
       mb = fmaxf(mb, __shfl_xor(mb, 32));
       if (__any(mb * sc > m_i * sc + kRescaleLog2)) {
+        // A lane whose keys so far (in this wave set) are all masked keeps m = -inf; its o and
+        // l are 0, and it must not form -inf - -inf.
         const float m_new = fmaxf(m_i, mb);
-        const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * sc);
+        const float alpha =
+            m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f((m_i - m_new) * sc);
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
         for (int r = 0; r < 16; ++r) lacc[r] *= alpha;
         m_i = m_new;
       }
-      const float mc = m_i * sc;
+      const float mc = m_i == -INFINITY ? 0.0f : m_i * sc;  // such a lane's p: exp2(-inf) = 0
       i32x4 pf[2][2];  // P^T as the B operand: 8 keys k0 + {0..3, 8..11} per (kb, mm)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -415,13 +422,14 @@ size_t attn_prefill_ws_floats(int c, int n, int H) {
 
 hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                uint16_t* out, float scale, float* ws, size_t ws_floats, int c,
-                               int n, int H, int KV, int64_t T, hipStream_t s) {
+                               int n, const int64_t* n_dev, int H, int KV, int64_t T,
+                               hipStream_t s) {
   const float sc = scale * 1.4426950408889634f;
   int P = attn_prefill_parts(c, n, H);
   if (ws == nullptr || ws_floats < (size_t)P * c * H * (kD + 2)) P = 1;
   const int items = ((c + kBQ - 1) / kBQ) * H;
-  attn_prefill_kernel<<<items * P, kThreads, 0, s>>>(q, kc, vc, out, ws, c, n, H, KV, (int)T, P,
-                                                      sc);
+  attn_prefill_kernel<<<items * P, kThreads, 0, s>>>(q, kc, vc, out, ws, c, n, n_dev, H, KV,
+                                                      (int)T, P, sc);
   if (P > 1) {
     const int64_t rows = (int64_t)c * H;
     attn_prefill_merge_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(ws, out, rows, P, sc);

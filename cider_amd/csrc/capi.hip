@@ -660,7 +660,8 @@ size_t cider_attn_prefill_workspace_bytes(int64_t c, int64_t n, int64_t H) {
 
 int cider_attn_prefill(const void* q_f16, const void* k_cache_f16, const void* v_cache_f16,
                        float scale, void* ws, size_t ws_bytes, void* out_f16, int64_t c,
-                       int64_t n, int64_t H, int64_t KV, int64_t D, int64_t T, void* stream) {
+                       int64_t n, const int64_t* n_dev, int64_t H, int64_t KV, int64_t D,
+                       int64_t T, void* stream) {
   static const char* fn = "cider_attn_prefill";
   if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
   if (H <= 0 || KV <= 0 || H > 4096 || H % KV != 0)
@@ -684,7 +685,7 @@ int cider_attn_prefill(const void* q_f16, const void* k_cache_f16, const void* v
                                  reinterpret_cast<const uint16_t*>(v_cache_f16),
                                  reinterpret_cast<uint16_t*>(out_f16), scale,
                                  reinterpret_cast<float*>(ws), ws ? ws_bytes / sizeof(float) : 0,
-                                 (int)c, (int)n, (int)H, (int)KV, T, (hipStream_t)stream),
+                                 (int)c, (int)n, n_dev, (int)H, (int)KV, T, (hipStream_t)stream),
       fn);
 }
 

@@ -118,14 +118,16 @@ hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* kc, const uint1
                               int KV, int64_t T, hipStream_t s);
 
 // Causal attention of a prefill chunk over the KV cache (attn_prefill.hip):
-// c queries at cache slots n - c .. n - 1, D == 128, H % KV == 0.  Launches
+// c queries at cache slots n - c .. n - 1, D == 128, H % KV == 0 (n_dev: n
+// read on the device, n its upper bound).  Launches
 // that would fill few CUs split their keys over parts when ws holds
 // attn_prefill_ws_floats(c, n, H) floats (nullptr / fewer: one part).
 int attn_prefill_parts(int c, int n, int H);
 size_t attn_prefill_ws_floats(int c, int n, int H);
 hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                                uint16_t* out, float scale, float* ws, size_t ws_floats, int c,
-                               int n, int H, int KV, int64_t T, hipStream_t s);
+                               int n, const int64_t* n_dev, int H, int KV, int64_t T,
+                               hipStream_t s);
 
 hipError_t launch_w4_repack_ref(const uint8_t* src_kn, uint8_t* dst_nk, int N,
                                 int K, hipStream_t s);

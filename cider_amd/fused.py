@@ -179,16 +179,21 @@ def attn_prefill_workspace(c: int, n: int, num_heads: int, device) -> Optional[t
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, n: int,
                  scale: float, out: Optional[torch.Tensor] = None,
                  ws: Optional[torch.Tensor] = None, split: bool = True,
-                 stream=None) -> torch.Tensor:
+                 n_dev: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """Causal grouped-query attention of a prefill chunk: q [c, H, 128] holds
     the queries of cache slots n - c .. n - 1, whose keys and values are
     already in k_cache / v_cache [KV, T, 128]; query i attends slots
     0 .. n - c + i.  Returns fp16 [c, H * 128] (the reference hands this to
     MLX's fused SDPA, ``cider/fused_hybrid.py:179-196``).  A launch with few
     query blocks splits its keys over several workgroups into a workspace
-    (allocated here unless ``ws`` is given); ``split=False`` runs unsplit."""
+    (allocated here unless ``ws`` is given); ``split=False`` runs unsplit.
+    ``n_dev`` (int64 [1] on the device): the length is read there, clamped to
+    [c, n], with n its upper bound -- for a call captured in a graph that
+    serves chunks at any cache offset."""
     fn = "attn_prefill"
-    dev = _require_gpu(fn, q, k_cache, v_cache, out, ws)
+    dev = _require_gpu(fn, q, k_cache, v_cache, out, ws, n_dev)
+    if n_dev is not None and (n_dev.dtype != torch.int64 or n_dev.numel() < 1):
+        raise ValueError(f"{fn}: n_dev must be an int64 tensor")
     _f16(fn, "q", q)
     _f16(fn, "k_cache", k_cache)
     _f16(fn, "v_cache", v_cache)
@@ -208,8 +213,8 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
             ws = attn_prefill_workspace(c, int(n), H, dev)
         wsp, wsb = (_ptr(ws), ws.numel()) if (ws is not None and split) else (None, 0)
         _lib.check(lib.cider_attn_prefill(_ptr(q), _ptr(k_cache), _ptr(v_cache), float(scale),
-                                          wsp, wsb, _ptr(out), c, int(n), H, KV, D, T,
-                                          _stream_ptr(dev, stream)))
+                                          wsp, wsb, _ptr(out), c, int(n), _ptr(n_dev), H, KV, D,
+                                          T, _stream_ptr(dev, stream)))
     return out
 
 

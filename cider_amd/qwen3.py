@@ -192,17 +192,19 @@ class Qwen3Layer(torch.nn.Module):
                                    want_y=want_y, want_q=want_q)
 
     def prefill_fused(self, x, pending, tables, rope_row, slot, k_cache, v_cache, n,
-                      attn_ws=None):
+                      attn_ws=None, n_dev=None):
         """x [L, hidden] (+ pending) at cache slots n - L .. n - 1 (`slot`);
         attends causally over cache slots 0..n-1 (``attn_ws``: the attention's
-        split workspace for this (L, n), shared by the layers).  Returns
+        split workspace for this (L, n), shared by the layers; ``n_dev``: n
+        read on the device, the host n its upper bound).  Returns
         (x, pending)."""
         c = self.cfg
         a = self._norm(x, pending, self.input_norm, False, True)
         qkv = self.qkv.forward_quantized(a.q, a.scale_a)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
                             rope_row, slot, k_cache, v_cache, c.num_heads, c.num_kv_heads)
-        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim), ws=attn_ws)
+        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim), ws=attn_ws,
+                               n_dev=n_dev)
         b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
         gu = self.gate_up.forward_quantized(b.q, b.scale_a)
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
@@ -267,7 +269,7 @@ class Qwen3(torch.nn.Module):
     """Random-init Qwen3-shaped causal LM over W8A8 per-channel linears."""
 
     def __init__(self, cfg: Qwen3Config = QWEN3_8B, max_len: int = 4096, seed: int = 0,
-                 device="cuda", fused: bool = True):
+                 device="cuda", fused: bool = True, capacity_multiple: int = 8):
         super().__init__()
         if fused and cfg.head_dim != 128:
             raise ValueError("Qwen3(fused=True): the q/k-norm, RoPE and attention kernels "
@@ -280,9 +282,11 @@ class Qwen3(torch.nn.Module):
         gen.manual_seed(seed)
         self.cfg = cfg
         self.max_len = max_len
-        # cache capacity: a multiple of 8 positions (16-byte rows of the
-        # transposed K cache for the attention kernel)
-        cap = (max_len + 7) // 8 * 8
+        # cache capacity: a multiple of 8 positions (the decode attention's
+        # 8-position groups), or of capacity_multiple (a chunked prefill that
+        # pads its last chunk to the chunk size writes that far)
+        mult = max(8, (capacity_multiple + 7) // 8 * 8)
+        cap = (max_len + mult - 1) // mult * mult
         self.capacity = cap
         self.device = dev
         h = cfg.hidden_size

@@ -119,9 +119,12 @@ class Qwen3VL(Qwen3):
 
     def __init__(self, cfg: Qwen3Config = QWEN3_VL_2B, max_len: int = 4096, seed: int = 0,
                  device="cuda", section: Sequence[int] = MROPE_SECTION):
-        super().__init__(cfg, max_len=max_len, seed=seed, device=device, fused=True)
+        # capacity a multiple of the chunk: the graph prefill pads its last chunk
+        super().__init__(cfg, max_len=max_len, seed=seed, device=device, fused=True,
+                         capacity_multiple=PREFILL_CHUNK)
         self.section = tuple(section)
         self.lm_head = self.embed          # tied, as the 2B model
+        self._chunk_graph = None           # (chunk, graph, static buffers, outputs)
 
     def embed_prompt(self, segments: Sequence[Segment], seed: int = 0) -> Tuple[torch.Tensor,
                                                                              torch.Tensor]:
@@ -143,18 +146,67 @@ class Qwen3VL(Qwen3):
                 ids.append(torch.full((n,), -1, dtype=torch.int64, device=self.device))
         return torch.cat(xs), torch.cat(ids)
 
+    def _chunk_layers(self, xc, rows, tables, slots, n, ws, n_dev=None):
+        """The 28 layers over one chunk xc [c, hidden] at cache slots `slots`."""
+        pc = None
+        for i, layer in enumerate(self.layers):
+            xc, pc = layer.prefill_fused(xc, pc, tables, rows, slots, self.k_cache[i],
+                                         self.v_cache[i], n, ws, n_dev)
+        return xc, pc
+
+    def _capture_chunk(self, chunk: int):
+        """One HIP graph of the layers over a chunk of `chunk` rows whose
+        inputs (embeddings, RoPE rows, cache slots, valid length) are static
+        device buffers: every chunk of a prompt replays it after filling them.
+        The warm-up and capture run with slots outside the cache, which the
+        q/k-norm kernel writes nowhere, so they leave the cache as it was."""
+        dev, h = self.device, self.cfg.hidden_size
+        buf = {"x": torch.zeros(chunk, h, dtype=torch.float16, device=dev),
+               "cos": torch.zeros(chunk, self.cfg.head_dim, dtype=torch.float16, device=dev),
+               "sin": torch.zeros(chunk, self.cfg.head_dim, dtype=torch.float16, device=dev),
+               "rows": torch.arange(chunk, device=dev),
+               "slots": torch.full((chunk,), -1, dtype=torch.int64, device=dev),
+               "n": torch.tensor([chunk], dtype=torch.int64, device=dev)}
+        cap = self.capacity
+        ws = FK.attn_prefill_workspace(chunk, cap, self.cfg.num_heads, dev)
+
+        def run():
+            return self._chunk_layers(buf["x"], buf["rows"], (buf["cos"], buf["sin"]),
+                                      buf["slots"], cap, ws, buf["n"])
+
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = run()
+        torch.cuda.synchronize(dev)
+        self._chunk_graph = (chunk, g, buf, out, ws)
+
     @torch.no_grad()
     def prefill_chunked(self, x: torch.Tensor, pos3: torch.Tensor,
-                        chunk: int = PREFILL_CHUNK) -> torch.Tensor:
+                        chunk: int = PREFILL_CHUNK, graph: bool = True) -> torch.Tensor:
         """Prefills embeddings x [L, hidden] at M-RoPE positions pos3 [3, L]
         in chunks, into cache slots 0..L-1.  Returns the logits [1, vocab] of
-        the last token, and sets the decode RoPE offset."""
+        the last token, and sets the decode RoPE offset.
+
+        graph=True: every chunk is one replay of a captured graph of the
+        layers over `chunk` rows; the last chunk is padded with zero rows at
+        the following slots (within the cache capacity, a multiple of the
+        chunk; where the padded prompt would not fit, the chunks run eagerly).  Causal attention keeps the real tokens from seeing the
+        padded keys, and every other step is row-wise, so the real rows get
+        what the eager chunks compute (up to the attention's rounding); the
+        padded slots past L are rewritten by decode before it reads them."""
         L = x.shape[0]
         if L > self.max_len:
             raise ValueError(f"prompt of {L} tokens exceeds max_len={self.max_len}")
         if pos3.shape != (3, L):
             raise ValueError("pos3 must be [3, L]")
         pos3 = pos3.to(self.device)
+        if graph and (L + chunk - 1) // chunk * chunk <= self.capacity:
+            return self._prefill_chunked_graph(x, pos3, chunk)
         cos, sin = mrope_cos_sin(pos3, self.cfg.head_dim, self.cfg.rope_theta, self.section)
         slots = torch.arange(L, device=self.device)
         out = None
@@ -171,10 +223,36 @@ class Qwen3VL(Qwen3):
                                              slots[s:e], self.k_cache[i], self.v_cache[i], e, ws)
             out = (xc, pc)
         xl, pl = out
-        logits = F.linear(self._final_norm(xl[-1:].clone(), pl[-1:].clone()), self.lm_head)
+        return self._prefill_logits(xl[-1:], pl[-1:], pos3, L)
+
+    def _prefill_logits(self, xl, pl, pos3, L):
+        logits = F.linear(self._final_norm(xl.clone(), pl.clone()), self.lm_head)
         delta = int(pos3.max()) + 1 - L
         self._rope_delta = torch.tensor([delta], dtype=torch.int64, device=self.device)
         return logits
+
+    def _prefill_chunked_graph(self, x, pos3, chunk):
+        L = x.shape[0]
+        if self._chunk_graph is None or self._chunk_graph[0] != chunk:
+            self._capture_chunk(chunk)
+        _, g, buf, (xo, po), _ = self._chunk_graph
+        nch = (L + chunk - 1) // chunk
+        Lp = nch * chunk
+        # positions of the padded rows repeat the last one (any finite RoPE row serves)
+        pos_p = torch.cat([pos3, pos3[:, -1:].expand(3, Lp - L)], dim=1) if Lp > L else pos3
+        cos, sin = mrope_cos_sin(pos_p, self.cfg.head_dim, self.cfg.rope_theta, self.section)
+        for k in range(nch):
+            s, e = k * chunk, min(L, (k + 1) * chunk)
+            buf["x"][: e - s].copy_(x[s:e])
+            if e - s < chunk:
+                buf["x"][e - s:].zero_()
+            buf["cos"].copy_(cos[s:s + chunk])
+            buf["sin"].copy_(sin[s:s + chunk])
+            torch.arange(s, s + chunk, device=self.device, out=buf["slots"])
+            buf["n"].fill_(s + chunk)
+            g.replay()
+        r = (L - 1) - (nch - 1) * chunk  # the last real row of the last chunk
+        return self._prefill_logits(xo[r:r + 1], po[r:r + 1], pos3, L)
 
     @torch.no_grad()
     def generate_from_prompt(self, segments: Sequence[Segment], steps: int, seed: int = 0,

@@ -281,12 +281,16 @@ size_t cider_attn_prefill_workspace_bytes(int64_t c, int64_t n, int64_t H);
  * probabilities rounded to fp16 for the P.V product.  ws (256-byte aligned)
  * of cider_attn_prefill_workspace_bytes lets a launch with few query blocks
  * split its keys; NULL or a smaller ws runs unsplit (results within the same
- * bar, not bit-identical).  D == 128, 1 <= c <= n <= T, H % KV == 0; q, the
- * caches and out 16-byte aligned; out and ws must not overlap the inputs. */
+ * bar, not bit-identical).  With n_dev non-NULL (device int64) the length is
+ * read on the device, clamped to [c, n], and n is its upper bound (it sizes
+ * the split), so one captured call serves chunks at any cache offset.
+ * D == 128, 1 <= c <= n <= T, H % KV == 0; q, the caches and out 16-byte
+ * aligned; out and ws must not overlap the inputs. */
 int cider_attn_prefill(const void* q_f16, const void* k_cache_f16,
                        const void* v_cache_f16, float scale, void* ws,
                        size_t ws_bytes, void* out_f16, int64_t c, int64_t n,
-                       int64_t H, int64_t KV, int64_t D, int64_t T, void* stream);
+                       const int64_t* n_dev, int64_t H, int64_t KV, int64_t D,
+                       int64_t T, void* stream);
 
 #ifdef __cplusplus
 }

@@ -211,19 +211,19 @@ def test_producer_and_attention_validation_without_gpu(lib):
     assert "workspace" in _err(lib)
     assert lib.cider_attn_decode(p, p, p, p, 0.1, p, wsb, p, 32, 8, 64, 4096, n) == E
     # prefill attention: head_dim, grouping, 1 <= c <= n <= T, pointers, alignment
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, 32, 8, 64, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, n, 32, 8, 64, 64, n) == E
     assert "head_dim" in _err(lib)
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, 30, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 33, 32, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 0, 32, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 65, 32, 8, 128, 64, n) == E
-    assert lib.cider_attn_prefill(n, p, p, 0.1, n, 0, p, 16, 32, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 32, n, 30, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 33, 32, n, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 0, 32, n, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, p, 16, 65, n, 32, 8, 128, 64, n) == E
+    assert lib.cider_attn_prefill(n, p, p, 0.1, n, 0, p, 16, 32, n, 32, 8, 128, 64, n) == E
     assert "q is NULL" in _err(lib)
-    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, ctypes.c_void_p(0x1008), 16, 32, 32, 8,
-                                  128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, n, 0, ctypes.c_void_p(0x1008), 16,
+                                  32, n, 32, 8, 128, 64, n) == E
     assert "aligned" in _err(lib)
-    assert lib.cider_attn_prefill(p, p, p, 0.1, ctypes.c_void_p(0x1010), 4096, p, 16, 32, 32, 8,
-                                  128, 64, n) == E
+    assert lib.cider_attn_prefill(p, p, p, 0.1, ctypes.c_void_p(0x1010), 4096, p, 16,
+                                  32, n, 32, 8, 128, 64, n) == E
     assert "256-byte" in _err(lib)
     # the workspace is what a split launch needs: none for a launch that fills the GPU
     assert lib.cider_attn_prefill_workspace_bytes(2048, 2048, 32) == 0

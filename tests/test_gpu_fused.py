@@ -310,6 +310,9 @@ PREFILL_CASES = [
     (100, 1000, 16, 8, 1024, 1.0), (1, 37, 32, 8, 64, 1.0), (130, 130, 8, 8, 136, 1.0),
     (64, 200, 64, 8, 256, 1.0), (300, 300, 12, 4, 320, 1.0), (257, 513, 5, 1, 520, 1.0),
     (640, 1280, 32, 8, 1280, 6.0), (300, 1500, 16, 8, 1536, 10.0), (129, 129, 16, 8, 4096, 1.0),
+    # chunk offsets n - c between 32 and 64: a wave's queries straddle key 64, so some lanes
+    # find every key of their set's first block masked while others do not
+    (100, 140, 8, 8, 144, 1.0), (60, 105, 16, 8, 128, 3.0), (24, 72, 4, 2, 512, 1.0),
 ]
 
 

@@ -137,6 +137,38 @@ def test_chunked_prefill_matches_one_shot_and_fp32():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("chunk", [16, 61, 24])
+def test_graph_chunked_prefill_matches_eager(chunk):
+    """Chunks replayed from one captured graph (the last one padded to the
+    chunk: 61 tokens in chunks of 16 and 24) give the eager chunks' logits
+    and cache (the attention's rounding apart), and leave the slots past the
+    prompt's end to decode."""
+    m = V.Qwen3VL(TINY, max_len=128, seed=14)
+    x, _ = m.embed_prompt(SEGS, seed=6)
+    pos3 = V.rope_index(SEGS)
+    L = x.shape[0]
+    eager = m.prefill_chunked(x, pos3, chunk=chunk, graph=False)
+    ke, ve = m.k_cache[:, :, :L].clone(), m.v_cache[:, :, :L].clone()
+    m.k_cache.zero_()
+    m.v_cache.zero_()
+    g1 = m.prefill_chunked(x, pos3, chunk=chunk, graph=True)
+    g2 = m.prefill_chunked(x, pos3, chunk=chunk, graph=True)  # a second replay of the graph
+    assert torch.isfinite(g1.float()).all()
+    assert torch.equal(g1, g2)
+    _close(g1, eager, 5e-2, "graph vs eager chunks")
+    # layer 0 sees the same rows in both: its cache is bit-identical
+    assert torch.equal(m.k_cache[0, :, :L], ke[0]) and torch.equal(m.v_cache[0, :, :L], ve[0])
+    _close(m.k_cache[:, :, :L], ke, 5e-2, "k cache graph vs eager")
+    # decode from the graph-prefilled cache continues like the eager one
+    tok = torch.argmax(g1[-1].float()).reshape(1)
+    dg = m.decode_step(tok, torch.tensor([L], device="cuda"))
+    m2 = V.Qwen3VL(TINY, max_len=128, seed=14)
+    m2.prefill_chunked(x, pos3, chunk=chunk, graph=False)
+    de = m2.decode_step(tok, torch.tensor([L], device="cuda"))
+    _close(dg[0], de[0], 5e-2, "decode after graph vs eager prefill")
+
+
+@pytest.mark.gpu
 def test_decode_continues_mrope_positions():
     m = V.Qwen3VL(TINY, max_len=128, seed=12)
     x, _ = m.embed_prompt(SEGS, seed=4)
