@@ -668,7 +668,10 @@ __global__ __launch_bounds__(256) void splitk_dequant_kernel(const GemmArgs p,
 // 256: 25.6 -> 17.9 us (8 slices), 32.3 -> 23.8 us (8), 32.6 -> 28.8 us (4);
 // N=4096 K=12288 M=64: 37.1 -> 23.7 us (8).  Grids of more tiles gained
 // little or lost (N=10240 K=2560 M=32, 80 tiles: 12.4 us whole, 16.2 us in
-// two slices).  The caller also checks the alignment of the operands.  The
+// two slices).  Nor where 64 x 64 tiles alone fill three quarters of the CUs
+// (M=512 N=2048 K=2048: 18.1 us in two slices against 10.3-10.6 us unsplit on
+// 256 tiles of 64 x 64; K=6144: 26.7-27.8 us in four against 21.5 us; whole
+// linears, weights from HBM).  The caller also checks the alignment of the operands.  The
 // tile's per-lane weight and activation offsets are 32-bit (up to 128 rows x
 // K bytes, and the slices address the full row pitch K), so K * 256 must stay
 // below 2^32 as for launch_gemm's DMA tiles.
@@ -679,6 +682,7 @@ int splitk_ways(int M, int N, int K) {
   const int tiles = ((M + bm - 1) / bm) * ((N + 127) / 128);
   const int cus = num_cus();
   if (4 * tiles > cus) return 1;
+  if ((int64_t)4 * ((M + 63) / 64) * ((N + 63) / 64) > (int64_t)3 * cus) return 1;
   int S = 1;
   while (S < 16 && tiles * 2 * S <= cus && K % (128 * 2 * S) == 0 && K / (2 * S) >= 1024) S *= 2;
   return S;

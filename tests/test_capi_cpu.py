@@ -86,6 +86,12 @@ def test_splitk_workspace_respects_32bit_tile_offsets(lib):
     # M=128 N=2560 K=10240: 20 tiles of 128 x 128, 8 slices of the int32 sums
     assert ws(_lib.CIDER_OP_PERCHANNEL, 128, 2560, 10240) == \
         quant(128, 10240) + 8 * 128 * 2560 * 4
+    # M=256 N=2560 K=10240: 160 tiles of 64 x 64 leave CUs idle, 4 slices
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 256, 2560, 10240) == \
+        quant(256, 10240) + 4 * 256 * 2560 * 4
+    # M=512 N=2048 K=2048: 64 tiles of 128 x 128, but 256 tiles of 64 x 64
+    # fill the CUs, so one pass
+    assert ws(_lib.CIDER_OP_PERCHANNEL, 512, 2048, 2048) == quant(512, 2048)
     # one tile, K = 2**26: 2**26 * 256 = 2**34 bytes of offsets, no split
     assert ws(_lib.CIDER_OP_PERCHANNEL, 32, 128, 1 << 26) == quant(32, 1 << 26)
     # just below the limit the split still applies

@@ -778,11 +778,12 @@ def test_pergroup_splitk_special_scales(M, N, gs):
 # (128, 2560, 10240) and (64, 2560, 10240) eight, (17, 4096, 12288) eight,
 # (130, 2560, 4096) four with a ragged row tile, (256, 2560, 10240) four,
 # (200, 1000, 4096) four with N past the last 128-column tile; (512, 2560,
-# 2560) has 80 tiles and runs one pass.  The extremes (-127 everywhere) are
-# summed over the longest slices.
+# 2560) has 80 tiles and runs one pass, and so does (512, 2048, 2048), whose
+# 64 x 64 tiles fill the CUs.  The extremes (-127 everywhere) are summed over
+# the longest slices.
 @pytest.mark.parametrize("M,N,K", [(128, 2560, 10240), (64, 2560, 10240), (17, 4096, 12288),
                                    (130, 2560, 4096), (256, 2560, 10240), (200, 1000, 4096),
-                                   (512, 2560, 2560)])
+                                   (512, 2560, 2560), (512, 2048, 2048)])
 def test_splitk_perchannel_exact(M, N, K):
     x, w, sw, b = synth_pc(M, N, K, 150 + M)
     x[0, :] = 0                                  # s = 1, q = 0
