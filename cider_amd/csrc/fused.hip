@@ -33,7 +33,9 @@
 // stream from L2 a second and third time.  Reductions are wave-local
 // (shuffles, no LDS, no barrier).  With at most 64 rows (decode) a row gets a
 // whole 256-thread workgroup instead (four waves, LDS for the cross-wave sum
-// and max), and SwiGLU without quantization is elementwise over the grid.
+// and max); SwiGLU + quantize takes a workgroup per row at every M (rows of up
+// to 16384 elements), and SwiGLU without quantization is elementwise over the
+// grid.
 #include "common.hpp"
 #include "kernels.hpp"
 #include "norm_common.hpp"
@@ -148,7 +150,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
 // ---------------------------------------------------------------------------
 // SwiGLU (+ per-token quantize)
 // ---------------------------------------------------------------------------
-template <int NV, bool WY, bool WQ>
+// Rows above 16384 elements (the shorter ones take silu_mul_row_kernel): one
+// wave per row, 4 rows per workgroup, the row streamed from L2 a second time
+// for the quantized store.
+template <bool WY, bool WQ>
 __global__ __launch_bounds__(256) void silu_mul_kernel(
     const uint16_t* __restrict__ gu, uint16_t* __restrict__ y, int8_t* __restrict__ q,
     float* __restrict__ sa, int M, int I) {
@@ -159,61 +164,19 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(
   const uint16_t* g = gu + row * 2 * I;
   const uint16_t* u = g + I;
   float amax = 0.0f;
-  if constexpr (NV > 0) {
-    // up to 24 vectors per lane every load first, unconditional (clamped: a
-    // lane past the row re-reads its last vector), as a load under a lane
-    // mask makes the compiler wait for each before the next (2048 x 12288:
-    // 47.4 -> 45.7 us per call; the hardware exp2 and reciprocal of swiglu1
-    // then 31.2 us).  At 32 the two register copies would leave one wave per
-    // SIMD.
-    constexpr bool HOIST = NV <= 24;
-    i32x4 v[NV], uv[HOIST ? NV : 1];
-    if constexpr (HOIST) {
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int e = min(lane + i * kWave, nvec - 1);
-        v[i] = ld16(g + 8 * e);
-        uv[i] = ld16(u + 8 * e);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int e = lane + i * kWave;
-      if (e < nvec) {
-        if constexpr (HOIST)
-          v[i] = swiglu8(v[i], uv[i]);
-        else
-          v[i] = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
-        if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v[i];
-        amax = absmax8(v[i], amax);
-      }
-    }
-    if constexpr (WQ) {
-      amax = wave_max(amax);
-      const float s = row_scale(amax);
-      const float inv = 1.0f / s;
-      if (lane == 0) sa[row] = s;
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int e = lane + i * kWave;
-        if (e < nvec) *reinterpret_cast<i32x2*>(q + row * I + 8 * e) = quant8(v[i], inv);
-      }
-    }
-  } else {
-    for (int e = lane; e < nvec; e += kWave) {
-      const i32x4 v = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
-      if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v;
-      amax = absmax8(v, amax);
-    }
-    if constexpr (WQ) {
-      amax = wave_max(amax);
-      const float s = row_scale(amax);
-      const float inv = 1.0f / s;
-      if (lane == 0) sa[row] = s;
-      for (int e = lane; e < nvec; e += kWave)
-        *reinterpret_cast<i32x2*>(q + row * I + 8 * e) =
-            quant8(swiglu8(ld16(g + 8 * e), ld16(u + 8 * e)), inv);
-    }
+  for (int e = lane; e < nvec; e += kWave) {
+    const i32x4 v = swiglu8(ld16(g + 8 * e), ld16(u + 8 * e));
+    if constexpr (WY) *reinterpret_cast<i32x4*>(y + row * I + 8 * e) = v;
+    amax = absmax8(v, amax);
+  }
+  if constexpr (WQ) {
+    amax = wave_max(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) sa[row] = s;
+    for (int e = lane; e < nvec; e += kWave)
+      *reinterpret_cast<i32x2*>(q + row * I + 8 * e) =
+          quant8(swiglu8(ld16(g + 8 * e), ld16(u + 8 * e)), inv);
   }
 }
 
@@ -468,22 +431,19 @@ struct RmsRun {
   }
 };
 
-template <int NV>
-struct SwiRun {
-  static hipError_t run(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
+hipError_t run_swi_wave(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa, int M, int I,
                         hipStream_t s) {
-    const dim3 grid((M + 3) / 4), block(256);
-    if (y && q)
-      silu_mul_kernel<NV, true, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
-    else if (y)
-      silu_mul_kernel<NV, true, false><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
-    else if (q)
-      silu_mul_kernel<NV, false, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
-    else
-      return hipErrorInvalidValue;
-    return hipGetLastError();
-  }
-};
+  const dim3 grid((M + 3) / 4), block(256);
+  if (y && q)
+    silu_mul_kernel<true, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+  else if (y)
+    silu_mul_kernel<true, false><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+  else if (q)
+    silu_mul_kernel<false, true><<<grid, block, 0, s>>>(gu, y, q, sa, M, I);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 }  // namespace
 
@@ -547,13 +507,15 @@ hipError_t launch_silu_mul(const uint16_t* gu, uint16_t* y, int8_t* q, float* sa
     silu_mul_ew_kernel<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(gu, y, M, I);
     return hipGetLastError();
   }
-  if (M <= kFewRows) {
-    if (nvec <= 256) return run_swi_row<1>(gu, y, q, sa, M, I, s);
-    if (nvec <= 512) return run_swi_row<2>(gu, y, q, sa, M, I, s);
-    if (nvec <= 1024) return run_swi_row<4>(gu, y, q, sa, M, I, s);
-    if (nvec <= 2048) return run_swi_row<8>(gu, y, q, sa, M, I, s);
-  }
-  return by_nv<SwiRun>(nvec, gu, y, q, sa, M, I, s);
+  // A workgroup per row at every M, not only for few rows: its four waves load
+  // a row at once, and at prefill sizes that beats a wave per row too (M=512
+  // I=6144: 7.65 -> 4.88 us; M=1024: 8.21 -> 7.43 us; M=2048 I=12288: 28.6 ->
+  // 23.0 us).  The same bits: the row's only reduction is a max.
+  if (nvec <= 256) return run_swi_row<1>(gu, y, q, sa, M, I, s);
+  if (nvec <= 512) return run_swi_row<2>(gu, y, q, sa, M, I, s);
+  if (nvec <= 1024) return run_swi_row<4>(gu, y, q, sa, M, I, s);
+  if (nvec <= 2048) return run_swi_row<8>(gu, y, q, sa, M, I, s);
+  return run_swi_wave(gu, y, q, sa, M, I, s);
 }
 
 hipError_t launch_qk_norm_rope(const uint16_t* qkv, const uint16_t* qw, const uint16_t* kw,

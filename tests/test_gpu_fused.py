@@ -122,7 +122,10 @@ def test_rmsnorm_in_place_residual_and_special_rows():
     assert torch.all(r.q[2] == 127)
 
 
-SWI_SHAPES = [(1, 12288), (3, 6144), (129, 4096), (2, 24576), (16, 8)]
+# a workgroup per row up to I = 16384 at every M (ragged last vector group at
+# I = 6152), a wave per row streaming above (I = 24576, 16392)
+SWI_SHAPES = [(1, 12288), (3, 6144), (129, 4096), (2, 24576), (16, 8), (300, 12288),
+              (517, 6152), (70, 16392)]
 
 
 @pytest.mark.parametrize("M,I", SWI_SHAPES)
