@@ -67,6 +67,9 @@ SIGNATURES = {
     "cider_attn_prefill_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "cider_attn_prefill": (_I, [_P, _P, _P, _F, _P, _SZ, _P, _I64, _I64, _P, _I64, _I64, _I64,
                                 _I64, _P]),
+    "cider_attn_prefill_quantize_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "cider_attn_prefill_quantize": (_I, [_P, _P, _P, _F, _P, _SZ, _P, _P, _I64, _I64, _P, _I64,
+                                         _I64, _I64, _I64, _P]),
     "cider_rmsnorm_mv": (_I, [_P, _P, _P, _P, _F, _P, _P, _P, _P, _I64, _I64, _P]),
     "cider_swiglu_mv": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P]),
 }

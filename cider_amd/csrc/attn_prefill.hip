@@ -51,6 +51,7 @@
 #include "common.hpp"
 #include "dma_common.hpp"
 #include "kernels.hpp"
+#include "quant_common.hpp"
 
 namespace cider {
 
@@ -370,14 +371,12 @@ __global__ __launch_bounds__(kThreads, 1) void attn_prefill_kernel(
   }
 }
 
-// out[i, h, :] = sum_p o_p 2^((m_p - M) sc) / sum_p l_p 2^((m_p - M) sc), M = max_p m_p:
-// 16 threads per (query, head), 8 dimensions each, parts in order.
-__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ ws,
-                                                                 uint16_t* __restrict__ out,
-                                                                 int64_t rows, int P, float sc) {
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int d0 = 8 * (threadIdx.x & 15);
-  if (row >= rows) return;
+// Output dims d0 .. d0 + 7 of partial row `row` ((token, head) pair) merged
+// over the P key parts in ws (P x rows x 128 fp32 numerators, then P x rows
+// x (m, l)): each part weighted by exp2((m_p - max_p m) * sc), the sum
+// divided by the weighted l, rounded to fp16 (8 halves, packed).
+__device__ __forceinline__ i32x4 merge8(const float* __restrict__ ws, int64_t rows, int64_t row,
+                                        int d0, int P, float sc) {
   const float* ml = ws + (int64_t)P * rows * kD;
   float M = -INFINITY;
   for (int p = 0; p < P; ++p) M = fmaxf(M, ml[((int64_t)p * rows + row) * 2]);
@@ -399,7 +398,53 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
   i32x4 v;
 #pragma unroll
   for (int t = 0; t < 4; ++t) v[t] = (int32_t)f2h2(acc[2 * t] * inv, acc[2 * t + 1] * inv);
-  *reinterpret_cast<i32x4*>(out + row * kD + d0) = v;
+  return v;
+}
+
+// out[i, h, :] = sum_p o_p 2^((m_p - M) sc) / sum_p l_p 2^((m_p - M) sc), M = max_p m_p:
+// 16 threads per (query, head), 8 dimensions each, parts in order.
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ ws,
+                                                                 uint16_t* __restrict__ out,
+                                                                 int64_t rows, int P, float sc) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int d0 = 8 * (threadIdx.x & 15);
+  if (row >= rows) return;
+  *reinterpret_cast<i32x4*>(out + row * kD + d0) = merge8(ws, rows, row, d0, P, sc);
+}
+
+// The merge with the per-token quantization of the o projection's input
+// fused in (cider/kernels/w8a8_quantize.metal:33-86, the helpers of
+// quantize_per_token): one workgroup per token, its H heads x 128 dims as
+// H * 16 vectors of 8, NVB per thread.  The fp16 values are those the merge
+// kernel stores, so q and sa are bit-identical to that kernel followed by
+// quantize_per_token, without the fp16 round trip through HBM.
+template <int NVB>
+__global__ __launch_bounds__(256) void attn_prefill_merge_quant_kernel(
+    const float* __restrict__ ws, int8_t* __restrict__ qo, float* __restrict__ sa, int H,
+    int64_t rows, int P, float sc) {
+  __shared__ float red[4];
+  const int64_t tok = blockIdx.x;
+  const int nvec = H * (kD / 8);
+  i32x4 v[NVB];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    if (e < nvec) {
+      v[i] = merge8(ws, rows, tok * H + (e >> 4), 8 * (e & 15), P, sc);
+      amax = absmax8(v[i], amax);
+    }
+  }
+  amax = block_max4(amax, red);
+  const float s = row_scale(amax);
+  const float inv = 1.0f / s;
+  if (threadIdx.x == 0) sa[tok] = s;
+  int8_t* qr = qo + tok * H * kD;
+#pragma unroll
+  for (int i = 0; i < NVB; ++i) {
+    const int e = threadIdx.x + 256 * i;
+    if (e < nvec) *reinterpret_cast<i32x2*>(qr + 8 * e) = quant8(v[i], inv);
+  }
 }
 
 }  // namespace
@@ -434,6 +479,43 @@ hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint
     const int64_t rows = (int64_t)c * H;
     attn_prefill_merge_kernel<<<(unsigned)((rows + 15) / 16), 256, 0, s>>>(ws, out, rows, P, sc);
   }
+  return hipGetLastError();
+}
+
+size_t attn_prefill_quant_ws_bytes(int c, int n, int H) {
+  const size_t f = attn_prefill_ws_floats(c, n, H) * sizeof(float);
+  const size_t h = (size_t)c * H * kD * sizeof(uint16_t);
+  return f > h ? f : h;
+}
+
+hipError_t launch_attn_prefill_quant(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                     int8_t* qo, float* sa, float scale, void* ws,
+                                     size_t ws_bytes, int c, int n, const int64_t* n_dev, int H,
+                                     int KV, int64_t T, hipStream_t s) {
+  const int P = attn_prefill_parts(c, n, H);
+  const size_t part_bytes = (size_t)P * c * H * (kD + 2) * sizeof(float);
+  if (P == 1 || ws_bytes < part_bytes) {
+    // one part: the fp16 output in the workspace, then the row quantization
+    uint16_t* out = reinterpret_cast<uint16_t*>(ws);
+    hipError_t e = launch_attn_prefill(q, kc, vc, out, scale, nullptr, 0, c, n, n_dev, H, KV, T, s);
+    if (e != hipSuccess) return e;
+    return launch_quantize(out, qo, sa, c, H * kD, s);
+  }
+  const float sc = scale * 1.4426950408889634f;
+  const int items = ((c + kBQ - 1) / kBQ) * H;
+  float* wf = reinterpret_cast<float*>(ws);
+  attn_prefill_kernel<<<items * P, kThreads, 0, s>>>(q, kc, vc, nullptr, wf, c, n, n_dev, H, KV,
+                                                      (int)T, P, sc);
+  const int64_t rows = (int64_t)c * H;
+  const int nvec = H * (kD / 8);
+  if (nvec <= 256)
+    attn_prefill_merge_quant_kernel<1><<<c, 256, 0, s>>>(wf, qo, sa, H, rows, P, sc);
+  else if (nvec <= 512)
+    attn_prefill_merge_quant_kernel<2><<<c, 256, 0, s>>>(wf, qo, sa, H, rows, P, sc);
+  else if (nvec <= 1024)
+    attn_prefill_merge_quant_kernel<4><<<c, 256, 0, s>>>(wf, qo, sa, H, rows, P, sc);
+  else
+    attn_prefill_merge_quant_kernel<8><<<c, 256, 0, s>>>(wf, qo, sa, H, rows, P, sc);
   return hipGetLastError();
 }
 

@@ -689,4 +689,45 @@ int cider_attn_prefill(const void* q_f16, const void* k_cache_f16, const void* v
       fn);
 }
 
+size_t cider_attn_prefill_quantize_workspace_bytes(int64_t c, int64_t n, int64_t H) {
+  if (H <= 0 || H > 128 || c < 1 || n < c || n > ((int64_t)1 << 24) || c * H > kMaxDim) return 0;
+  return align256(cider::attn_prefill_quant_ws_bytes((int)c, (int)n, (int)H));
+}
+
+int cider_attn_prefill_quantize(const void* q_f16, const void* k_cache_f16,
+                                const void* v_cache_f16, float scale, void* ws, size_t ws_bytes,
+                                int8_t* q_out, float* sa_out, int64_t c, int64_t n,
+                                const int64_t* n_dev, int64_t H, int64_t KV, int64_t D, int64_t T,
+                                void* stream) {
+  static const char* fn = "cider_attn_prefill_quantize";
+  if (D != 128) return fail(CIDER_E_INVALID, "%s: head_dim must be 128 (got %lld)", fn, (long long)D);
+  if (H <= 0 || KV <= 0 || H > 128 || H % KV != 0)
+    return fail(CIDER_E_INVALID, "%s: H=%lld must be a positive multiple of KV=%lld (H <= 128)",
+                fn, (long long)H, (long long)KV);
+  if (T <= 0 || T > ((int64_t)1 << 24) || n < 1 || n > T || c < 1 || c > n || c * H > kMaxDim)
+    return fail(CIDER_E_INVALID, "%s: need 1 <= c <= n <= T <= 2^24 (c=%lld n=%lld T=%lld)", fn,
+                (long long)c, (long long)n, (long long)T);
+  CIDER_TRY(need(fn, q_f16, "q", true));
+  CIDER_TRY(need(fn, k_cache_f16, "k_cache", true));
+  CIDER_TRY(need(fn, v_cache_f16, "v_cache", true));
+  CIDER_TRY(need(fn, q_out, "q_out", true));
+  CIDER_TRY(need(fn, sa_out, "sa_out", true));
+  CIDER_TRY(need(fn, ws, "ws", true));
+  if (!aligned16(q_f16) || !aligned16(k_cache_f16) || !aligned16(v_cache_f16) || !aligned16(q_out))
+    return fail(CIDER_E_INVALID, "%s: q, the caches and q_out must be 16-byte aligned", fn);
+  if (((uintptr_t)ws & 255) != 0)
+    return fail(CIDER_E_INVALID, "%s: ws must be 256-byte aligned", fn);
+  const size_t need_bytes = (size_t)c * H * D * 2;
+  if (ws_bytes < need_bytes)
+    return fail(CIDER_E_INVALID, "%s: ws holds %zu bytes, needs at least %zu (c * H * 256)", fn,
+                ws_bytes, need_bytes);
+  return hip_status(
+      cider::launch_attn_prefill_quant(reinterpret_cast<const uint16_t*>(q_f16),
+                                       reinterpret_cast<const uint16_t*>(k_cache_f16),
+                                       reinterpret_cast<const uint16_t*>(v_cache_f16), q_out,
+                                       sa_out, scale, ws, ws_bytes, (int)c, (int)n, n_dev, (int)H,
+                                       (int)KV, T, (hipStream_t)stream),
+      fn);
+}
+
 }  // extern "C"

@@ -184,15 +184,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(
 // Few rows (decode): one 256-thread workgroup per row, so a row's loads come
 // from four waves at once; the sums and maxima go through LDS in wave order.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float block_max4(float v, float* red) {
-  const int wave = threadIdx.x >> 6;
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
 template <int NVB, bool ADD, bool WY, bool WQ>
 __global__ __launch_bounds__(256) void rmsnorm_row_kernel(
     const uint16_t* x, const uint16_t* __restrict__ add, uint16_t* hsum,

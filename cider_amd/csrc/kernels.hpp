@@ -128,6 +128,16 @@ hipError_t launch_attn_prefill(const uint16_t* q, const uint16_t* kc, const uint
                                uint16_t* out, float scale, float* ws, size_t ws_floats, int c,
                                int n, const int64_t* n_dev, int H, int KV, int64_t T,
                                hipStream_t s);
+// The same attention with its output quantized per token (q int8 [c, H*128],
+// sa fp32 [c]): split launches quantize in the merge, one-part launches write
+// the fp16 output into ws and quantize it from there.  ws: at least
+// attn_prefill_quant_ws_bytes(c, n, H) bytes, 256-byte aligned (c*H*256 bytes
+// run one part).
+size_t attn_prefill_quant_ws_bytes(int c, int n, int H);
+hipError_t launch_attn_prefill_quant(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                                     int8_t* qo, float* sa, float scale, void* ws,
+                                     size_t ws_bytes, int c, int n, const int64_t* n_dev, int H,
+                                     int KV, int64_t T, hipStream_t s);
 
 hipError_t launch_w4_repack_ref(const uint8_t* src_kn, uint8_t* dst_nk, int N,
                                 int K, hipStream_t s);

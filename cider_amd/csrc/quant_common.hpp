@@ -16,6 +16,17 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// amax over a 256-thread workgroup (4 waves); red: 4 floats of LDS.  Every
+// thread gets the result.
+__device__ __forceinline__ float block_max4(float v, float* red) {
+  const int wave = threadIdx.x >> 6;
+  v = wave_max(v);
+  __syncthreads();  // red may still be read from the previous reduction
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
 __device__ __forceinline__ float row_scale(float amax) {
   float s = amax / 127.0f;
   return s == 0.0f ? 1.0f : s;

@@ -1,7 +1,9 @@
 """Producers of the W8A8 linear's input, with the per-token quantization fused
 in, prefill-chunk and single-query decode attention (HIP kernels behind the C ABI of
 ``include/cider_hip.h``: ``cider_rmsnorm_quantize``, ``cider_silu_mul_quantize``,
-``cider_qk_norm_rope``, ``cider_attn_decode``, ``cider_attn_prefill``).
+``cider_qk_norm_rope``, ``cider_attn_decode``, ``cider_attn_prefill``,
+``cider_attn_prefill_quantize``, the last one the attention as the producer of
+the o projection's input).
 
 The reference library quantizes a linear's fp16 input inside the linear
 (``cider/kernels/w8a8_quantize.metal:17-87``); its models produce that input
@@ -216,6 +218,51 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
                                           wsp, wsb, _ptr(out), c, int(n), _ptr(n_dev), H, KV, D,
                                           T, _stream_ptr(dev, stream)))
     return out
+
+
+def attn_prefill_quantize_workspace(c: int, n: int, num_heads: int, device) -> torch.Tensor:
+    """The workspace of ``attn_prefill_quantize`` for a chunk of c queries over
+    n slots: the key parts' partials when the launch splits, else the fp16
+    output before its quantization."""
+    nbytes = _lib.load().cider_attn_prefill_quantize_workspace_bytes(c, n, num_heads)
+    if nbytes == 0:
+        raise ValueError(f"attn_prefill_quantize: unsupported shape c={c} n={n} H={num_heads}")
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def attn_prefill_quantize(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, n: int,
+                          scale: float, ws: Optional[torch.Tensor] = None,
+                          n_dev: Optional[torch.Tensor] = None, stream=None):
+    """``attn_prefill`` with its output quantized per token for the o
+    projection: returns (q int8 [c, H * 128], scale_a fp32 [c]), bit-identical
+    to ``ops.quantize_per_token`` of ``attn_prefill``'s output, for
+    ``CiderLinear.forward_quantized``.  A launch that splits its keys
+    quantizes where it merges the parts, with no fp16 output in HBM.  ``ws``:
+    ``attn_prefill_quantize_workspace(c, n, H)`` (allocated here if None)."""
+    fn = "attn_prefill_quantize"
+    dev = _require_gpu(fn, q, k_cache, v_cache, ws, n_dev)
+    if n_dev is not None and (n_dev.dtype != torch.int64 or n_dev.numel() < 1):
+        raise ValueError(f"{fn}: n_dev must be an int64 tensor")
+    _f16(fn, "q", q)
+    _f16(fn, "k_cache", k_cache)
+    _f16(fn, "v_cache", v_cache)
+    if q.dim() != 3:
+        raise ValueError(f"{fn}: q must be [c, H, D]")
+    c, H, D = q.shape
+    KV, T, d = k_cache.shape
+    if tuple(v_cache.shape) != (KV, T, d) or d != D:
+        raise ValueError(f"{fn}: the caches must be [KV, T, {D}]")
+    lib = _lib.load()
+    with _on_stream(dev, stream):
+        if ws is None:
+            ws = attn_prefill_quantize_workspace(c, int(n), H, dev)
+        qo = torch.empty(c, H * D, dtype=torch.int8, device=dev)
+        sa = torch.empty(c, dtype=torch.float32, device=dev)
+        _lib.check(lib.cider_attn_prefill_quantize(_ptr(q), _ptr(k_cache), _ptr(v_cache),
+                                                   float(scale), _ptr(ws), ws.numel(), _ptr(qo),
+                                                   _ptr(sa), c, int(n), _ptr(n_dev), H, KV, D, T,
+                                                   _stream_ptr(dev, stream)))
+    return qo, sa
 
 
 def _mv_linear(fn: str, linear, K: int):

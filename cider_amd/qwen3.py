@@ -194,8 +194,10 @@ class Qwen3Layer(torch.nn.Module):
     def prefill_fused(self, x, pending, tables, rope_row, slot, k_cache, v_cache, n,
                       attn_ws=None, n_dev=None):
         """x [L, hidden] (+ pending) at cache slots n - L .. n - 1 (`slot`);
-        attends causally over cache slots 0..n-1 (``attn_ws``: the attention's
-        split workspace for this (L, n), shared by the layers; ``n_dev``: n
+        attends causally over cache slots 0..n-1, the attention's output
+        quantized for o_proj in the attention (``attn_ws``: its workspace for
+        this (L, n), ``fused.attn_prefill_quantize_workspace``, shared by the
+        layers; ``n_dev``: n
         read on the device, the host n its upper bound).  Returns
         (x, pending)."""
         c = self.cfg
@@ -203,9 +205,9 @@ class Qwen3Layer(torch.nn.Module):
         qkv = self.qkv.forward_quantized(a.q, a.scale_a)
         q = FK.qk_norm_rope(qkv, self.q_norm, self.k_norm, c.rms_eps, tables[0], tables[1],
                             rope_row, slot, k_cache, v_cache, c.num_heads, c.num_kv_heads)
-        attn = FK.attn_prefill(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim), ws=attn_ws,
-                               n_dev=n_dev)
-        b = self._norm(a.h, self.o(attn), self.post_norm, False, True)
+        qa, sa = FK.attn_prefill_quantize(q, k_cache, v_cache, n, 1.0 / math.sqrt(c.head_dim),
+                                          ws=attn_ws, n_dev=n_dev)
+        b = self._norm(a.h, self.o.forward_quantized(qa, sa), self.post_norm, False, True)
         gu = self.gate_up.forward_quantized(b.q, b.scale_a)
         _, qd, sd = FK.silu_mul_quantize(gu, want_y=False, want_q=True)
         return b.h, self.down.forward_quantized(qd, sd)
@@ -326,7 +328,7 @@ class Qwen3(torch.nn.Module):
         if self.fused:
             pos = torch.arange(L, device=self.device)
             pending = None
-            ws = FK.attn_prefill_workspace(L, L, self.cfg.num_heads, self.device)
+            ws = FK.attn_prefill_quantize_workspace(L, L, self.cfg.num_heads, self.device)
             for i, layer in enumerate(self.layers):
                 x, pending = layer.prefill_fused(x, pending, (self.cos, self.sin), pos, pos,
                                                  self.k_cache[i], self.v_cache[i], L, ws)

@@ -168,7 +168,7 @@ class Qwen3VL(Qwen3):
                "slots": torch.full((chunk,), -1, dtype=torch.int64, device=dev),
                "n": torch.tensor([chunk], dtype=torch.int64, device=dev)}
         cap = self.capacity
-        ws = FK.attn_prefill_workspace(chunk, cap, self.cfg.num_heads, dev)
+        ws = FK.attn_prefill_quantize_workspace(chunk, cap, self.cfg.num_heads, dev)
 
         def run():
             return self._chunk_layers(buf["x"], buf["rows"], (buf["cos"], buf["sin"]),
@@ -216,7 +216,7 @@ class Qwen3VL(Qwen3):
             xc = x[s:e].clone()
             rows = torch.arange(c, device=self.device)
             pc = None
-            ws = FK.attn_prefill_workspace(e - s, e, self.cfg.num_heads, self.device)
+            ws = FK.attn_prefill_quantize_workspace(e - s, e, self.cfg.num_heads, self.device)
             for i, layer in enumerate(self.layers):
                 # query i (slot s + i) sees slots 0 .. s + i
                 xc, pc = layer.prefill_fused(xc, pc, (cos[s:e], sin[s:e]), rows,

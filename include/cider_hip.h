@@ -292,6 +292,32 @@ int cider_attn_prefill(const void* q_f16, const void* k_cache_f16,
                        const int64_t* n_dev, int64_t H, int64_t KV, int64_t D,
                        int64_t T, void* stream);
 
+/* Bytes of workspace cider_attn_prefill_quantize uses: the split partials of
+ * cider_attn_prefill_workspace_bytes when the launch splits, else c * H * 256
+ * (the fp16 output before its quantization); 0 for shapes it rejects. */
+size_t cider_attn_prefill_quantize_workspace_bytes(int64_t c, int64_t n, int64_t H);
+
+/* cider_attn_prefill with its output quantized per token for the o
+ * projection: q_out int8 [c, H * D] and sa_out fp32 [c] are, bit for bit,
+ * cider_quantize_per_token of the fp16 output cider_attn_prefill computes
+ * with the same ws (the reference quantizes the o projection's input inside
+ * its W8A8 linear, csrc/src/w8a8_primitive.mm:180-203, with
+ * cider/kernels/w8a8_quantize.metal:33-86).  A launch that splits its keys
+ * quantizes in the kernel that merges the parts, so the fp16 output never
+ * goes through HBM; one that does not writes it into ws and quantizes it from
+ * there.  ws (256-byte aligned, not overlapping the other buffers) of
+ * cider_attn_prefill_quantize_workspace_bytes; at least c * H * 256 bytes
+ * (which run one part).  H <= 128; otherwise as cider_attn_prefill (q_out
+ * 16-byte aligned).  The reference has no fused attention; this entry serves
+ * the same prefill call (cider/fused_hybrid.py:179-196) and the o projection
+ * after it. */
+int cider_attn_prefill_quantize(const void* q_f16, const void* k_cache_f16,
+                                const void* v_cache_f16, float scale, void* ws,
+                                size_t ws_bytes, int8_t* q_out, float* sa_out,
+                                int64_t c, int64_t n, const int64_t* n_dev,
+                                int64_t H, int64_t KV, int64_t D, int64_t T,
+                                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

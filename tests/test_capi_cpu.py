@@ -31,7 +31,7 @@ def lib():
 def test_header_declares_entry_points():
     syms = header_symbols()
     assert "cider_perchannel_linear" in syms and "cider_int8_matmul_int32" in syms
-    assert len(syms) == 22, syms
+    assert len(syms) == 24, syms
 
 
 @pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
@@ -236,6 +236,32 @@ def test_producer_and_attention_validation_without_gpu(lib):
     assert lib.cider_attn_prefill_workspace_bytes(0, 2048, 32) == 0
     # a 512-query chunk over 2048 slots with 16 heads (64 query blocks): 4 parts of fp32 partials
     assert lib.cider_attn_prefill_workspace_bytes(512, 2048, 16) == 4 * 512 * 16 * 130 * 4
+    # prefill attention quantized for o_proj: as above, plus H <= 128, the
+    # output pointers, and a workspace of at least c * H * 256 bytes (each call
+    # below breaks one argument, so none launches)
+    good = [p, p, p, 0.1, p, 1 << 30, p, p, 16, 32, n, 32, 8, 128, 64, n]
+
+    def apq(i, v):
+        a = list(good)
+        a[i] = v
+        return lib.cider_attn_prefill_quantize(*a)
+
+    assert apq(13, 64) == E and "head_dim" in _err(lib)
+    assert apq(11, 256) == E and "H <= 128" in _err(lib)
+    assert apq(11, 30) == E
+    assert apq(8, 33) == E and apq(8, 0) == E and apq(9, 65) == E
+    assert apq(0, n) == E and "q is NULL" in _err(lib)
+    assert apq(6, n) == E and "q_out is NULL" in _err(lib)
+    assert apq(7, n) == E and "sa_out is NULL" in _err(lib)
+    assert apq(4, n) == E and "ws is NULL" in _err(lib)
+    assert apq(6, ctypes.c_void_p(0x1008)) == E and "aligned" in _err(lib)
+    assert apq(4, ctypes.c_void_p(0x1010)) == E and "256-byte" in _err(lib)
+    assert apq(5, 16 * 32 * 256 - 1) == E and "needs at least" in _err(lib)
+    # its workspace: the fp16 output of an unsplit launch, the partials of a split one
+    wq = lib.cider_attn_prefill_quantize_workspace_bytes
+    assert wq(2048, 2048, 32) == 2048 * 32 * 256
+    assert wq(512, 2048, 16) == 4 * 512 * 16 * 130 * 4
+    assert wq(16, 16, 256) == 0 and wq(0, 16, 8) == 0
     # empty problems succeed
     assert lib.cider_rmsnorm_quantize(n, n, n, n, 1e-6, p, n, n, 0, 16, n) == _lib.CIDER_OK
     assert lib.cider_qk_norm_rope(*(args[:12] + [0] + args[13:])) == _lib.CIDER_OK

@@ -372,6 +372,42 @@ def test_attn_prefill_split_and_unsplit(c, n, H, KV, T):
         assert bool((err <= 3e-3 + 5e-3 * exp.abs()).all()), f"max err {err.max().item():.3e}"
 
 
+# The attention with its output quantized for o_proj: q and sa are, bit for
+# bit, the oracle's quantize_per_token of attn_prefill's fp16 output with the
+# same key split -- split launches (quantized in the merge), launches that fill
+# the GPU (the fp16 output staged in the workspace), 1..128 heads (one to
+# eight vectors per merge thread), a workspace of c * H * 256 bytes (one part),
+# the length read on the device, and stale workspace contents.
+QUANT_CASES = SPLIT_CASES + [(2048, 2048, 32, 8, 2048), (1, 37, 32, 8, 64), (100, 140, 8, 8, 144),
+                             (257, 2000, 5, 1, 2048), (64, 1200, 64, 8, 1280),
+                             (16, 1100, 128, 8, 1152), (16, 300, 128, 8, 320)]
+
+
+@pytest.mark.parametrize("c,n,H,KV,T", QUANT_CASES)
+def test_attn_prefill_quantize_bits(c, n, H, KV, T):
+    D = 128
+    print(f"attn_prefill_quantize c={c} n={n} H={H} KV={KV} T={T}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(c + 5 * n + H)
+    q = (torch.randn(c, H, D, device="cuda", generator=g) * 2).half()
+    kc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    vc = torch.randn(KV, T, D, device="cuda", generator=g).half()
+    kc[:, n:, :] = float("nan")
+    vc[:, n:, :] = float("nan")
+    scale = 1.0 / math.sqrt(D)
+    wsq = F.attn_prefill_quantize_workspace(c, n, H, "cuda")
+    wsq.fill_(0xFF)
+    qa, sa = F.attn_prefill_quantize(q, kc, vc, n, scale, ws=wsq)
+    out = F.attn_prefill(q, kc, vc, n, scale, ws=F.attn_prefill_workspace(c, n, H, "cuda"))
+    _quant_check(out, qa, sa, f"attn q c={c} n={n} H={H}")
+    n_dev = torch.tensor([n], dtype=torch.int64, device="cuda")
+    qd, sd = F.attn_prefill_quantize(q, kc, vc, n, scale, ws=wsq, n_dev=n_dev)
+    assert torch.equal(qd, qa) and torch.equal(sd, sa), "device length"
+    small = torch.full((c * H * 256,), 0xFF, dtype=torch.uint8, device="cuda")
+    q1, s1 = F.attn_prefill_quantize(q, kc, vc, n, scale, ws=small)
+    plain = F.attn_prefill(q, kc, vc, n, scale, split=False)
+    _quant_check(plain, q1, s1, f"attn q one part c={c} n={n} H={H}")
+
+
 def test_attn_prefill_chunks_match_one_shot():
     """Chunks of 512 after earlier slots (the Qwen3-VL prefill) give what one
     launch over the whole prompt gives, within the same bar."""
