@@ -42,7 +42,6 @@ __device__ __forceinline__ float load_scale1(const void* base, int64_t idx) {
 
 template <int TM, int WF, int EPI, bool SWH, int GS, bool VEC, int KW>
 __global__ __launch_bounds__(KW * 64) void skinny_kernel(const GemmArgs p) {
-  constexpr int kThreads = KW * 64;
   // k-steps per batch: two batches in flight per lane; 16-wave workgroups
   // have 128 VGPRs per lane, which holds two batches of 6 (int4) or 4 (int8)
   constexpr int U = (TM == 1) ? (KW == 16 ? (WF == W_I4 ? 6 : 4) : 8) : 4;
