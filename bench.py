@@ -814,7 +814,10 @@ def measure_qwen3(torch, args, dev, torch_producers=False):
 def bench_attn(torch, args, dev):
     """--attn: the causal prefill attention kernel per launch (HIP events on the
     launch stream), against the 2.5 PFLOP/s dense fp16 MFMA peak, with
-    PyTorch's fused SDPA at the same shapes (the path the models used before)."""
+    PyTorch's fused SDPA at the same shapes (the path the models used before);
+    and the form the models call, which ends in o_proj's per-token
+    quantization (cider_attn_prefill_quantize), beside the attention followed
+    by a quantize launch."""
     import math
 
     import torch.nn.functional as TF
@@ -822,6 +825,7 @@ def bench_attn(torch, args, dev):
 
     from cider_amd import _lib
     from cider_amd import fused as FK
+    from cider_amd import ops as OPS
     D, reps = 128, 20
     stream = torch.cuda.current_stream(dev)
     cases = []
@@ -836,11 +840,19 @@ def bench_attn(torch, args, dev):
         scale = 1.0 / math.sqrt(D)
         out = torch.empty(c, H * D, dtype=torch.float16, device=dev)
         ws = FK.attn_prefill_workspace(c, n, H, dev)
+        wsq = FK.attn_prefill_quantize_workspace(c, n, H, dev)
         qq, kk, vv = q.permute(1, 0, 2).unsqueeze(0), kc.unsqueeze(0), vc.unsqueeze(0)
         mask = None if c == n else causal_lower_right(c, n)
 
         def ours():
             FK.attn_prefill(q, kc, vc, n, scale, out=out, ws=ws)
+
+        def quantized():
+            FK.attn_prefill_quantize(q, kc, vc, n, scale, ws=wsq)
+
+        def then_quantize():
+            FK.attn_prefill(q, kc, vc, n, scale, out=out, ws=ws)
+            OPS.quantize_per_token(out)
 
         def sdpa():
             if mask is None:
@@ -848,7 +860,8 @@ def bench_attn(torch, args, dev):
             return TF.scaled_dot_product_attention(qq, kk, vv, attn_mask=mask, enable_gqa=True)
 
         times = {}
-        for key, fn in (("kernel", ours), ("sdpa", sdpa)):
+        for key, fn in (("kernel", ours), ("quantized", quantized), ("then_quantize", then_quantize),
+                        ("sdpa", sdpa)):
             for _ in range(3):
                 fn()
             torch.cuda.synchronize()
@@ -867,6 +880,8 @@ def bench_attn(torch, args, dev):
                       // max(1, c * H * 130 * 4) or 1,
                       "kernel_us": round(times["kernel"], 2), "tflops": round(tf, 1),
                       "frac_fp16_peak": round(tf / 2500.0, 4),
+                      "quantized_us": round(times["quantized"], 2),
+                      "attention_then_quantize_us": round(times["then_quantize"], 2),
                       "sdpa_us": round(times["sdpa"], 2),
                       "speedup_vs_sdpa": round(times["sdpa"] / times["kernel"], 2)})
     print(json.dumps({"metric": "causal prefill attention (cider_attn_prefill) per launch",
